@@ -1,0 +1,215 @@
+"""bench.py -- decode tok/s @ batch 1 and k4 GEMV HBM GB/s on one MI355X.
+
+Workload (BASELINE.json configs[0] shape, the metric's model): Qwen3-0.6B-shaped
+decoder (28 blocks, d 1024, FFN 3072, 16/8 heads, hd 128, vocab 151936), random
+N(0,0.02) weights from seed 0 packed to MCF k4, a 31-token prompt (seed 1),
+then greedy decode.  A "step" is one decode token.  Inputs are resident in HBM
+before the timed region; the timed steps run back to back from the captured
+HIP graph with the device-side argmax feeding the next step.
+
+Also measured (not the headline value): BASELINE configs[1] k4 GEMV shapes at
+batch 1 and 8, each launch on a different copy of the weights (>= 1 GiB
+rotation, so the 256 MB MALL cannot serve them), timed with HIP events on the
+launch stream; the lm_head GEMV (151936 x 1024) is the `roofline` kernel.
+The CPU baseline is the C restatement of Mantle's CPU path (oracle/) timed on
+this host on a bounded sample of the same decode.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+PROMPT_LEN = 31
+CPU_BASELINE_README_TOKS = 3.20  # Qwen3-0.6B k4, Mantle CPU, README.md:43-60
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30):
+    """k4 W4A8 GEMV on pre-quantised activations (the decode GEMV), per-launch HIP events."""
+    import numpy as np
+    import torch
+
+    from mantle_amd import _lib, mcf
+
+    stream = torch.cuda.current_stream()
+    out = []
+    for rows, cols in shapes:
+        w = mcf.fill_normal(rows * cols, 2 + rows).reshape(rows, cols)
+        payload = mcf.quantize_k4(w)
+        del w
+        psize = payload.nbytes
+        copies = max(2, -(-rotate_bytes // psize))
+        base = torch.from_numpy(payload).to("cuda:0")
+        bufs = [base] + [base.clone() for _ in range(copies - 1)]
+        bpr = (cols + 31) // 32
+        spr = (bpr + 7) // 8
+        sub_off = (rows * spr * 2 + 63) & ~63
+        data_off = (sub_off + rows * bpr + 63) & ~63
+        for batch in batches:
+            x = torch.randn(batch, cols, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(2))
+            qx = torch.empty(batch * bpr * 32, dtype=torch.int8, device="cuda:0")
+            xs = torch.empty(batch * bpr, dtype=torch.float32, device="cuda:0")
+            y = torch.empty(batch * rows, dtype=torch.float32, device="cuda:0")
+            for b in range(batch):
+                _lib.call("mantleHipQuantizeVecBlocksF32", x[b].data_ptr(), cols,
+                          qx.data_ptr() + b * bpr * 32, xs.data_ptr() + 4 * b * bpr, stream.cuda_stream)
+
+            def launch(i):
+                p = bufs[i % copies].data_ptr()
+                _lib.call("mantleHipQuantMatVecK4W4A8QF32", p + data_off, p, p + sub_off, qx.data_ptr(),
+                          xs.data_ptr(), y.data_ptr(), rows, bpr, cols, batch, stream.cuda_stream)
+
+            for i in range(copies + 5):
+                launch(i)
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+            torch.cuda.synchronize()
+            for i, (e0, e1) in enumerate(evs):
+                e0.record(stream)
+                launch(i)
+                e1.record(stream)
+            torch.cuda.synchronize()
+            ms = np.array([e0.elapsed_time(e1) for e0, e1 in evs])
+            algo_bytes = psize + 4 * cols * batch + 4 * rows * batch
+            avg_s = float(ms.mean()) * 1e-3
+            med_s = float(np.median(ms)) * 1e-3
+            out.append(dict(rows=rows, cols=cols, batch=batch, payload_bytes=psize, algo_bytes=algo_bytes,
+                            avg_us=avg_s * 1e6, median_us=med_s * 1e6, gbs=algo_bytes / avg_s / 1e9,
+                            frac=algo_bytes / avg_s / 1e9 / PEAK_HBM_GBS, rotation_copies=copies))
+            log(f"gemv {rows}x{cols} B={batch}: {avg_s*1e6:.2f} us avg, {algo_bytes/avg_s/1e9:.0f} GB/s")
+        del bufs, base
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(path, cfg, prompt, budget_s=15.0, max_tokens=24):
+    """The oracle (C restatement of Mantle's CPU path) on this host: decode tok/s."""
+    from oracle import oracle as o
+    from tests import models
+
+    threads = min(16, os.cpu_count() or 1)
+    o.set_threads(threads)
+    m = models.oracle_model(path, cfg, PROMPT_LEN + max_tokens + 2)
+    try:
+        t0 = time.perf_counter()
+        nxt = None
+        for t in prompt:
+            nxt = m.forward_greedy(t)
+        t_prefill = time.perf_counter() - t0
+        n = 0
+        t0 = time.perf_counter()
+        while n < max_tokens and time.perf_counter() - t0 < budget_s:
+            nxt = m.forward_greedy(nxt)
+            n += 1
+        dt = time.perf_counter() - t0
+    finally:
+        m.close()
+    return dict(value=n / dt, unit="tok/s", cores=threads, kind="port",
+                sample=f"{PROMPT_LEN}-token prompt ({PROMPT_LEN / t_prefill:.2f} tok/s) then {n} greedy decode "
+                       f"steps of the same Qwen3-0.6B k4 model, {threads} threads, oracle/ C restatement "
+                       f"of Mantle's archsimd path (AVX-512 reduction order)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV microbench")
+    ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "single-GPU build: bench.py measures one MI355X; --gpus > 1 is not supported "
+                                   "(see DESIGN.md for how the path would shard)"}))
+        sys.exit(2)
+
+    import torch
+
+    import mantle_amd
+    from mantle_amd.mcf import QWEN3_0_6B
+    from tests import models
+
+    os.makedirs(args.model_dir, exist_ok=True)
+    path = os.path.join(args.model_dir, "qwen3_0_6b_k4_seed0.mcf")
+    t0 = time.perf_counter()
+    models.pack(path, 0, QWEN3_0_6B)
+    log(f"model ready in {time.perf_counter() - t0:.1f} s: {path}")
+    prompt = models.prompt(PROMPT_LEN, QWEN3_0_6B["vocab"], 1)
+    max_ctx = PROMPT_LEN + args.warmup + args.steps + 8
+    rt = mantle_amd.new_backend("hip").load_model(path, max_context=max_ctx)
+    try:
+        # prefill (token-by-token, as Mantle runs k4 prefill), includes graph capture on first use
+        rt.prefill_tokens(prompt[:1])
+        rt.synchronize()
+        t0 = time.perf_counter()
+        rt.prefill_tokens(prompt[1:])
+        prefill_tps = (PROMPT_LEN - 1) / (time.perf_counter() - t0)
+        if args.warmup:
+            rt.decode_steps(args.warmup)
+        rt.synchronize()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        rt.decode_steps(args.steps)
+        rt.synchronize()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    finally:
+        rt.close()
+    tps = args.steps / dt
+    log(f"decode: {tps:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token), prefill {prefill_tps:.1f} tok/s")
+
+    gemv = []
+    if not args.no_gemv:
+        gemv = gemv_microbench([(151936, 1024), (3072, 1024), (1024, 3072), (2048, 1024)], [1, 8])
+    head = next((g for g in gemv if g["rows"] == 151936 and g["batch"] == 1), None)
+    roofline = None
+    if head:
+        roofline = dict(bound="hbm", achieved=round(head["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                        frac=round(head["frac"], 4), traffic=None,
+                        kernel="k4_gemv_kernel<W4A8,Store> 151936x1024 B=1",
+                        avg_launch_us=round(head["avg_us"], 3), algo_bytes_per_launch=head["algo_bytes"])
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(path, QWEN3_0_6B, prompt)
+            log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+        except Exception as e:  # the baseline is reported, never required
+            log(f"cpu baseline failed: {e!r}")
+    bytes_per_token = 321_272_832
+    line = {
+        "metric": "decode tok/s @batch1 + k4 GEMV HBM GB/s (% of peak), Qwen3-0.6B-shape k4",
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tps / CPU_BASELINE_README_TOKS, 2),
+        "dtype": "k4 weights x int8 activations, int32 block dots, fp32 accumulation",
+        "data": "synthetic: random-init N(0,0.02) weights seed 0 packed to MCF k4, 31 uniform token ids seed 1",
+        "config": {"workload": "Qwen3-0.6B-shape k4 greedy decode, batch 1 (28 blocks, d1024, ffn3072, 16/8 heads, "
+                               "hd128, vocab151936)", "prompt_tokens": PROMPT_LEN, "parallelism": "none (1 GPU)"},
+        "prefill_tok_s": round(prefill_tps, 2),
+        "effective_weight_gbs": round(bytes_per_token * tps / 1e9, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gemv],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

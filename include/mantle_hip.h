@@ -1,0 +1,166 @@
+/*
+ * mantle_hip.h -- C ABI of libmantle_hip.so, the MI355X (gfx950) backend for
+ * Mantle's k4 decode path.
+ *
+ * Conventions (same as Mantle's CUDA C ABI, internal/backend/cuda/native/softmax.h:1-115):
+ *  - every call returns a hipError_t as int (0 = success); null pointers and
+ *    non-positive sizes return hipErrorInvalidValue (1) before any launch;
+ *  - kernel-level calls take caller-owned device pointers, launch on the
+ *    caller's stream and never allocate, free or synchronise;
+ *  - the three k4 regions (f16 super-scales, u6 sub-scales, packed nibbles)
+ *    are passed as separate pointers, exactly as the MCF payload stores them
+ *    (pkg/mcf/quant_payload.go:86-112).
+ * "Parity" kernels reproduce the arithmetic order of Mantle's CPU archsimd
+ * path bit for bit; which ISA flavour (AVX-512 / AVX2 / scalar reduction
+ * order) they follow is set with mantleHipSetParityISA.
+ */
+#ifndef MANTLE_HIP_H
+#define MANTLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mantleHipStream_t; /* hipStream_t */
+
+#define MANTLE_HIP_ISA_SCALAR 0
+#define MANTLE_HIP_ISA_AVX2 1
+#define MANTLE_HIP_ISA_AVX512 2
+
+/* ---------------- library / device ---------------- */
+/* Replaces mantleCudaGetErrorString / mantleCudaGetDeviceCount
+ * (internal/backend/cuda/native/runtime.go:122-130). */
+const char* mantleHipGetErrorString(int err);
+int mantleHipGetDeviceCount(int* out);
+/* Reduction order the parity kernels follow (internal/backend/simd/tensor_cpu.go:18-24). */
+int mantleHipSetParityISA(int isa);
+int mantleHipGetParityISA(void);
+
+/* ---------------- k4 kernels ---------------- */
+/* W4A32 k4 GEMV; replaces mantleCudaQuantMatVecK4F32
+ * (internal/backend/cuda/native/softmax.h:32-41).  y[rows] = W x, fp32 x. */
+int mantleHipQuantMatVecK4F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                              const float* x, float* y, int rows, int blocksPerRow, int cols,
+                              mantleHipStream_t stream);
+/* W4A8 CPU-parity k4 GEMV: the arithmetic of Mantle's AVX2+ CPU path
+ * (internal/backend/simd/matvec.go:154-209, matvec_quant.go:256-296); batch
+ * vectors x[batch][cols] -> y[batch][rows].  Bit-exact to the CPU path. */
+int mantleHipQuantMatVecK4W4A8F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                                  const float* x, float* y, int rows, int blocksPerRow, int cols, int batch,
+                                  int8_t* qxScratch, float* xScaleScratch, mantleHipStream_t stream);
+/* Same GEMV on an activation already quantised by mantleHipQuantizeVecBlocksF32
+ * (MatVecWithQuant with a PrepareQuantVec result, internal/backend/simd/matvec.go:150-152,
+ * internal/backend/simd/quant_vec.go:7-16): qx [batch][blocksPerRow*32] permuted, xScales [batch][blocksPerRow]. */
+int mantleHipQuantMatVecK4W4A8QF32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                                   const int8_t* qx, const float* xScales, float* y, int rows, int blocksPerRow,
+                                   int cols, int batch, mantleHipStream_t stream);
+/* k4 -> f16 dense; replaces mantleCudaDequantizeK4ToF16 (internal/backend/cuda/native/softmax.h:50-57). */
+int mantleHipDequantizeK4ToF16(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                               uint16_t* outF16, int rows, int blocksPerRow, int cols, mantleHipStream_t stream);
+/* k4 -> f32 dense (exact: rowToQuant, internal/backend/core/quant_stub.go:51-85). */
+int mantleHipDequantizeK4ToF32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                               float* out, int rows, int blocksPerRow, int cols, mantleHipStream_t stream);
+/* Activation int8 quantiser (quantizeVecBlocksInto, internal/backend/simd/matvec_quant.go:746-797).
+ * qx is written in the even/odd permuted block layout the W4A8 GEMV reads:
+ * element e of block b lives at byte 32*b + 16*(e&1) + 4*(e>>3) + ((e>>1)&3). */
+int mantleHipQuantizeVecBlocksF32(const float* x, int n, int8_t* qx, float* scales, mantleHipStream_t stream);
+
+/* ---------------- fused / elementwise kernels ---------------- */
+/* Replaces mantleCudaRMSNormF32 / mantleCudaRMSNormBatchedF32 (internal/backend/cuda/native/rmsnorm.cu:91-123). */
+int mantleHipRMSNormF32(float* out, const float* x, const float* weight, float eps, int n, mantleHipStream_t stream);
+int mantleHipRMSNormBatchedF32(float* out, const float* x, const float* weight, float eps, int headDim, int nHeads,
+                               mantleHipStream_t stream);
+/* Replaces mantleCudaApplyRoPEInplaceF32 (internal/backend/cuda/native/attn_fused.cu:51-75); takes
+ * Mantle's float64 inverse frequencies (internal/backend/simd/loader.go:1604-1612). */
+int mantleHipApplyRoPEInplaceF32(float* x, const double* invFreq, int pos, float attnScale, int headDim, int half,
+                                 int nHeads, mantleHipStream_t stream);
+/* RoPE from precomputed float32 cos/sin rows (what the decode runtime uses). */
+int mantleHipApplyRoPEInplaceTableF32(float* x, const float* cosv, const float* sinv, int headDim, int half,
+                                      int nHeads, mantleHipStream_t stream);
+/* f32 KV append; the f32 twin of mantleCudaStoreKVF16Row (internal/backend/cuda/native/attn_fused.cu:91-107). */
+int mantleHipStoreKVF32Row(float* cache, const float* src, int cachePos, int kvStride, mantleHipStream_t stream);
+/* Decode attention over an f32 cache; f32 twin of mantleCudaAttentionInnerF16CacheF32
+ * (internal/backend/cuda/native/softmax.h:70-83), CPU-parity with RunAttnHeads
+ * (internal/backend/simd/attnpool.go:77-153).  scoresScratch: nHead*(pos+1) floats. */
+int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const float* cacheV, float* out,
+                                    float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
+                                    int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
+/* Replaces mantleCudaSoftmaxRowsF32 (softmax.h:13), with Mantle's CPU fastExp / ordered sum. */
+int mantleHipSoftmaxRowsF32(float* data, int rows, int cols, mantleHipStream_t stream);
+/* Replaces mantleCudaSiluMulF32 (softmax.h:59-64), CPU fastSiluVec arithmetic. */
+int mantleHipSiluMulF32(const float* gate, const float* up, float* out, int n, mantleHipStream_t stream);
+/* Replaces mantleCudaAddVectorsF32 (internal/backend/cuda/native/add_vectors.cu:18-30). */
+int mantleHipAddVectorsF32(float* dst, const float* src, int n, mantleHipStream_t stream);
+/* Replaces mantleCudaArgMaxF32 (softmax.h:105-109): first maximum wins. */
+int mantleHipArgMaxF32(const float* x, int n, int* outIdx, mantleHipStream_t stream);
+
+/* ---------------- host-side k4 producer and MCF container ---------------- */
+/* QuantPayloadSize for k4 (pkg/mcf/quant_payload.go:15-113). */
+int64_t mantleHipK4PayloadSize(int64_t rows, int64_t cols);
+/* quantizeTensor + quantizeK (cmd/mantle/quantize.go:352-398, 530-651), host code. */
+int mantleHipQuantizeK4Host(const float* src, int64_t rows, int64_t cols, uint8_t* payload);
+
+typedef struct {
+    int n_layers, d_model, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    double rope_base;
+    float eps;
+    int tie_embeddings;
+} mantleHipQwen3Config;
+
+/* Write a random-init (N(0,0.02), unit norm gains) Qwen3-shaped model as an MCF
+ * file with k4 weights: the equivalent of `mantle pack` + `mantle quantize
+ * --method k4` (pkg/mcf/pack.go:68, cmd/mantle/quantize.go:174-350). */
+int mantleHipPackSyntheticQwen3(const char* path, const mantleHipQwen3Config* cfg, uint64_t seed, int threads);
+/* Deterministic N(0, std) generator used by the packer (splitmix64 + Box-Muller). */
+int mantleHipFillNormal(float* dst, int64_t n, uint64_t seed, float std);
+
+/* Read-only MCF view (pkg/mcf/reader.go:21-69, pkg/mcf/tensor_index.go:132-220). */
+typedef struct mantleHipMCF mantleHipMCF;
+int mantleHipMCFOpen(const char* path, mantleHipMCF** out);
+void mantleHipMCFClose(mantleHipMCF* f);
+int mantleHipMCFTensorCount(const mantleHipMCF* f);
+/* name (NUL-terminated copy into nameBuf), dtype, rank, shape[4], payload pointer into the mapping. */
+int mantleHipMCFTensorInfo(const mantleHipMCF* f, int i, char* nameBuf, int nameBufLen, int* dtype, int* rank,
+                           int64_t* shape, const uint8_t** data, uint64_t* size);
+int mantleHipMCFFind(const mantleHipMCF* f, const char* name);
+/* Section payload by type (e.g. 0x0100 = HF config.json). */
+int mantleHipMCFSection(const mantleHipMCF* f, uint32_t type, const uint8_t** data, uint64_t* size);
+
+/* ---------------- model runtime (Backend.LoadModel / core.Runtime) ---------------- */
+/* One Qwen3-shaped k4 model resident in HBM, greedy decode on one stream.
+ * Replaces backend.Backend.LoadModel + core.Runtime (internal/backend/backend.go:17-36,
+ * internal/backend/core/interfaces.go:4-18) for the k4 decode path. */
+typedef struct mantleHipModel mantleHipModel;
+int mantleHipModelLoadMCF(const char* path, int maxContext, mantleHipModel** out);
+void mantleHipModelClose(mantleHipModel* m);
+int mantleHipModelConfig(const mantleHipModel* m, mantleHipQwen3Config* out);
+/* Reset(): Pos = 0 (internal/backend/simd/runtime.go:293-333). */
+int mantleHipModelReset(mantleHipModel* m);
+int mantleHipModelPos(const mantleHipModel* m, int* pos);
+/* ForwardToken (runtime.go:224): logits of the step copied to host (vocab floats). */
+int mantleHipModelForwardToken(mantleHipModel* m, int tok, float* logitsHost);
+/* ForwardTokenGreedy (internal/backend/simd/runtime_greedy.go:12-67). */
+int mantleHipModelForwardTokenGreedy(mantleHipModel* m, int tok, int* next);
+/* PrefillTokens (internal/backend/simd/runtime_prefill.go:11-30): token-by-token,
+ * as Mantle runs k4 prefill; *next receives the greedy token after the last one. */
+int mantleHipModelPrefillTokens(mantleHipModel* m, const int* toks, int n, int* next);
+/* Greedy generation kept on the device: prompt then nGen tokens, one replay
+ * of the captured decode-step graph per position, no host round trip between
+ * steps.  outTokens receives the nGen generated ids. */
+int mantleHipModelGenerateGreedy(mantleHipModel* m, const int* prompt, int nPrompt, int nGen, int* outTokens);
+/* Launch `steps` decode steps continuing from the current position with the
+ * device-side argmax feeding the next step (no host sync); for timing. */
+int mantleHipModelDecodeSteps(mantleHipModel* m, int steps);
+int mantleHipModelSynchronize(mantleHipModel* m);
+/* Residual stream x after the last step (d_model floats) -- divergence bisection aid. */
+int mantleHipModelHidden(mantleHipModel* m, float* out);
+/* Use the captured HIP graph for a decode step (1, default) or plain launches (0). */
+int mantleHipModelSetUseGraph(mantleHipModel* m, int on);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,115 @@
+"""ctypes binding of libmantle_hip.so (the C ABI in include/mantle_hip.h).
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback behind any entry point of this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmantle_hip.so")
+
+P = C.c_void_p
+I = C.c_int
+I64 = C.c_int64
+U64 = C.c_uint64
+F = C.c_float
+D = C.c_double
+
+
+class Qwen3Config(C.Structure):
+    _fields_ = [
+        ("n_layers", I), ("d_model", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I),
+        ("ffn", I), ("vocab", I), ("rope_base", D), ("eps", F), ("tie_embeddings", I),
+    ]
+
+    def as_dict(self) -> dict:
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "mantleHipGetErrorString": (C.c_char_p, [I]),
+    "mantleHipGetDeviceCount": (I, [C.POINTER(I)]),
+    "mantleHipSetParityISA": (I, [I]),
+    "mantleHipGetParityISA": (I, []),
+    "mantleHipQuantMatVecK4F32": (I, [P, P, P, P, P, I, I, I, P]),
+    "mantleHipQuantMatVecK4W4A8F32": (I, [P, P, P, P, P, I, I, I, I, P, P, P]),
+    "mantleHipQuantMatVecK4W4A8QF32": (I, [P, P, P, P, P, P, I, I, I, I, P]),
+    "mantleHipDequantizeK4ToF16": (I, [P, P, P, P, I, I, I, P]),
+    "mantleHipDequantizeK4ToF32": (I, [P, P, P, P, I, I, I, P]),
+    "mantleHipQuantizeVecBlocksF32": (I, [P, I, P, P, P]),
+    "mantleHipRMSNormF32": (I, [P, P, P, F, I, P]),
+    "mantleHipRMSNormBatchedF32": (I, [P, P, P, F, I, I, P]),
+    "mantleHipApplyRoPEInplaceF32": (I, [P, P, I, F, I, I, I, P]),
+    "mantleHipApplyRoPEInplaceTableF32": (I, [P, P, P, I, I, I, P]),
+    "mantleHipStoreKVF32Row": (I, [P, P, I, I, P]),
+    "mantleHipAttentionInnerF32Cache": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "mantleHipSoftmaxRowsF32": (I, [P, I, I, P]),
+    "mantleHipSiluMulF32": (I, [P, P, P, I, P]),
+    "mantleHipAddVectorsF32": (I, [P, P, I, P]),
+    "mantleHipArgMaxF32": (I, [P, I, P, P]),
+    "mantleHipK4PayloadSize": (I64, [I64, I64]),
+    "mantleHipQuantizeK4Host": (I, [P, I64, I64, P]),
+    "mantleHipPackSyntheticQwen3": (I, [C.c_char_p, C.POINTER(Qwen3Config), U64, I]),
+    "mantleHipFillNormal": (I, [P, I64, U64, F]),
+    "mantleHipMCFOpen": (I, [C.c_char_p, C.POINTER(P)]),
+    "mantleHipMCFClose": (None, [P]),
+    "mantleHipMCFTensorCount": (I, [P]),
+    "mantleHipMCFTensorInfo": (I, [P, I, C.c_char_p, I, C.POINTER(I), C.POINTER(I), C.POINTER(I64),
+                                   C.POINTER(P), C.POINTER(U64)]),
+    "mantleHipMCFFind": (I, [P, C.c_char_p]),
+    "mantleHipMCFSection": (I, [P, C.c_uint32, C.POINTER(P), C.POINTER(U64)]),
+    "mantleHipModelLoadMCF": (I, [C.c_char_p, I, C.POINTER(P)]),
+    "mantleHipModelClose": (None, [P]),
+    "mantleHipModelConfig": (I, [P, C.POINTER(Qwen3Config)]),
+    "mantleHipModelReset": (I, [P]),
+    "mantleHipModelPos": (I, [P, C.POINTER(I)]),
+    "mantleHipModelForwardToken": (I, [P, I, P]),
+    "mantleHipModelForwardTokenGreedy": (I, [P, I, C.POINTER(I)]),
+    "mantleHipModelPrefillTokens": (I, [P, P, I, C.POINTER(I)]),
+    "mantleHipModelGenerateGreedy": (I, [P, P, I, I, P]),
+    "mantleHipModelDecodeSteps": (I, [P, I]),
+    "mantleHipModelSynchronize": (I, [P]),
+    "mantleHipModelHidden": (I, [P, P]),
+    "mantleHipModelSetUseGraph": (I, [P, I]),
+}
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        msg = lib().mantleHipGetErrorString(code)
+        super().__init__(f"{fn} failed: hip error {code} ({msg.decode() if msg else '?'})")
+        self.code = code
+
+
+def lib() -> C.CDLL:
+    """The loaded libmantle_hip.so; raises if it was never built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m mantle_amd.build`")
+        so = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(so, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = so
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGS)
+
+
+def check(fn: str, code: int) -> None:
+    if code != 0:
+        raise HipError(fn, code)
+
+
+def call(fn: str, *args) -> None:
+    check(fn, getattr(lib(), fn)(*args))

@@ -1,0 +1,108 @@
+"""Host-side mirror of Mantle's backend seam for the HIP backend.
+
+Mantle: backend.New(name) -> Backend{Name(), LoadModel(...)} -> core.Runtime
+with ForwardToken / ForwardTokenGreedy / PrefillTokens / Reset / Close
+(internal/backend/backend.go:17-36, internal/backend/core/interfaces.go:4-18,
+internal/inference/engine.go:129-191).  Errors surface as exceptions, as the
+Go side surfaces them as `error` values; nothing falls back to the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import I, P, Qwen3Config, call, lib
+
+ISA = {"scalar": 0, "avx2": 1, "avx512": 2}
+
+
+def new_backend(name: str = "hip") -> "Backend":
+    """backend.New (internal/backend/backend.go:22-36) with the `hip` case."""
+    n = name.strip().lower()
+    if n in ("hip", "rocm", "auto"):
+        return Backend()
+    raise ValueError(f"unknown backend {name!r} (this package provides only 'hip')")
+
+
+class Backend:
+    def name(self) -> str:
+        return "hip"
+
+    def load_model(self, path: str, max_context: int = 4096, parity_isa: str = "avx512") -> "Runtime":
+        call("mantleHipSetParityISA", ISA[parity_isa])
+        h = P()
+        call("mantleHipModelLoadMCF", path.encode(), int(max_context), C.byref(h))
+        return Runtime(h, max_context)
+
+
+class Runtime:
+    def __init__(self, handle: P, max_context: int):
+        self._h = handle
+        self.max_context = max_context
+        cfg = Qwen3Config()
+        call("mantleHipModelConfig", handle, C.byref(cfg))
+        self.config = cfg.as_dict()
+
+    def _handle(self):
+        if not self._h:
+            raise RuntimeError("runtime is closed")
+        return self._h
+
+    @property
+    def pos(self) -> int:
+        p = I()
+        call("mantleHipModelPos", self._handle(), C.byref(p))
+        return p.value
+
+    def reset(self) -> None:
+        call("mantleHipModelReset", self._handle())
+
+    def forward_token(self, tok: int) -> np.ndarray:
+        logits = np.empty(self.config["vocab"], dtype=np.float32)
+        call("mantleHipModelForwardToken", self._handle(), int(tok), logits.ctypes.data)
+        return logits
+
+    def forward_token_greedy(self, tok: int) -> int:
+        nxt = I()
+        call("mantleHipModelForwardTokenGreedy", self._handle(), int(tok), C.byref(nxt))
+        return nxt.value
+
+    def prefill_tokens(self, toks) -> int:
+        arr = np.ascontiguousarray(toks, dtype=np.int32)
+        nxt = I()
+        call("mantleHipModelPrefillTokens", self._handle(), arr.ctypes.data, len(arr), C.byref(nxt))
+        return nxt.value
+
+    def generate_greedy(self, prompt, n_gen: int) -> list[int]:
+        arr = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_gen, dtype=np.int32)
+        call("mantleHipModelGenerateGreedy", self._handle(), arr.ctypes.data, len(arr), int(n_gen),
+             out.ctypes.data)
+        return out.tolist()
+
+    def decode_steps(self, steps: int) -> None:
+        """Enqueue `steps` device-fed greedy steps (asynchronous)."""
+        call("mantleHipModelDecodeSteps", self._handle(), int(steps))
+
+    def synchronize(self) -> None:
+        call("mantleHipModelSynchronize", self._handle())
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(self.config["d_model"], dtype=np.float32)
+        call("mantleHipModelHidden", self._handle(), out.ctypes.data)
+        return out
+
+    def set_use_graph(self, on: bool) -> None:
+        call("mantleHipModelSetUseGraph", self._handle(), int(bool(on)))
+
+    def close(self) -> None:
+        if self._h:
+            lib().mantleHipModelClose(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()

@@ -1,0 +1,103 @@
+// kernels.h -- host-side launchers for the gfx950 kernels in kernels.hip.
+// Every launcher validates its arguments on the host, enqueues on `stream`
+// and returns a hipError_t; nothing here allocates or synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mantle {
+
+// CPU ISA flavour whose reduction order the parity kernels reproduce
+// (internal/backend/simd/tensor_cpu.go:18-24 selects it on the host).
+enum Isa : int { kIsaScalar = 0, kIsaAvx2 = 1, kIsaAvx512 = 2 };
+
+// One k4 matrix inside a (possibly multi-matrix) GEMV launch.  The three
+// pointers are the SoA regions of the MCF k4 payload (pkg/mcf/quant_payload.go).
+struct K4Mat {
+    const uint8_t* nib;    // [rows][blocks_per_row][16]
+    const uint8_t* sub;    // [rows][blocks_per_row] u6 in bits 0-5
+    const uint16_t* sup;   // [rows][super_per_row] f16 (Mantle truncating encoding)
+    int rows;
+};
+
+// Region pointers of a k4 payload that starts at `payload`.
+K4Mat k4_mat_from_payload(const uint8_t* payload, int rows, int cols);
+int64_t k4_payload_size(int64_t rows, int64_t cols);
+
+enum GemvEpi : int {
+    kEpiStore = 0,    // y[b][r] = sum
+    kEpiResAdd = 1,   // y[r] = y[r] + sum  (residual folded into the epilogue)
+    kEpiSiluMul = 2,  // two matrices (gate, up): y[r] = silu(gate_r) * up_r
+    kEpiArgmax = 3,   // y[r] = sum and a 64-bit (value, -index) atomicMax key
+};
+
+// Device-resident decode state (one per model).
+struct DecodeState {
+    int pos;            // next position to run
+    int next_tok;       // argmax of the last step
+    int n_prompt;       // positions < n_prompt take their token from prompt[]
+    int pad;
+    unsigned long long argmax_key;
+};
+
+// y = W * x with x quantised per 32-block to int8 (Mantle's W4A8 CPU path).
+// qx: [batch][blocks*32] in the even/odd permuted layout quantize_vec writes;
+// xs: [batch][blocks].  outs[i] receives matrix i's rows.
+hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, int cols,
+                               const int8_t* qx, const float* xs, int batch, GemvEpi epi,
+                               unsigned long long* argmax_key, hipStream_t stream);
+// y = W * x with fp32 x (W4A32; tolerance-checked, not bit-exact).
+hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch,
+                                hipStream_t stream);
+
+// Activation quantiser (internal/backend/simd/matvec_quant.go:746-797), optionally
+// preceded by Mantle's RMSNorm (weight != nullptr).  norm_out (nullable) receives
+// the normalised fp32 vector.  batch rows of length n, one workgroup per row.
+hipError_t launch_quantize_vec(const float* x, const float* weight, float eps, int n, int batch, int isa,
+                               int8_t* qx, float* xs, float* norm_out, hipStream_t stream);
+
+hipError_t launch_rmsnorm(float* out, const float* x, const float* weight, float eps, int n, int rows,
+                          int isa, hipStream_t stream);
+
+// Fused decode attention for one layer: per-head q/k RMSNorm, RoPE (host
+// tables), KV append at *pos, scores, softmax, weighted V sum.
+struct AttnArgs {
+    const float* q;        // [n_head*head_dim] raw projection
+    const float* k;        // [kv_heads*head_dim]
+    const float* v;
+    const float* q_norm;   // [head_dim] or null (no norm)
+    const float* k_norm;
+    float eps;
+    const float* rope_cos; // [max_ctx][head_dim/2] or null (no RoPE)
+    const float* rope_sin;
+    const int* pos_dev;    // device position (fused) ...
+    int pos_host;          // ... or a host position when pos_dev is null
+    float* cache_k;        // [max_ctx][kv_stride]
+    float* cache_v;
+    float* scores;         // [n_head][max_ctx] scratch
+    float* out;            // [n_head*head_dim]
+    int n_head, kv_heads, head_dim, kv_stride, max_ctx;
+    float scale;
+    int fused;             // 1: norm/rope/append inside, 0: q and cache are final
+    int isa;
+};
+hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
+
+hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
+                        hipStream_t stream);
+hipError_t launch_finish_step(DecodeState* st, int* out_tokens, hipStream_t stream);
+
+// Small standalone ops behind the mantleHip* C ABI.
+hipError_t launch_dequant_k4(const K4Mat& m, int cols, float* out_f32, uint16_t* out_f16, hipStream_t stream);
+hipError_t launch_silu_mul(const float* gate, const float* up, float* out, int n, hipStream_t stream);
+hipError_t launch_add(float* dst, const float* src, int n, hipStream_t stream);
+hipError_t launch_argmax(const float* x, int n, int* out_idx, hipStream_t stream);
+hipError_t launch_softmax_rows(float* data, int rows, int cols, hipStream_t stream);
+hipError_t launch_rope_table(float* x, const float* cosv, const float* sinv, int head_dim, int half, int n_heads,
+                             hipStream_t stream);
+hipError_t launch_rope_f64(float* x, const double* inv_freq, int pos, float attn_scale, int head_dim, int half,
+                           int n_heads, hipStream_t stream);
+hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, int kv_stride, hipStream_t stream);
+
+}  // namespace mantle

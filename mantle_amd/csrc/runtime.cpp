@@ -1,0 +1,474 @@
+// runtime.cpp -- Qwen3-shaped k4 decoder resident in HBM, greedy decode.
+//
+// Replaces, for the k4 decode path, the Go plug-in seam backend.Backend.LoadModel
+// + core.Runtime (internal/backend/backend.go:17-36, internal/backend/core/interfaces.go:4-18)
+// with the CUDA backend's "whole token on device" design
+// (internal/backend/cuda/attn_pipeline.go:391-805, internal/backend/cuda/ops.go:2180-2519):
+//
+//   * every k4 payload of the MCF is copied once, unchanged, into one HBM
+//     arena (256-byte aligned per tensor); the GEMV reads the MCF layout;
+//   * the decode state (position, next token, prompt, argmax key) lives in
+//     device memory, so one decode step is a fixed sequence of kernel
+//     launches that never reads the host: it is captured once as a HIP
+//     graph and replayed per position;
+//   * the f32 KV cache is [layer][max_ctx][kv_heads*head_dim], contiguous per layer.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/mantle_hip.h"
+#include "kernels.h"
+#include "mcf.h"
+
+using namespace mantle;
+
+extern "C" int mantleHipGetParityISA(void);
+
+struct mantleHipModel {
+    mantleHipQwen3Config cfg{};
+    int max_ctx = 0;
+    int isa = kIsaAvx512;
+    int q_dim = 0, kv_dim = 0;
+    hipStream_t stream = nullptr;
+    uint8_t* arena = nullptr;
+    size_t arena_bytes = 0;
+    K4Mat embed{}, lm_head{};
+    const float* final_norm = nullptr;
+    struct Layer {
+        const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+        K4Mat wq, wk, wv, wo, gate, up, down;
+    };
+    std::vector<Layer> layers;
+    // activations / scratch
+    float *x = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *scores = nullptr;
+    int8_t* qx = nullptr;
+    float* xs = nullptr;
+    float *cache_k = nullptr, *cache_v = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    DecodeState* state = nullptr;
+    int* prompt = nullptr;
+    int* out_tokens = nullptr;
+    int pos = 0;  // host mirror of state->pos
+    bool use_graph = true;
+    hipGraphExec_t graph = nullptr;
+};
+
+static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
+    const mantleHipQwen3Config& c = m->cfg;
+    hipError_t e;
+#define TRY(x)                         \
+    do {                               \
+        if ((e = (x)) != hipSuccess) { \
+            return e;                  \
+        }                              \
+    } while (0)
+    const int d = c.d_model;
+    float* q = m->qkv;
+    float* k = m->qkv + m->q_dim;
+    float* v = k + m->kv_dim;
+    TRY(launch_embed(m->embed, d, m->prompt, m->state, m->x, s));
+    for (int l = 0; l < c.n_layers; l++) {
+        const auto& L = m->layers[l];
+        // runtime_decode.go:107 RMSNorm + attn.go:180-205 shared int8 activation for Q, K, V
+        TRY(launch_quantize_vec(m->x, L.attn_norm, c.eps, d, 1, m->isa, m->qx, m->xs, nullptr, s));
+        K4Mat qkv[3] = {L.wq, L.wk, L.wv};
+        float* outs[3] = {q, k, v};
+        TRY(launch_k4_gemv_w4a8(qkv, outs, 3, d, m->qx, m->xs, 1, kEpiStore, nullptr, s));
+        AttnArgs a{};
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.q_norm = L.q_norm;
+        a.k_norm = L.k_norm;
+        a.eps = c.eps;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.pos_dev = &m->state->pos;
+        a.cache_k = m->cache_k + (size_t)l * m->max_ctx * m->kv_dim;
+        a.cache_v = m->cache_v + (size_t)l * m->max_ctx * m->kv_dim;
+        a.scores = m->scores;
+        a.out = m->attn;
+        a.n_head = c.n_heads;
+        a.kv_heads = c.n_kv_heads;
+        a.head_dim = c.head_dim;
+        a.kv_stride = m->kv_dim;
+        a.max_ctx = m->max_ctx;
+        a.scale = (float)(1.0 / sqrt((double)c.head_dim));  // attn.go:311-314
+        a.fused = 1;
+        a.isa = m->isa;
+        TRY(launch_attention_decode(a, s));
+        // attn.go:417 Wo on the re-quantised attention output, residual folded in
+        TRY(launch_quantize_vec(m->attn, nullptr, 0.0f, m->q_dim, 1, m->isa, m->qx, m->xs, nullptr, s));
+        float* xo[1] = {m->x};
+        TRY(launch_k4_gemv_w4a8(&L.wo, xo, 1, m->q_dim, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
+        // ffn.go:18-91: RMSNorm, up/gate on one int8 activation, SiLU*up, down + residual
+        TRY(launch_quantize_vec(m->x, L.ffn_norm, c.eps, d, 1, m->isa, m->qx, m->xs, nullptr, s));
+        K4Mat gu[2] = {L.gate, L.up};
+        float* ao[2] = {m->act, m->act};
+        TRY(launch_k4_gemv_w4a8(gu, ao, 2, d, m->qx, m->xs, 1, kEpiSiluMul, nullptr, s));
+        TRY(launch_quantize_vec(m->act, nullptr, 0.0f, c.ffn, 1, m->isa, m->qx, m->xs, nullptr, s));
+        TRY(launch_k4_gemv_w4a8(&L.down, xo, 1, c.ffn, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
+    }
+    // runtime_greedy.go:53-67: final RMSNorm, lm_head, argmax (first max wins)
+    TRY(launch_quantize_vec(m->x, m->final_norm, c.eps, d, 1, m->isa, m->qx, m->xs, nullptr, s));
+    float* lo[1] = {m->logits};
+    TRY(launch_k4_gemv_w4a8(&m->lm_head, lo, 1, d, m->qx, m->xs, 1, kEpiArgmax, &m->state->argmax_key, s));
+    TRY(launch_finish_step(m->state, m->out_tokens, s));
+#undef TRY
+    return hipSuccess;
+}
+
+static hipError_t run_steps(mantleHipModel* m, int steps) {
+    if (steps <= 0) return hipSuccess;
+    if (m->pos + steps > m->max_ctx) return hipErrorInvalidValue;  // context length exceeded
+    hipError_t e = hipSuccess;
+    if (m->use_graph && !m->graph) {
+        hipGraph_t g = nullptr;
+        e = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return e;
+        hipError_t le = enqueue_step(m, m->stream);
+        e = hipStreamEndCapture(m->stream, &g);
+        if (le != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return le;
+        }
+        if (e != hipSuccess) return e;
+        e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            m->graph = nullptr;
+            return e;
+        }
+    }
+    for (int i = 0; i < steps; i++) {
+        e = m->use_graph ? hipGraphLaunch(m->graph, m->stream) : enqueue_step(m, m->stream);
+        if (e != hipSuccess) return e;
+        m->pos++;
+    }
+    return hipSuccess;
+}
+
+// Minimal reader for the numeric keys of an HF config.json.
+static bool json_number(const std::string& js, const char* key, double* out) {
+    std::string k = std::string("\"") + key + "\"";
+    size_t p = js.find(k);
+    if (p == std::string::npos) return false;
+    p = js.find(':', p + k.size());
+    if (p == std::string::npos) return false;
+    p++;
+    while (p < js.size() && (js[p] == ' ' || js[p] == '\t' || js[p] == '\n' || js[p] == '\r')) p++;
+    if (js.compare(p, 4, "true") == 0) { *out = 1; return true; }
+    if (js.compare(p, 5, "false") == 0) { *out = 0; return true; }
+    char* end = nullptr;
+    double v = strtod(js.c_str() + p, &end);
+    if (end == js.c_str() + p) return false;
+    *out = v;
+    return true;
+}
+
+static void free_model(mantleHipModel* m) {
+    if (!m) return;
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->qx, m->xs, m->cache_k,
+                    m->cache_v, m->rope_cos, m->rope_sin, m->state, m->prompt, m->out_tokens};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+extern "C" void mantleHipModelClose(mantleHipModel* m) {
+    if (m && m->stream) (void)hipStreamSynchronize(m->stream);
+    free_model(m);
+}
+
+// LoadModelMCF (internal/backend/simd/loader.go:51-80 + internal/backend/cuda/cuda.go:39-73,
+// internal/backend/cuda/ops.go:5214-5313 weight residency).
+extern "C" int mantleHipModelLoadMCF(const char* path, int max_ctx, mantleHipModel** out) {
+    if (!path || !out || max_ctx <= 0) return hipErrorInvalidValue;
+    *out = nullptr;
+    McfFile f;
+    std::string err;
+    if (!f.open(path, &err)) {
+        fprintf(stderr, "mantle_hip: %s: %s\n", path, err.c_str());
+        return hipErrorInvalidValue;
+    }
+    const McfSection* cs = f.section(kSecHFConfigJSON);
+    if (!cs) {
+        fprintf(stderr, "mantle_hip: %s: missing config.json section\n", path);
+        return hipErrorInvalidValue;
+    }
+    std::string js((const char*)f.data() + cs->off, cs->size);
+    mantleHipModel* m = new mantleHipModel();
+    mantleHipQwen3Config& c = m->cfg;
+    double v;
+    auto need = [&](const char* key, double* dst) {
+        if (!json_number(js, key, dst)) {
+            fprintf(stderr, "mantle_hip: config.json lacks %s\n", key);
+            return false;
+        }
+        return true;
+    };
+    double L, D, H, KV, F, V, HD;
+    if (!need("num_hidden_layers", &L) || !need("hidden_size", &D) || !need("num_attention_heads", &H) ||
+        !need("intermediate_size", &F) || !need("vocab_size", &V)) {
+        free_model(m);
+        return hipErrorInvalidValue;
+    }
+    KV = json_number(js, "num_key_value_heads", &v) ? v : H;
+    HD = json_number(js, "head_dim", &v) ? v : D / H;
+    c.n_layers = (int)L;
+    c.d_model = (int)D;
+    c.n_heads = (int)H;
+    c.n_kv_heads = (int)KV;
+    c.head_dim = (int)HD;
+    c.ffn = (int)F;
+    c.vocab = (int)V;
+    c.rope_base = json_number(js, "rope_theta", &v) ? v : 10000.0;
+    c.eps = json_number(js, "rms_norm_eps", &v) ? (float)v : 1e-6f;
+    c.tie_embeddings = f.find("lm_head.weight") < 0;
+    m->max_ctx = max_ctx;
+    m->isa = mantleHipGetParityISA();
+    m->q_dim = c.n_heads * c.head_dim;
+    m->kv_dim = c.n_kv_heads * c.head_dim;
+    if (c.head_dim > 256 || (c.head_dim & 1) || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) {
+        fprintf(stderr, "mantle_hip: unsupported attention shape\n");
+        free_model(m);
+        return hipErrorInvalidValue;
+    }
+
+    // Tensor plan: (name, expected dtype, rows, cols); qwen3Spec names (internal/model/modelspec.go:173-240).
+    struct Want {
+        std::string name;
+        uint16_t dtype;
+        int64_t rows, cols;
+        size_t arena_off;
+    };
+    std::vector<Want> wants;
+    auto lname = [](int l, const char* s) { return "model.layers." + std::to_string(l) + "." + s; };
+    wants.push_back({"model.embed_tokens.weight", kDTypeK4, c.vocab, c.d_model, 0});
+    if (!c.tie_embeddings) wants.push_back({"lm_head.weight", kDTypeK4, c.vocab, c.d_model, 0});
+    wants.push_back({"model.norm.weight", kDTypeF32, c.d_model, 1, 0});
+    for (int l = 0; l < c.n_layers; l++) {
+        wants.push_back({lname(l, "input_layernorm.weight"), kDTypeF32, c.d_model, 1, 0});
+        wants.push_back({lname(l, "post_attention_layernorm.weight"), kDTypeF32, c.d_model, 1, 0});
+        wants.push_back({lname(l, "self_attn.q_norm.weight"), kDTypeF32, c.head_dim, 1, 0});
+        wants.push_back({lname(l, "self_attn.k_norm.weight"), kDTypeF32, c.head_dim, 1, 0});
+        wants.push_back({lname(l, "self_attn.q_proj.weight"), kDTypeK4, m->q_dim, c.d_model, 0});
+        wants.push_back({lname(l, "self_attn.k_proj.weight"), kDTypeK4, m->kv_dim, c.d_model, 0});
+        wants.push_back({lname(l, "self_attn.v_proj.weight"), kDTypeK4, m->kv_dim, c.d_model, 0});
+        wants.push_back({lname(l, "self_attn.o_proj.weight"), kDTypeK4, c.d_model, m->q_dim, 0});
+        wants.push_back({lname(l, "mlp.gate_proj.weight"), kDTypeK4, c.ffn, c.d_model, 0});
+        wants.push_back({lname(l, "mlp.up_proj.weight"), kDTypeK4, c.ffn, c.d_model, 0});
+        wants.push_back({lname(l, "mlp.down_proj.weight"), kDTypeK4, c.d_model, c.ffn, 0});
+    }
+    size_t total = 0;
+    std::vector<int> tidx;
+    for (auto& w : wants) {
+        int i = f.find(w.name);
+        if (i < 0) {
+            fprintf(stderr, "mantle_hip: missing tensor %s\n", w.name.c_str());
+            free_model(m);
+            return hipErrorInvalidValue;
+        }
+        const McfTensor& t = f.tensors()[i];
+        bool shape_ok = w.dtype == kDTypeK4
+                            ? (t.shape.size() == 2 && (int64_t)t.shape[0] == w.rows && (int64_t)t.shape[1] == w.cols)
+                            : (t.shape.size() == 1 && (int64_t)t.shape[0] == w.rows);
+        if (t.dtype != w.dtype || !shape_ok) {
+            fprintf(stderr, "mantle_hip: tensor %s has unexpected dtype/shape\n", w.name.c_str());
+            free_model(m);
+            return hipErrorInvalidValue;
+        }
+        w.arena_off = total;
+        total += (t.size + 255) & ~(size_t)255;
+        tidx.push_back(i);
+    }
+    hipError_t e;
+#define CHECK(x)                  \
+    do {                          \
+        if ((e = (x)) != hipSuccess) { \
+            free_model(m);        \
+            return e;             \
+        }                         \
+    } while (0)
+    CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    CHECK(hipMalloc((void**)&m->arena, total));
+    m->arena_bytes = total;
+    for (size_t j = 0; j < wants.size(); j++) {
+        const McfTensor& t = f.tensors()[tidx[j]];
+        CHECK(hipMemcpy(m->arena + wants[j].arena_off, f.data() + t.off, t.size, hipMemcpyHostToDevice));
+    }
+    size_t wi = 0;
+    auto nextk = [&](int rows, int cols) { return k4_mat_from_payload(m->arena + wants[wi++].arena_off, rows, cols); };
+    auto nextf = [&]() { return reinterpret_cast<const float*>(m->arena + wants[wi++].arena_off); };
+    m->embed = nextk(c.vocab, c.d_model);
+    m->lm_head = c.tie_embeddings ? m->embed : nextk(c.vocab, c.d_model);
+    m->final_norm = nextf();
+    m->layers.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        auto& Ly = m->layers[l];
+        Ly.attn_norm = nextf();
+        Ly.ffn_norm = nextf();
+        Ly.q_norm = nextf();
+        Ly.k_norm = nextf();
+        Ly.wq = nextk(m->q_dim, c.d_model);
+        Ly.wk = nextk(m->kv_dim, c.d_model);
+        Ly.wv = nextk(m->kv_dim, c.d_model);
+        Ly.wo = nextk(c.d_model, m->q_dim);
+        Ly.gate = nextk(c.ffn, c.d_model);
+        Ly.up = nextk(c.ffn, c.d_model);
+        Ly.down = nextk(c.d_model, c.ffn);
+    }
+    int big = c.d_model > m->q_dim ? c.d_model : m->q_dim;
+    big = big > c.ffn ? big : c.ffn;
+    const int big_blocks = (big + 31) / 32;
+    CHECK(hipMalloc((void**)&m->x, sizeof(float) * c.d_model));
+    CHECK(hipMalloc((void**)&m->qkv, sizeof(float) * (m->q_dim + 2 * m->kv_dim)));
+    CHECK(hipMalloc((void**)&m->attn, sizeof(float) * m->q_dim));
+    CHECK(hipMalloc((void**)&m->act, sizeof(float) * c.ffn));
+    CHECK(hipMalloc((void**)&m->logits, sizeof(float) * c.vocab));
+    CHECK(hipMalloc((void**)&m->scores, sizeof(float) * (size_t)c.n_heads * max_ctx));
+    CHECK(hipMalloc((void**)&m->qx, (size_t)big_blocks * 32));
+    CHECK(hipMalloc((void**)&m->xs, sizeof(float) * big_blocks));
+    const size_t kv_elems = (size_t)c.n_layers * max_ctx * m->kv_dim;
+    CHECK(hipMalloc((void**)&m->cache_k, sizeof(float) * kv_elems));
+    CHECK(hipMalloc((void**)&m->cache_v, sizeof(float) * kv_elems));
+    CHECK(hipMalloc((void**)&m->state, sizeof(DecodeState)));
+    CHECK(hipMalloc((void**)&m->prompt, sizeof(int) * max_ctx));
+    CHECK(hipMalloc((void**)&m->out_tokens, sizeof(int) * max_ctx));
+    // RoPE tables (internal/backend/simd/loader.go:1604-1612, ops_avx512.go:146-160), host f64.
+    const int half = c.head_dim / 2;
+    std::vector<float> cs_tab((size_t)max_ctx * half), sn_tab((size_t)max_ctx * half);
+    std::vector<double> inv(half);
+    for (int i = 0; i < half; i++) inv[i] = 1.0 / pow(c.rope_base > 0 ? c.rope_base : 10000.0, (double)(2 * i) / (double)c.head_dim);
+    for (int p = 0; p < max_ctx; p++)
+        for (int i = 0; i < half; i++) {
+            double ang = (double)p * inv[i];
+            cs_tab[(size_t)p * half + i] = (float)cos(ang);
+            sn_tab[(size_t)p * half + i] = (float)sin(ang);
+        }
+    CHECK(hipMalloc((void**)&m->rope_cos, sizeof(float) * cs_tab.size()));
+    CHECK(hipMalloc((void**)&m->rope_sin, sizeof(float) * sn_tab.size()));
+    CHECK(hipMemcpy(m->rope_cos, cs_tab.data(), sizeof(float) * cs_tab.size(), hipMemcpyHostToDevice));
+    CHECK(hipMemcpy(m->rope_sin, sn_tab.data(), sizeof(float) * sn_tab.size(), hipMemcpyHostToDevice));
+    CHECK(hipMemset(m->state, 0, sizeof(DecodeState)));
+    CHECK(hipMemset(m->prompt, 0, sizeof(int) * max_ctx));
+    CHECK(hipMemset(m->out_tokens, 0, sizeof(int) * max_ctx));
+    CHECK(hipMemset(m->cache_k, 0, sizeof(float) * kv_elems));
+    CHECK(hipMemset(m->cache_v, 0, sizeof(float) * kv_elems));
+    CHECK(hipDeviceSynchronize());
+#undef CHECK
+    *out = m;
+    return hipSuccess;
+}
+
+extern "C" int mantleHipModelConfig(const mantleHipModel* m, mantleHipQwen3Config* out) {
+    if (!m || !out) return hipErrorInvalidValue;
+    *out = m->cfg;
+    return hipSuccess;
+}
+
+extern "C" int mantleHipModelReset(mantleHipModel* m) {
+    if (!m) return hipErrorInvalidValue;
+    DecodeState st{};
+    m->pos = 0;
+    hipError_t e = hipMemcpyAsync(m->state, &st, sizeof st, hipMemcpyHostToDevice, m->stream);
+    if (e != hipSuccess) return e;
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelPos(const mantleHipModel* m, int* pos) {
+    if (!m || !pos) return hipErrorInvalidValue;
+    *pos = m->pos;
+    return hipSuccess;
+}
+
+// Writes prompt[pos..pos+n) and n_prompt = pos+n into device memory.
+static hipError_t upload_tokens(mantleHipModel* m, const int* toks, int n) {
+    for (int i = 0; i < n; i++)
+        if (toks[i] < 0 || toks[i] >= m->cfg.vocab) return hipErrorInvalidValue;  // token id out of range
+    if (m->pos + n > m->max_ctx) return hipErrorInvalidValue;
+    hipError_t e = hipMemcpyAsync(m->prompt + m->pos, toks, sizeof(int) * n, hipMemcpyHostToDevice, m->stream);
+    if (e != hipSuccess) return e;
+    static thread_local int np;
+    np = m->pos + n;
+    e = hipMemcpyAsync(&m->state->n_prompt, &np, sizeof(int), hipMemcpyHostToDevice, m->stream);
+    if (e != hipSuccess) return e;
+    return hipStreamSynchronize(m->stream);  // np is a host stack-lifetime value
+}
+
+extern "C" int mantleHipModelForwardTokenGreedy(mantleHipModel* m, int tok, int* next) {
+    if (!m || !next) return hipErrorInvalidValue;
+    hipError_t e = upload_tokens(m, &tok, 1);
+    if (e != hipSuccess) return e;
+    if ((e = run_steps(m, 1)) != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(next, &m->state->next_tok, sizeof(int), hipMemcpyDeviceToHost, m->stream)) != hipSuccess)
+        return e;
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelForwardToken(mantleHipModel* m, int tok, float* logits) {
+    if (!m || !logits) return hipErrorInvalidValue;
+    hipError_t e = upload_tokens(m, &tok, 1);
+    if (e != hipSuccess) return e;
+    if ((e = run_steps(m, 1)) != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(logits, m->logits, sizeof(float) * m->cfg.vocab, hipMemcpyDeviceToHost, m->stream)) !=
+        hipSuccess)
+        return e;
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelPrefillTokens(mantleHipModel* m, const int* toks, int n, int* next) {
+    if (!m || !toks || n <= 0) return hipErrorInvalidValue;
+    hipError_t e = upload_tokens(m, toks, n);
+    if (e != hipSuccess) return e;
+    if ((e = run_steps(m, n)) != hipSuccess) return e;
+    if (next) {
+        if ((e = hipMemcpyAsync(next, &m->state->next_tok, sizeof(int), hipMemcpyDeviceToHost, m->stream)) !=
+            hipSuccess)
+            return e;
+    }
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelGenerateGreedy(mantleHipModel* m, const int* prompt, int n_prompt, int n_gen,
+                                            int* out_tokens) {
+    if (!m || !prompt || n_prompt <= 0 || n_gen <= 0 || !out_tokens) return hipErrorInvalidValue;
+    const int p0 = m->pos;
+    if (p0 + n_prompt + n_gen - 1 > m->max_ctx) return hipErrorInvalidValue;
+    hipError_t e = upload_tokens(m, prompt, n_prompt);
+    if (e != hipSuccess) return e;
+    if ((e = run_steps(m, n_prompt + n_gen - 1)) != hipSuccess) return e;
+    e = hipMemcpyAsync(out_tokens, m->out_tokens + p0 + n_prompt - 1, sizeof(int) * n_gen, hipMemcpyDeviceToHost,
+                       m->stream);
+    if (e != hipSuccess) return e;
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelDecodeSteps(mantleHipModel* m, int steps) {
+    if (!m || steps <= 0) return hipErrorInvalidValue;
+    return run_steps(m, steps);
+}
+
+extern "C" int mantleHipModelSynchronize(mantleHipModel* m) {
+    if (!m) return hipErrorInvalidValue;
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelHidden(mantleHipModel* m, float* out) {
+    if (!m || !out) return hipErrorInvalidValue;
+    hipError_t e = hipMemcpyAsync(out, m->x, sizeof(float) * m->cfg.d_model, hipMemcpyDeviceToHost, m->stream);
+    if (e != hipSuccess) return e;
+    return hipStreamSynchronize(m->stream);
+}
+
+extern "C" int mantleHipModelSetUseGraph(mantleHipModel* m, int on) {
+    if (!m) return hipErrorInvalidValue;
+    m->use_graph = on != 0;
+    return hipSuccess;
+}

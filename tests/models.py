@@ -1,0 +1,48 @@
+"""Model fixtures shared by the GPU model tests, smoke() and bench.py's CPU leg."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+
+TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=128, ffn=512, vocab=3000,
+            rope_base=1e6, eps=1e-6, tie_embeddings=1)
+
+
+def pack(path: str, seed: int, cfg: dict) -> str:
+    from mantle_amd import mcf
+    if not os.path.exists(path):
+        tmp = path + ".part"
+        mcf.pack_synthetic_qwen3(tmp, seed, **cfg)
+        os.replace(tmp, path)
+    return path
+
+
+def oracle_model(path: str, cfg: dict, max_ctx: int, isa: int = 2):
+    """Oracle decoder over the same MCF payloads (views into the product's mmap)."""
+    from mantle_amd.mcf import DTYPE_F32, MCFFile
+    from oracle import oracle as o
+    f = MCFFile(path)
+
+    def tensors(name):
+        raw = f.raw(name)
+        return raw.view(np.float32) if f.tensors[name]["dtype"] == DTYPE_F32 else raw
+
+    m = o.Model(cfg, tensors, max_ctx, isa)
+    m._mcf = f  # keep the mapping alive
+    return m
+
+
+def splitmix64(x: int) -> int:
+    m = (1 << 64) - 1
+    z = (x + 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    return z ^ (z >> 31)
+
+
+def prompt(n: int, vocab: int, seed: int) -> list[int]:
+    """Uniform-random token ids (31 tokens, seed 1):
+    id_i = splitmix64(splitmix64(seed) + i) mod vocab."""
+    base = splitmix64(seed)
+    return [splitmix64((base + i) & ((1 << 64) - 1)) % vocab for i in range(n)]

@@ -1,0 +1,99 @@
+"""End-to-end greedy decode on the GPU vs the CPU oracle: identical tokens,
+bit-identical logits and residual stream."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from tests import models  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def tiny_path(tmp_models):
+    return models.pack(str(tmp_models / "tiny.mcf"), 0, models.TINY)
+
+
+@pytest.mark.parametrize("isa", ["avx512", "avx2"])
+def test_tiny_greedy_logits_bitexact(hip, tiny_path, isa):
+    import mantle_amd
+    isa_id = {"avx512": 2, "avx2": 1}[isa]
+    rt = mantle_amd.new_backend("hip").load_model(tiny_path, max_context=96, parity_isa=isa)
+    om = models.oracle_model(tiny_path, models.TINY, 96, isa_id)
+    try:
+        tok = 17
+        for step in range(40):
+            logits = rt.forward_token(tok)
+            nxt, want = om.forward_greedy(tok, want_logits=True)
+            np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+            np.testing.assert_array_equal(rt.hidden().view(np.uint32), om.hidden().view(np.uint32))
+            assert int(np.argmax(logits)) == nxt
+            tok = nxt
+        assert rt.pos == 40
+    finally:
+        rt.close()
+        om.close()
+
+
+def test_tiny_generate_graph_matches_eager(hip, tiny_path):
+    import mantle_amd
+    p = models.prompt(9, models.TINY["vocab"], 1)
+    rt = mantle_amd.new_backend().load_model(tiny_path, max_context=128)
+    om = models.oracle_model(tiny_path, models.TINY, 128)
+    try:
+        want = om.generate_greedy(p, 64)
+        got = rt.generate_greedy(p, 64)
+        assert got == want
+        rt.reset()
+        rt.set_use_graph(False)
+        assert rt.generate_greedy(p, 64) == want
+        rt.reset()
+        rt.set_use_graph(True)
+        nxt = rt.prefill_tokens(p)
+        assert nxt == want[0]
+        seq = [nxt]
+        for _ in range(7):
+            seq.append(rt.forward_token_greedy(seq[-1]))
+        assert seq == want[:8]
+    finally:
+        rt.close()
+        om.close()
+
+
+def test_context_limit_and_bad_token(hip, tiny_path):
+    import mantle_amd
+    rt = mantle_amd.new_backend().load_model(tiny_path, max_context=4)
+    try:
+        with pytest.raises(mantle_amd.HipError):
+            rt.forward_token_greedy(models.TINY["vocab"])
+        rt.prefill_tokens([1, 2, 3, 4])
+        with pytest.raises(mantle_amd.HipError):
+            rt.forward_token_greedy(1)
+        rt.reset()
+        assert rt.pos == 0
+        rt.forward_token_greedy(1)
+    finally:
+        rt.close()
+
+
+def test_qwen3_0_6b_first_64_tokens(hip, tmp_models):
+    """Qwen3-0.6B shape, weights seed 0, 31-token prompt seed 1:
+    the first 64 greedy tokens equal the CPU oracle's."""
+    import mantle_amd
+    from mantle_amd.mcf import QWEN3_0_6B
+    from oracle import oracle as o
+    path = models.pack(str(tmp_models / "qwen3_0_6b_k4.mcf"), 0, QWEN3_0_6B)
+    p = models.prompt(31, QWEN3_0_6B["vocab"], 1)
+    rt = mantle_amd.new_backend().load_model(path, max_context=128)
+    try:
+        got = rt.generate_greedy(p, 64)
+    finally:
+        rt.close()
+    o.set_threads(16)
+    om = models.oracle_model(path, QWEN3_0_6B, 128)
+    try:
+        want = om.generate_greedy(p, 64)
+    finally:
+        om.close()
+    assert got == want

@@ -1,0 +1,135 @@
+"""GPU parity of the norm / RoPE / softmax / SiLU / argmax / attention kernels
+against the CPU oracle (bit-exact: they reproduce Mantle's CPU lane orders)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from tests import gpu_util as g  # noqa: E402
+
+ISAS = [0, 1, 2]
+
+
+@pytest.fixture(autouse=True)
+def _reset_isa(hip):
+    yield
+    g.call("mantleHipSetParityISA", 2)
+
+
+@pytest.mark.parametrize("isa", ISAS)
+@pytest.mark.parametrize("n", [7, 128, 1000, 1024, 2048])
+def test_rmsnorm_bitexact(hip, oracle, isa, n):
+    rng = np.random.default_rng(n + isa)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    g.call("mantleHipSetParityISA", isa)
+    out = g.empty(n)
+    g.call("mantleHipRMSNormF32", g.ptr(out), g.ptr(g.keep(x)), g.ptr(g.keep(w)), ctypes.c_float(1e-6), n, g.stream())
+    g.assert_bitexact(g.host(out), oracle.rmsnorm(isa, x, w, 1e-6), f"rmsnorm isa={isa} n={n}")
+
+
+@pytest.mark.parametrize("isa", ISAS)
+def test_rmsnorm_batched_bitexact(hip, oracle, isa):
+    hd, nh = 128, 16
+    rng = np.random.default_rng(isa)
+    x = rng.standard_normal(hd * nh).astype(np.float32)
+    w = rng.standard_normal(hd).astype(np.float32)
+    g.call("mantleHipSetParityISA", isa)
+    out = g.empty(hd * nh)
+    g.call("mantleHipRMSNormBatchedF32", g.ptr(out), g.ptr(g.keep(x)), g.ptr(g.keep(w)), ctypes.c_float(1e-6), hd, nh,
+           g.stream())
+    want = np.concatenate([oracle.rmsnorm(isa, x[h * hd:(h + 1) * hd], w, 1e-6) for h in range(nh)])
+    g.assert_bitexact(g.host(out), want, "rmsnorm batched")
+
+
+@pytest.mark.parametrize("pos", [0, 1, 31, 4095, 16383])
+def test_rope_table_bitexact(hip, oracle, pos):
+    hd, nh = 128, 24
+    x = np.random.default_rng(pos).standard_normal(hd * nh).astype(np.float32)
+    c, s = oracle.rope_tables(1e6, hd, pos)
+    xd = g.dev(x)
+    g.call("mantleHipApplyRoPEInplaceTableF32", g.ptr(xd), g.ptr(g.keep(c)), g.ptr(g.keep(s)), hd, hd // 2, nh,
+           g.stream())
+    g.assert_bitexact(g.host(xd), oracle.apply_rope(x, nh, hd, c, s), "rope")
+
+
+def test_rope_f64_close(hip, oracle):
+    """Device f64 cos/sin path: within 1 ulp-level tolerance of the host tables."""
+    hd, nh, pos = 128, 16, 777
+    x = np.random.default_rng(1).standard_normal(hd * nh).astype(np.float32)
+    inv = np.array([1.0 / (1e6 ** (2 * i / hd)) for i in range(hd // 2)], dtype=np.float64)
+    xd = g.dev(x)
+    g.call("mantleHipApplyRoPEInplaceF32", g.ptr(xd), g.ptr(g.keep(inv)), pos, ctypes.c_float(1.0), hd, hd // 2, nh,
+           g.stream())
+    c, s = oracle.rope_tables(1e6, hd, pos)
+    np.testing.assert_allclose(g.host(xd), oracle.apply_rope(x, nh, hd, c, s), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("cols", [1, 5, 160, 4097])
+def test_softmax_bitexact(hip, oracle, cols):
+    rows = 3
+    x = (np.random.default_rng(cols).standard_normal(rows * cols) * 4).astype(np.float32)
+    xd = g.dev(x)
+    g.call("mantleHipSoftmaxRowsF32", g.ptr(xd), rows, cols, g.stream())
+    want = np.concatenate([oracle.softmax(x[r * cols:(r + 1) * cols]) for r in range(rows)])
+    g.assert_bitexact(g.host(xd), want, "softmax")
+
+
+@pytest.mark.parametrize("n", [3072, 3075])
+def test_silu_mul_bitexact(hip, oracle, n):
+    rng = np.random.default_rng(n)
+    gate = (rng.standard_normal(n) * 5).astype(np.float32)
+    up = rng.standard_normal(n).astype(np.float32)
+    out = g.empty(n)
+    g.call("mantleHipSiluMulF32", g.ptr(g.keep(gate)), g.ptr(g.keep(up)), g.ptr(out), n, g.stream())
+    g.assert_bitexact(g.host(out), oracle.silu_mul(gate, up), "silu*up")
+
+
+def test_argmax_first_max_wins(hip):
+    x = np.zeros(151936, dtype=np.float32)
+    x[[5, 70000, 151935]] = 3.0
+    x[4] = -1.0
+    out = g.empty(1, torch.int32)
+    g.call("mantleHipArgMaxF32", g.ptr(g.keep(x)), len(x), g.ptr(out), g.stream())
+    assert int(g.host(out)[0]) == 5
+    x = -np.abs(np.random.default_rng(0).standard_normal(1000)).astype(np.float32)
+    g.call("mantleHipArgMaxF32", g.ptr(g.keep(x)), len(x), g.ptr(out), g.stream())
+    assert int(g.host(out)[0]) == int(np.argmax(x))
+
+
+def test_add_vectors(hip):
+    a = np.arange(1000, dtype=np.float32)
+    b = np.full(1000, 0.5, dtype=np.float32)
+    ad = g.dev(a)
+    g.call("mantleHipAddVectorsF32", g.ptr(ad), g.ptr(g.keep(b)), 1000, g.stream())
+    np.testing.assert_array_equal(g.host(ad), a + b)
+
+
+def _fill(n, scale):  # fillTestData (internal/backend/simd/attn_test.go:240-244)
+    return np.array([scale * np.float32((i % 29) - 14) for i in range(n)], dtype=np.float32)
+
+
+@pytest.mark.parametrize("isa", ISAS)
+@pytest.mark.parametrize("n_head,kv_heads,head_dim,pos", [(4, 2, 8, 5), (16, 8, 128, 0), (16, 8, 128, 130),
+                                                         (32, 8, 128, 1000)])
+def test_attention_bitexact(hip, oracle, isa, n_head, kv_heads, head_dim, pos):
+    kv = kv_heads * head_dim
+    if head_dim == 8:
+        q, ck, cv = _fill(n_head * head_dim, 0.1), _fill((pos + 1) * kv, 0.2), _fill((pos + 1) * kv, 0.3)
+    else:
+        rng = np.random.default_rng(pos)
+        q = rng.standard_normal(n_head * head_dim).astype(np.float32)
+        ck = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+        cv = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(head_dim))
+    g.call("mantleHipSetParityISA", isa)
+    out = g.empty(n_head * head_dim)
+    scratch = g.empty(n_head * (pos + 1))
+    g.call("mantleHipAttentionInnerF32Cache", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)), g.ptr(out),
+           g.ptr(scratch), pos, 0, kv, head_dim, n_head, kv_heads, pos + 1, ctypes.c_float(scale), g.stream())
+    want = oracle.attn_heads(isa, q, ck, cv, pos, kv, head_dim, n_head, kv_heads, float(scale))
+    g.assert_bitexact(g.host(out), want, "attention")

@@ -1,0 +1,314 @@
+"""Pins the CPU oracle: known-answer tests from Mantle's own test files,
+closed forms that a plausible slip (dropped term, wrong lane order, wrong
+index, wrong rounding) would break, and float64 references within tolerance."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+
+
+# ---------------------------------------------------------------- fp16 ----
+@pytest.mark.parametrize("v,bits", [(1.0, 0x3C00), (0.04, 0x291E), (0.1, 0x2E66), (-0.1, 0xAE66), (65504.0, 0x7BFF),
+                                    (65536.0, 0x7C00), (1e-8, 0x0000), (-1e-8, 0x8000), (6.1035156e-05, 0x0400),
+                                    (float("inf"), 0x7C00), (float("nan"), 0x7E00)])
+def test_f32_to_f16_truncating_kat(v, bits):
+    """Float32ToFloat16 (internal/backend/simd/float16.go:7-46) truncates the
+    mantissa and flushes f16-subnormal results to zero; 0.04 -> 0x291E is the
+    scale TestRowToQuant uses (internal/backend/simd/matvec_quant_test.go:9-29)."""
+    assert o.f32_to_f16(v) == bits
+
+
+def test_f32_to_f16_truncates_never_rounds_up():
+    rng = np.random.default_rng(0)
+    v = (rng.standard_normal(20000) * 10).astype(np.float32)
+    v = v[np.abs(v) > 1e-4]
+    t = np.array([o.f32_to_f16(float(x)) for x in v], dtype=np.uint16).view(np.float16).astype(np.float32)
+    assert np.all(np.abs(t) <= np.abs(v))
+    assert np.all(np.abs(v - t) < np.abs(v) * 2.0 ** -10)
+
+
+@pytest.mark.parametrize("bits,v", [(0x3C00, 1.0), (0x0001, 0.0), (0x03FF, 0.0), (0x8001, -0.0), (0x0400, 2.0 ** -14),
+                                    (0x7BFF, 65504.0), (0x7C00, float("inf"))])
+def test_f16_to_f32_ftz_kat(bits, v):
+    """Float16ToFloat32 (internal/backend/core/float16.go:42-64): subnormals -> 0."""
+    assert o.f16_to_f32(bits) == v
+
+
+# -------------------------------------------------------------- layout ----
+@pytest.mark.parametrize("rows,cols,size", [(3072, 1024, 1_695_744), (1024, 3072, 1_695_744), (2048, 1024, 1_130_496),
+                                            (1024, 1024, 565_248), (1024, 2048, 1_130_496),
+                                            (151936, 1024, 83_868_672), (2, 96, 64 + 64 + 96), (1, 1, 64 + 64 + 16)])
+def test_payload_size(rows, cols, size):
+    """QuantPayloadSize (pkg/mcf/quant_payload.go:15-113) at the BASELINE shapes."""
+    assert o.payload_size(rows, cols) == size
+
+
+# ------------------------------------------------------------ quantizer ----
+def test_quantize_k4_kat_single_block():
+    """One block, values k*0.1: block scale 0.7/7 = 0.1 = super; the stored super
+    is the TRUNCATED f16 0x2E66, u6 = 32, q = k; dequant w = f16(0x2E66) * k."""
+    k = np.array([(i % 15) - 7 for i in range(32)], dtype=np.float32)
+    w = (k * np.float32(0.1)).astype(np.float32).reshape(1, 32)
+    p = o.quantize_k4(w)
+    assert int(p[0]) | (int(p[1]) << 8) == 0x2E66
+    assert p[64] == 32
+    nib = p[128:144]
+    q = np.empty(32, dtype=np.int8)
+    q[0::2] = (nib & 0xF).astype(np.int8)
+    q[1::2] = (nib >> 4).astype(np.int8)
+    q = np.where(q > 7, q - 16, q)
+    np.testing.assert_array_equal(q, k.astype(np.int8))
+    np.testing.assert_array_equal(o.dequant_k4(p, 1, 32)[0], (k * np.float32(o.f16_to_f32(0x2E66))).astype(np.float32))
+
+
+def test_quantize_k4_kat_sub_scale_uses_unrounded_super():
+    """Second block with max 0.35: s_b = 0.05, ratio to the fp32 super 0.1 is
+    0.5 -> u6 = 16 and q = round(v / (0.1 * 16/32)) with the UNROUNDED super."""
+    a = np.zeros(64, dtype=np.float32)
+    a[0] = 0.7
+    a[32:64] = np.array([((i % 15) - 7) * 0.05 for i in range(32)], dtype=np.float32)
+    p = o.quantize_k4(a.reshape(1, 64))
+    assert p[64] == 32 and p[65] == 16
+    q = o.dequant_k4(p, 1, 64)[0, 32:] / np.float32(o.f16_to_f32(0x2E66) * 0.5)
+    np.testing.assert_array_equal(np.round(q), [((i % 15) - 7) for i in range(32)])
+
+
+def test_quantize_k4_error_bound_and_ranges():
+    rng = np.random.default_rng(1)
+    for rows, cols in [(7, 300), (16, 1024), (3, 33)]:
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        p = o.quantize_k4(w)
+        bpr = (cols + 31) // 32
+        spr = (bpr + 7) // 8
+        sub_off = (rows * spr * 2 + 63) & ~63
+        sub = p[sub_off:sub_off + rows * bpr]
+        assert sub.max() <= 63 and sub.min() >= 1
+        d = o.dequant_k4(p, rows, cols)
+        s = np.repeat(o.block_scales(p, rows, cols), 32, axis=1)[:, :cols]
+        # |w - q*s_unrounded| <= s/2 and the truncated super shifts q*s by < 7*s*2^-10
+        assert np.all(np.abs(d - w) <= s * (0.5 + 8 * 2.0 ** -10) * 1.001 + 1e-12)
+
+
+def test_quantize_k4_zero_and_padding():
+    p = o.quantize_k4(np.zeros((2, 40), dtype=np.float32))
+    assert not p.any()
+    w = np.ones((1, 40), dtype=np.float32)
+    d = o.dequant_k4(o.quantize_k4(w), 1, 40)
+    np.testing.assert_allclose(d, w, rtol=2e-3)
+
+
+# -------------------------------------------------------- int8 activations ----
+def test_quantize_vec_kat():
+    """quantizeVecBlocksInto (internal/backend/simd/matvec_quant.go:746-797):
+    maxAbs 127 -> scale 1, ties round away from zero, zero block -> scale 0."""
+    x = np.zeros(96, dtype=np.float32)
+    x[0:8] = [127.0, 2.5, -2.5, 0.5, -0.5, 126.5, -126.49, 3.0]
+    x[64:96] = np.float32(-7.0)
+    q, s = o.quantize_vec(x)
+    np.testing.assert_array_equal(s, [1.0, 0.0, np.float32(7.0) / np.float32(127.0)])
+    np.testing.assert_array_equal(q[0:8], [127, 3, -3, 1, -1, 127, -126, 3])
+    assert not q[32:64].any()
+    np.testing.assert_array_equal(q[64:96], -127)
+
+
+# -------------------------------------------------------------- GEMV ----
+def _kat_payload(rows, cols):
+    """TestQuantMatVecK4F32 fixture (internal/backend/cuda/native/runtime_test.go:425-470):
+    super = fp16(1.0), u6 = 32, q = (i+b)%13-6."""
+    bpr = (cols + 31) // 32
+    q = np.array([[(i + b) % 13 - 6 for i in range(32)] for b in range(rows * bpr)], dtype=np.int8)
+    p = np.zeros(o.payload_size(rows, cols), dtype=np.uint8)
+    spr = (bpr + 7) // 8
+    p[:rows * spr * 2].view(np.uint16)[:] = 0x3C00
+    sub_off = (rows * spr * 2 + 63) & ~63
+    data_off = (sub_off + rows * bpr + 63) & ~63
+    p[sub_off:sub_off + rows * bpr] = 32
+    nib = (q.astype(np.int16) & 0xF).astype(np.uint8)
+    p[data_off:data_off + rows * bpr * 16] = (nib[:, 0::2] | (nib[:, 1::2] << 4)).reshape(-1)
+    return p, q.reshape(rows, bpr * 32)[:, :cols]
+
+
+def test_w4a32_kat():
+    rows, cols = 2, 96
+    p, q = _kat_payload(rows, cols)
+    x = np.array([((i % 17) - 8) * 0.125 for i in range(cols)], dtype=np.float32)
+    want = q.astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_array_equal(o.matvec_w4a32(p, rows, cols, x), want.astype(np.float32))
+    np.testing.assert_array_equal(o.dequant_k4(p, rows, cols), q.astype(np.float32))
+
+
+def test_w4a8_closed_form_integer_activations():
+    """Integer activations whose block max is 127 quantise exactly (scale 1), so
+    the W4A8 result is the exact integer matmul."""
+    rows, cols = 5, 256
+    p, q = _kat_payload(rows, cols)
+    rng = np.random.default_rng(2)
+    x = rng.integers(-127, 128, size=cols).astype(np.float32)
+    x[0::32] = 127.0
+    want = (q.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
+    np.testing.assert_array_equal(o.matvec_w4a8(p, rows, cols, x), want)
+
+
+def test_w4a8_numpy_emulation():
+    """Independent numpy formulation: int64 block dots of the decoded nibbles
+    with the int8 activations, term = f32(dot) * f32(s_w*s_x), blocks added in
+    order in float32."""
+    rng = np.random.default_rng(3)
+    rows, cols = 9, 200
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    p = o.quantize_k4(w)
+    bpr = (cols + 31) // 32
+    spr = (bpr + 7) // 8
+    sub_off = (rows * spr * 2 + 63) & ~63
+    data_off = (sub_off + rows * bpr + 63) & ~63
+    nib = p[data_off:data_off + rows * bpr * 16].reshape(rows, bpr, 16)
+    qw = np.empty((rows, bpr, 32), dtype=np.int64)
+    qw[:, :, 0::2] = nib & 0xF
+    qw[:, :, 1::2] = nib >> 4
+    qw = np.where(qw > 7, qw - 16, qw)
+    sup = p[:rows * spr * 2].view(np.uint16).reshape(rows, spr).astype(np.uint32)
+    supf = np.where((sup & 0x7C00) == 0, 0, ((sup & 0x8000) << 16) | (((sup >> 10) & 0x1F) + 112) << 23
+                    | ((sup & 0x3FF) << 13)).astype(np.uint32).view(np.float32)
+    u6 = (p[sub_off:sub_off + rows * bpr].reshape(rows, bpr) & 0x3F).astype(np.float32)
+    sw = (np.repeat(supf, 8, axis=1)[:, :bpr] * (u6 / np.float32(32))).astype(np.float32)
+    qx, sx = o.quantize_vec(x)
+    dots = np.einsum("rbi,bi->rb", qw, qx.reshape(bpr, 32).astype(np.int64))
+    terms = dots.astype(np.float32) * (sw * sx[None, :]).astype(np.float32)
+    y = np.zeros(rows, dtype=np.float32)
+    for b in range(bpr):
+        y = (y + terms[:, b]).astype(np.float32)
+    np.testing.assert_array_equal(o.matvec_w4a8(p, rows, cols, x), y)
+
+
+# ------------------------------------------------------- dot / rmsnorm ----
+def test_dot_lane_order_kat():
+    """Mantle's reduction orders differ and the bits show it:
+    AVX-512 (ops_avx512.go:27-90) keeps 4 accumulators x 16 lanes over 64-wide
+    steps, AVX2 (ops_avx2.go:25-51) 2 x 8 lanes over 16-wide steps, scalar adds in order."""
+    b = np.ones(128, dtype=np.float32)
+    a = np.zeros(128, dtype=np.float32)
+    a[0], a[1], a[64] = 1e8, 1.0, -1e8         # lane 0 of acc0 in both SIMD orders
+    assert [o.dot(i, a, b) for i in (0, 1, 2)] == [0.0, 1.0, 1.0]
+    a = np.zeros(128, dtype=np.float32)
+    a[0], a[1], a[32] = 1e8, 1.0, -1e8         # acc2 lane 0 for AVX-512, acc0 lane 0 for AVX2
+    assert [o.dot(i, a, b) for i in (0, 1, 2)] == [0.0, 1.0, 0.0]
+
+
+@pytest.mark.parametrize("isa", [0, 1, 2])
+@pytest.mark.parametrize("n", [5, 128, 1000])
+def test_dot_vs_float64(isa, n):
+    rng = np.random.default_rng(n)
+    a, b = rng.standard_normal((2, n)).astype(np.float32)
+    assert abs(o.dot(isa, a, b) - float(a.astype(np.float64) @ b.astype(np.float64))) < 1e-4 * math.sqrt(n)
+
+
+@pytest.mark.parametrize("isa", [0, 1, 2])
+def test_rmsnorm_kat_and_float64(isa):
+    x = np.full(1024, 2.0, dtype=np.float32)
+    w = np.full(1024, 0.5, dtype=np.float32)
+    np.testing.assert_array_equal(o.rmsnorm(isa, x, w, 0.0), np.full(1024, 0.5, dtype=np.float32))
+    rng = np.random.default_rng(isa)
+    for n in (7, 128, 1024, 3000):
+        x = rng.standard_normal(n).astype(np.float32) * 3
+        w = rng.standard_normal(n).astype(np.float32)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * w
+        np.testing.assert_allclose(o.rmsnorm(isa, x, w, 1e-6), want, rtol=2e-6, atol=2e-6)
+
+
+# -------------------------------------------------- exp / softmax / silu ----
+def test_fast_exp_kat_and_accuracy():
+    assert o.fast_exp(0.0) == 1.0
+    assert o.fast_exp(89.0) == np.float32(3.4028235e38)
+    assert o.fast_exp(-89.0) == 0.0
+    for x in np.linspace(-20, 10, 4001, dtype=np.float32):
+        assert abs(o.fast_exp(float(x)) / math.exp(float(x)) - 1) < 1e-3
+        assert abs(o.fast_exp_vec(float(x)) / math.exp(float(x)) - 1) < 1e-3
+
+
+def test_sigmoid_silu_kat():
+    """TestSigmoidValues / TestSiluMatchesDefinition (internal/backend/simd/ops_test.go:5-33):
+    both the 8-wide (fastSiluVec) and the scalar-tail (Silu) paths."""
+    for v, sig in [(0.0, 0.5), (2.0, 0.8807971), (-2.0, 0.1192029)]:
+        assert abs(o.fast_silu_vec(v) - v * sig) <= 1e-5 * max(1.0, abs(v))
+        tail = o.silu_mul(np.full(9, v, dtype=np.float32), np.ones(9, dtype=np.float32))
+        assert abs(tail[8] - v * sig) <= 1e-5 * max(1.0, abs(v))
+    g = np.array([-4, -1, 0, 1, 4, -4, -1, 0, 1], dtype=np.float32)
+    got = o.silu_mul(g, np.ones_like(g))
+    np.testing.assert_allclose(got, g / (1 + np.exp(-g.astype(np.float64))), atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [1, 6, 160, 5000])
+def test_softmax_vs_float64(n):
+    """softmaxRef (internal/backend/cuda/native/runtime_test.go:821-845) within 1e-5."""
+    x = (np.random.default_rng(n).standard_normal(n) * 4).astype(np.float32)
+    e = np.exp(x.astype(np.float64) - x.max())
+    np.testing.assert_allclose(o.softmax(x), e / e.sum(), atol=1e-5, rtol=1e-3)
+
+
+# -------------------------------------------------------------- RoPE ----
+def test_rope_identity_at_pos0_and_float64():
+    hd, nh = 128, 3
+    x = np.random.default_rng(0).standard_normal(hd * nh).astype(np.float32)
+    c, s = o.rope_tables(1e6, hd, 0)
+    np.testing.assert_array_equal(o.apply_rope(x, nh, hd, c, s), x)
+    pos = 1234
+    c, s = o.rope_tables(1e6, hd, pos)
+    got = o.apply_rope(x, nh, hd, c, s).reshape(nh, hd)
+    inv = 1.0 / (1e6 ** (np.arange(hd // 2) * 2.0 / hd))
+    ang = pos * inv
+    xr = x.reshape(nh, hd).astype(np.float64)
+    lo, hi = xr[:, :hd // 2], xr[:, hd // 2:]
+    want = np.concatenate([lo * np.cos(ang) - hi * np.sin(ang), lo * np.sin(ang) + hi * np.cos(ang)], axis=1)
+    np.testing.assert_allclose(got, want, atol=1e-5)
+
+
+# --------------------------------------------------------- attention ----
+def _ref_attention(q, ck, cv, pos, kv_stride, hd, nh, kvh, scale, start=0):
+    """referenceAttention (internal/backend/simd/attn_test.go:177-236) in float64."""
+    out = np.zeros(nh * hd)
+    for h in range(nh):
+        g = h * kvh // nh
+        qh = q[h * hd:(h + 1) * hd].astype(np.float64)
+        ks = np.array([ck[t * kv_stride + g * hd: t * kv_stride + (g + 1) * hd] for t in range(start, pos + 1)])
+        vs = np.array([cv[t * kv_stride + g * hd: t * kv_stride + (g + 1) * hd] for t in range(start, pos + 1)])
+        sc = ks.astype(np.float64) @ qh * scale
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        out[h * hd:(h + 1) * hd] = p @ vs
+    return out
+
+
+def _fill(n, scale):  # fillTestData (internal/backend/simd/attn_test.go:240-244)
+    return np.array([scale * np.float32((i % 29) - 14) for i in range(n)], dtype=np.float32)
+
+
+@pytest.mark.parametrize("isa", [0, 1, 2])
+def test_attention_kat_full(isa):
+    """TestRunAttnHeadsMatchesReferenceFull (internal/backend/simd/attn_test.go:10-46)."""
+    nh, kvh, hd, pos = 4, 2, 8, 5
+    kv = kvh * hd
+    q, ck, cv = _fill(nh * hd, 0.1), _fill((pos + 1) * kv, 0.2), _fill((pos + 1) * kv, 0.3)
+    scale = np.float32(1.0 / math.sqrt(hd))
+    got = o.attn_heads(isa, q, ck, cv, pos, kv, hd, nh, kvh, float(scale))
+    np.testing.assert_allclose(got, _ref_attention(q, ck, cv, pos, kv, hd, nh, kvh, float(scale)), atol=1e-5)
+
+
+def test_attention_kat_sliding_window():
+    """TestRunAttnHeadsMatchesReferenceSlidingWindow (internal/backend/simd/attn_test.go:48-86)."""
+    nh, kvh, hd, pos, window = 6, 3, 8, 9, 4
+    start = pos - window + 1
+    kv = kvh * hd
+    q, ck, cv = _fill(nh * hd, 0.05), _fill((pos + 1) * kv, 0.07), _fill((pos + 1) * kv, 0.09)
+    scale = float(np.float32(1.0 / math.sqrt(hd)))
+    got = o.attn_heads(2, q, ck, cv, pos, kv, hd, nh, kvh, scale, start)
+    np.testing.assert_allclose(got, _ref_attention(q, ck, cv, pos, kv, hd, nh, kvh, scale, start), atol=1e-5)
+
+
+def test_argmax_first_max():
+    x = np.array([1, 3, 3, -1, 3], dtype=np.float32)
+    assert o.argmax(x) == 1
+    assert o.argmax(np.array([-5.0], dtype=np.float32)) == 0
