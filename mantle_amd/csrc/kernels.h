@@ -47,6 +47,12 @@ struct DecodeState {
 hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, int cols,
                                const int8_t* qx, const float* xs, int batch, GemvEpi epi,
                                unsigned long long* argmax_key, hipStream_t stream);
+// Same arithmetic, but each workgroup quantises the fp32 activation x itself
+// (after Mantle's RMSNorm with norm_w when non-null): no separate quantiser
+// launch, and the weight loads are issued before the prologue runs.
+hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int nmat, int cols, const float* x,
+                                     const float* norm_w, float eps, int isa, int batch, GemvEpi epi,
+                                     unsigned long long* argmax_key, hipStream_t stream);
 // y = W * x with fp32 x (W4A32; tolerance-checked, not bit-exact).
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch,
                                 hipStream_t stream);

@@ -17,11 +17,29 @@
 //
 // Compiled with -ffp-contract=off: every fused multiply-add is explicit.
 #include <hip/hip_fp16.h>
+#include <stdlib.h>
 
 #include "device_common.h"
 #include "kernels.h"
 
 namespace mantle {
+
+// Phase timestamps of workgroup 0 (100 MHz wall clock) for latency studies;
+// compiled only into a -DMANTLE_PHASE_TRACE build, never into the product.
+#ifdef MANTLE_PHASE_TRACE
+__device__ unsigned long long g_phase[8192 * 8];
+__device__ unsigned int g_phase_n;
+#define PHASE_SLOT()                                                            \
+    unsigned phase_slot_ = 0;                                                   \
+    if (blockIdx.x == 0 && threadIdx.x == 0) phase_slot_ = atomicAdd(&g_phase_n, 1u) & 8191u
+#define PHASE(k)                                                                \
+    do {                                                                        \
+        if (blockIdx.x == 0 && threadIdx.x == 0) g_phase[phase_slot_ * 8 + (k)] = wall_clock64(); \
+    } while (0)
+#else
+#define PHASE_SLOT() (void)0
+#define PHASE(k) (void)0
+#endif
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -36,15 +54,25 @@ __device__ __forceinline__ int qx_perm(int e) { return ((e & 1) << 4) | ((e >> 3
 // Parity reductions (Mantle's archsimd lane orders)
 
 // Sum of squares exactly as rmsNormAVX512 / rmsNormSIMD / rmsNormScalar do it
-// (internal/backend/simd/ops_avx512.go:92-112, ops_avx2.go:54-77, ops.go:70-76).
-// Executed by a whole workgroup; red needs 17 floats of LDS.
+// (internal/backend/simd/ops_avx512.go:92-112, ops_avx2.go:54-77, ops.go:70-76):
+// lane l accumulates fma(x, x, acc) over i = l, l+L, ... (L = 16 / 8), then the L
+// partial sums are added left to right and the scalar tail follows.  Each lane
+// loads 8 operands ahead of its dependent FMA chain.  Whole workgroup; red >= 17 floats.
 __device__ float wg_sumsq_parity(const float* src, int n, int isa, float* red) {
     const int lanes = isa == kIsaAvx512 ? 16 : (isa == kIsaAvx2 ? 8 : 0);
     const int nfull = lanes ? (n / lanes) * lanes : 0;
     const int tid = threadIdx.x;
     if (lanes && tid < lanes) {
         float acc = 0.0f;
-        for (int i = tid; i < nfull; i += lanes) acc = __builtin_fmaf(src[i], src[i], acc);
+        int i = tid;
+        for (; i + 7 * lanes < nfull; i += 8 * lanes) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = src[i + k * lanes];
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc = __builtin_fmaf(v[k], v[k], acc);
+        }
+        for (; i < nfull; i += lanes) acc = __builtin_fmaf(src[i], src[i], acc);
         red[tid] = acc;
     }
     __syncthreads();
@@ -54,13 +82,36 @@ __device__ float wg_sumsq_parity(const float* src, int n, int isa, float* red) {
             sum = red[0];
             for (int l = 1; l < lanes; l++) sum += red[l];
         }
-        for (int i = nfull; i < n; i++) sum += src[i] * src[i];
+        int i = nfull;
+        for (; i + 8 <= n; i += 8) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = src[i + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) sum += v[k] * v[k];
+        }
+        for (; i < n; i++) sum += src[i] * src[i];
         red[16] = sum;
     }
     __syncthreads();
     float r = red[16];
     __syncthreads();
     return r;
+}
+
+// sum = ((t[0] + t[s]) + t[2s]) + ... in order, loads issued 8 ahead of the adds.
+__device__ __forceinline__ float ordered_sum(const float* t, int stride, int n) {
+    float sum = 0.0f;
+    int b = 0;
+    for (; b + 16 <= n; b += 16) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = t[(b + k) * stride];
+#pragma unroll
+        for (int k = 0; k < 16; k++) sum += v[k];
+    }
+    for (; b < n; b++) sum += t[b * stride];
+    return sum;
 }
 
 // Dot exactly as dotAVX512 / dotSIMD / dotScalar (internal/backend/simd/ops_avx512.go:27-90,
@@ -130,61 +181,165 @@ __device__ float dot_parity(const float* a, const float* b, int n, int isa) {
 // ---------------------------------------------------------------------------
 // Activation quantiser (+ optional RMSNorm), one workgroup per row.
 
+// Load 16 values (half h of block b) of x, and of the gains when weight != null.
+__device__ __forceinline__ void load_half16(const float* __restrict__ x, const float* __restrict__ weight, int n,
+                                            int base, bool vec4, float (&v)[16], float (&g)[16]) {
+    if (vec4 && base + 16 <= n) {
+        const float4* x4 = reinterpret_cast<const float4*>(x + base);
+        const float4* w4 = reinterpret_cast<const float4*>(weight + base);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 t = x4[k];
+            v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
+            if (weight) {
+                const float4 u = w4[k];
+                g[4 * k] = u.x; g[4 * k + 1] = u.y; g[4 * k + 2] = u.z; g[4 * k + 3] = u.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int idx = base + k;
+            v[k] = idx < n ? x[idx] : 0.0f;
+            if (weight) g[k] = idx < n ? weight[idx] : 0.0f;
+        }
+    }
+}
+
+// Stage one activation vector as Mantle's W4A8 operand: optional RMSNorm
+// (weight != null), then per-32-block int8 quantisation (quantizeVecBlocksInto,
+// internal/backend/simd/matvec_quant.go:746-797).  Two adjacent lanes own one
+// 32-element block (16 values each, loaded once up front); the block max is
+// one lane-pair exchange (max is exact in any order).  The RMS sum of squares
+// runs on 16 / 8 lanes in Mantle's lane-striped order over an LDS copy (vals,
+// ceil32(n) floats, only touched with weight).  Whole workgroup; red >= 17
+// floats; q_out / s_out may be LDS or global (q_out in the even/odd permuted
+// layout: dword j of the first 16 bytes holds elements 8j+0,2,4,6, of the
+// second 16 bytes elements 8j+1,3,5,7).
+// First-trip loads of wg_quantize_vec (this lane's 16 values and gains), so a
+// caller can put them in flight ahead of its own, larger loads.
+__device__ __forceinline__ void wg_quantize_vec_load(const float* __restrict__ x, const float* __restrict__ weight,
+                                                     int n, float (&v)[16], float (&g)[16]) {
+    const int halves = ((n + 31) >> 5) * 2;
+    const bool vec4 = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0;
+    if ((int)threadIdx.x < halves) load_half16(x, weight, n, threadIdx.x * 16, vec4, v, g);
+}
+
+template <int NT = kThreads>
+__device__ void wg_quantize_vec_pre(const float* __restrict__ x, const float* __restrict__ weight, float eps, int n,
+                                    int isa, float* vals, float* red, int8_t* q_out, float* s_out, float* norm_out,
+                                    float (&v)[16], float (&g)[16]) {
+    const int tid = threadIdx.x;
+    const int halves = ((n + 31) >> 5) * 2;
+    const bool vec4 = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0;
+    float scale = 1.0f;
+    if (weight) {
+        if (halves <= NT) {
+            if (tid < halves) {
+                float4* d4 = reinterpret_cast<float4*>(vals + tid * 16);
+#pragma unroll
+                for (int k = 0; k < 4; k++) d4[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+            }
+        } else {
+            for (int i = tid; i < halves * 16; i += NT) vals[i] = i < n ? x[i] : 0.0f;
+        }
+        __syncthreads();
+        const int lanes = isa == kIsaAvx512 ? 16 : (isa == kIsaAvx2 ? 8 : 0);
+        const int nfull = lanes ? (n / lanes) * lanes : 0;
+        if (lanes && tid < lanes) {
+            float acc = 0.0f;
+            int i = tid;
+            for (; i + 15 * lanes < nfull; i += 16 * lanes) {
+                float t[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) t[k] = vals[i + k * lanes];
+#pragma unroll
+                for (int k = 0; k < 16; k++) acc = __builtin_fmaf(t[k], t[k], acc);
+            }
+            for (; i < nfull; i += lanes) acc = __builtin_fmaf(vals[i], vals[i], acc);
+            red[tid] = acc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            if (lanes) {
+                sum = red[0];
+                for (int l = 1; l < lanes; l++) sum += red[l];
+            }
+            for (int i = nfull; i < n; i++) sum += vals[i] * vals[i];
+            red[16] = rms_scale(sum, n, eps);
+        }
+        __syncthreads();
+        scale = red[16];
+    }
+    // halves is even and NT a multiple of 2: both lanes of a pair take the same trips.
+    for (int hh = tid; hh < ((halves + NT - 1) / NT) * NT; hh += NT) {
+        const bool live = hh < halves;
+        const int base = hh * 16;
+        if (hh != tid && live) load_half16(x, weight, n, base, vec4, v, g);
+        if (live && weight) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = (v[k] * scale) * g[k];
+        }
+        if (live && norm_out)
+            for (int k = 0; k < 16 && base + k < n; k++) norm_out[base + k] = v[k];
+        float m = 0.0f;
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float a = v[k] < 0 ? -v[k] : v[k];
+                m = a > m ? a : m;
+            }
+        }
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        if (!live) continue;
+        uint32_t we[2] = {0, 0}, wo[2] = {0, 0};
+        float sc = 0.0f;
+        if (m != 0.0f) {
+            sc = m / 127.0f;
+            const float inv = 1.0f / sc;
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                int32_t q = go_round(v[k] * inv);
+                q = q > 127 ? 127 : (q < -127 ? -127 : q);
+                const uint32_t byte = (uint32_t)(uint8_t)(int8_t)q;
+                // element e = 16*half + k of the block: dword (e>>3) of the even/odd half
+                const int dw = (k >> 3), sh = ((k >> 1) & 3) * 8;
+                if (k & 1) wo[dw] |= byte << sh; else we[dw] |= byte << sh;
+            }
+        }
+        const int blk = hh >> 1, half = hh & 1;
+        uint2* qb = reinterpret_cast<uint2*>(q_out + blk * 32);
+        qb[half] = make_uint2(we[0], we[1]);      // even lanes: bytes 8*half .. +7
+        qb[2 + half] = make_uint2(wo[0], wo[1]);  // odd lanes: bytes 16 + 8*half .. +7
+        if (half == 0) s_out[blk] = sc;
+    }
+    __syncthreads();
+}
+
+template <int NT = kThreads>
+__device__ void wg_quantize_vec(const float* __restrict__ x, const float* __restrict__ weight, float eps, int n,
+                                int isa, float* vals, float* red, int8_t* q_out, float* s_out, float* norm_out) {
+    float v[16], g[16];
+    wg_quantize_vec_load(x, weight, n, v, g);
+    wg_quantize_vec_pre<NT>(x, weight, eps, n, isa, vals, red, q_out, s_out, norm_out, v, g);
+}
+
 __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(const float* __restrict__ x, const float* __restrict__ weight,
                                                                   float eps, int n, int isa, int8_t* __restrict__ qx,
                                                                   float* __restrict__ xs, float* __restrict__ norm_out) {
-    extern __shared__ __align__(16) float vals[];  // n + 17
-    float* red = vals + n;
+    extern __shared__ __align__(16) float vals[];  // ceil32(n) + 17
     const int row = blockIdx.x;
-    const int blocks = (n + 31) / 32;
-    x += (size_t)row * n;
-    qx += (size_t)row * blocks * 32;
-    xs += (size_t)row * blocks;
-    if (weight) {
-        float sumsq = wg_sumsq_parity(x, n, isa, red);
-        float scale = rms_scale(sumsq, n, eps);
-        for (int i = threadIdx.x; i < n; i += kThreads) vals[i] = (x[i] * scale) * weight[i];
-    } else {
-        for (int i = threadIdx.x; i < n; i += kThreads) vals[i] = x[i];
-    }
-    __syncthreads();
-    if (norm_out)
-        for (int i = threadIdx.x; i < n; i += kThreads) norm_out[(size_t)row * n + i] = vals[i];
-    // quantizeVecBlocksInto (internal/backend/simd/matvec_quant.go:746-797): one lane per block.
-    for (int b = threadIdx.x; b < blocks; b += kThreads) {
-        const int base = b * 32;
-        float maxabs = 0.0f;
-        for (int i = 0; i < 32; i++) {
-            if (base + i >= n) continue;
-            float v = vals[base + i];
-            if (v < 0) v = -v;
-            if (v > maxabs) maxabs = v;
-        }
-        uint32_t words[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        float scale = 0.0f;
-        if (maxabs != 0.0f) {
-            scale = maxabs / 127.0f;
-            const float inv = 1.0f / scale;
-            for (int i = 0; i < 32; i++) {
-                if (base + i >= n) continue;
-                int32_t q = go_round(vals[base + i] * inv);
-                q = q > 127 ? 127 : (q < -127 ? -127 : q);
-                const int p = qx_perm(i);
-                words[p >> 2] |= ((uint32_t)(uint8_t)(int8_t)q) << ((p & 3) * 8);
-            }
-        }
-        uint4* dst = reinterpret_cast<uint4*>(qx + base);
-        dst[0] = make_uint4(words[0], words[1], words[2], words[3]);
-        dst[1] = make_uint4(words[4], words[5], words[6], words[7]);
-        xs[b] = scale;
-    }
+    const int np = (n + 31) & ~31;
+    wg_quantize_vec(x + (size_t)row * n, weight, eps, n, isa, vals, vals + np, qx + (size_t)row * np,
+                    xs + (size_t)row * (np / 32), norm_out ? norm_out + (size_t)row * n : nullptr);
 }
 
 hipError_t launch_quantize_vec(const float* x, const float* weight, float eps, int n, int batch, int isa,
                                int8_t* qx, float* xs, float* norm_out, hipStream_t stream) {
     if (!x || !qx || !xs || n <= 0 || batch <= 0) return hipErrorInvalidValue;
-    size_t smem = sizeof(float) * ((size_t)n + 17);
-    if (smem > 160 * 1024) return hipErrorInvalidValue;
+    const size_t smem = sizeof(float) * ((size_t)(n + 31) / 32 * 32 + 17);
+    if (smem > 64 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(quantize_vec_kernel, dim3(batch), dim3(kThreads), smem, stream, x, weight, eps, n, isa, qx,
                        xs, norm_out);
     return hipGetLastError();
@@ -233,16 +388,32 @@ K4Mat k4_mat_from_payload(const uint8_t* payload, int rows, int cols) {
 struct GemvParams {
     K4Mat mats[3];
     float* outs[3];
-    int wg_begin[4];
+    int wg_begin[4];  // first tile of each matrix
+    int ntiles;
     int nmat;
     int cols, bpr, spr, rpw, batch;
     const int8_t* qx;
     const float* xs;
-    const float* x;  // W4A32 input
+    const float* x;       // W4A32 / in-kernel-quantised fp32 input [batch][cols]
+    const float* norm_w;  // RMSNorm gains applied before quantisation (nullable)
+    float eps;
+    int isa;
     unsigned long long* key;
 };
 
-enum GemvMode : int { kModeW4A8 = 0, kModeW4A32 = 1 };
+// kModeW4A8: activation already quantised (qx/xs); kModeW4A32: fp32 activation
+// used as is; kModeW4A8Fused: every workgroup quantises the fp32 activation
+// itself (after RMSNorm when norm_w is set) while its weight loads are in flight.
+// Selects instead of a dynamic index into the by-value kernel argument: an
+// indexed p.mats[k] would make the compiler copy the whole struct to scratch.
+__device__ __forceinline__ K4Mat pick_mat(const GemvParams& p, int k) {
+    return k == 0 ? p.mats[0] : (k == 1 ? p.mats[1] : p.mats[2]);
+}
+__device__ __forceinline__ float* pick_out(const GemvParams& p, int k) {
+    return k == 0 ? p.outs[0] : (k == 1 ? p.outs[1] : p.outs[2]);
+}
+
+enum GemvMode : int { kModeW4A8 = 0, kModeW4A32 = 1, kModeW4A8Fused = 2 };
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
     uint32_t u = __float_as_uint(v);
@@ -256,120 +427,179 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvParams p) {
     const int bpr = p.bpr;
     const int B = p.batch;
     const int tid = threadIdx.x;
-    const int qbytes = MODE == kModeW4A8 ? B * bpr * 32 : 0;
+    constexpr bool kInt8 = MODE != kModeW4A32;
+    const int qbytes = kInt8 ? B * bpr * 32 : 0;
     int8_t* sq = reinterpret_cast<int8_t*>(smem);
     float* sxs = reinterpret_cast<float*>(smem + qbytes);
-    float* terms = sxs + (MODE == kModeW4A8 ? B * bpr : 0);
-    const int tstride = bpr + 1;  // odd stride: the row-sum lanes hit distinct banks
-
-    int s = 0;
-    if (EPI != kEpiSiluMul)
-        while (s + 1 < p.nmat && (int)blockIdx.x >= p.wg_begin[s + 1]) s++;
-    const int row0 = ((int)blockIdx.x - p.wg_begin[s]) * p.rpw;
+    // terms[b * tp + row]: one fp32 term per (32-weight block, output row).  Rows
+    // are contiguous so the ordered row sums read conflict-free; the odd pitch
+    // keeps the writers (consecutive lanes = consecutive blocks) on distinct banks.
+    // The fused prologue uses the same region as its fp32 staging buffer first.
+    float* terms = sxs + (kInt8 ? B * bpr : 0);
     constexpr int nsub = EPI == kEpiSiluMul ? 2 : 1;
-
-    if (MODE == kModeW4A8) {
-        for (int i = tid * 16; i < qbytes; i += kThreads * 16)
-            *reinterpret_cast<uint4*>(sq + i) = *reinterpret_cast<const uint4*>(p.qx + i);
-        for (int i = tid; i < B * bpr; i += kThreads) sxs[i] = p.xs[i];
-        __syncthreads();
-    }
-
+    const int tp = (nsub * p.rpw * B) | 1;
     const int per_sub = p.rpw * bpr;
-    const int npairs = nsub * per_sub;
-    for (int base = 0; base < npairs; base += kThreads * kMaxPairs) {
+    const int npairs = nsub * per_sub;  // <= kThreads * kMaxPairs: one load pass per tile
+
+    // A workgroup walks tiles blockIdx.x, +gridDim.x, ...; tile t covers rows
+    // [row0, row0 + rpw) of matrix s (of both matrices for the SiLU pair).
+    auto tile_rows = [&](int tile, int& ms, int& row0) {
+        ms = 0;
+        int first = 0;
+        if (EPI != kEpiSiluMul) {
+            if (p.nmat > 1 && tile >= p.wg_begin[1]) { ms = 1; first = p.wg_begin[1]; }
+            if (p.nmat > 2 && tile >= p.wg_begin[2]) { ms = 2; first = p.wg_begin[2]; }
+        }
+        row0 = (tile - first) * p.rpw;
+    };
+
+    // One tile's worth of in-flight weight registers.  Two of them let a
+    // workgroup keep the next tile's loads in flight while it computes one.
+    struct TileRegs {
         uint4 w[kMaxPairs];
-        float sw[kMaxPairs];
-        int sk[kMaxPairs], rl[kMaxPairs], bb[kMaxPairs];
+        uint32_t wsc[kMaxPairs];  // f16 super-scale bits | u6 byte << 16
+        int meta[kMaxPairs];      // term row << 16 | block, or -1
+        int tile, ms, row0;
+        float resid;              // residual operand of this lane's row (kEpiResAdd)
+    };
+    // Issue this lane's 128-bit nibble loads (one 32-weight block each) for a
+    // tile; the scale bytes are decoded only when used, so nothing here waits.
+    auto load_tile = [&](TileRegs& R, int tile) {
+        R.tile = tile;
+        tile_rows(tile, R.ms, R.row0);
+        const int ms = R.ms, row0 = R.row0;
 #pragma unroll
         for (int j = 0; j < kMaxPairs; j++) {
-            const int pi = base + j * kThreads + tid;
-            sw[j] = 0.0f;
-            w[j] = make_uint4(0, 0, 0, 0);
-            sk[j] = -1;
+            const int pi = j * kThreads + tid;
+            R.wsc[j] = 0;
+            R.w[j] = make_uint4(0, 0, 0, 0);
+            R.meta[j] = -1;
             if (pi < npairs) {
                 const int k = nsub == 2 ? pi / per_sub : 0;
                 const int rem = pi - k * per_sub;
                 const int r = rem / bpr;
                 const int b = rem - r * bpr;
-                sk[j] = k;
-                rl[j] = r;
-                bb[j] = b;
-                const K4Mat& M = p.mats[nsub == 2 ? k : s];
+                R.meta[j] = (((k * p.rpw + r) * B) << 16) | b;
+                const K4Mat M = pick_mat(p, nsub == 2 ? k : ms);
                 const int grow = row0 + r;
                 if (grow < M.rows) {
                     const size_t blk = (size_t)grow * bpr + b;
                     const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(M.nib) + blk);
-                    w[j] = make_uint4(v.x, v.y, v.z, v.w);
-                    sw[j] = k4_scale(M.sup[(size_t)grow * p.spr + (b >> 3)], M.sub[blk]);
+                    R.w[j] = make_uint4(v.x, v.y, v.z, v.w);
+                    R.wsc[j] = (uint32_t)M.sup[(size_t)grow * p.spr + (b >> 3)] | ((uint32_t)M.sub[blk] << 16);
                 }
             }
         }
+        R.resid = 0.0f;
+        if (EPI == kEpiResAdd && tid < p.rpw && row0 + tid < p.mats[0].rows) R.resid = p.outs[0][row0 + tid];
+    };
+    auto compute_tile = [&](const TileRegs& R) {
 #pragma unroll
         for (int j = 0; j < kMaxPairs; j++) {
-            if (sk[j] < 0) continue;
-            const int b = bb[j];
-            float* trow = terms + ((sk[j] * p.rpw + rl[j]) * B) * tstride + b;
+            if (R.meta[j] < 0) continue;
+            const int b = R.meta[j] & 0xFFFF;
+            const float swj = k4_scale((uint16_t)(R.wsc[j] & 0xFFFFu), (uint8_t)(R.wsc[j] >> 16));
+            float* tcol = terms + b * tp + (R.meta[j] >> 16);
             for (int bi = 0; bi < B; bi++) {
                 float term = 0.0f;
-                if (MODE == kModeW4A8) {
+                if (kInt8) {
                     const float xsv = sxs[bi * bpr + b];
-                    if (sw[j] != 0.0f && xsv != 0.0f) {
+                    if (swj != 0.0f && xsv != 0.0f) {
                         const int8_t* xb = sq + (bi * bpr + b) * 32;
                         const uint4 xe = *reinterpret_cast<const uint4*>(xb);
                         const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
-                        term = (float)k4_block_dot(w[j], xe, xo) * (sw[j] * xsv);
+                        term = (float)k4_block_dot(R.w[j], xe, xo) * (swj * xsv);
                     }
                 } else {
-                    if (sw[j] != 0.0f) {
+                    if (swj != 0.0f) {
                         const float* xb = p.x + (size_t)bi * p.cols + b * 32;
                         const int n = min(32, p.cols - b * 32);
-                        const uint32_t wd[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+                        const uint32_t wd[4] = {R.w[j].x, R.w[j].y, R.w[j].z, R.w[j].w};
                         float d = 0.0f;
                         for (int e = 0; e < n; e++) d = __builtin_fmaf((float)k4_nib(wd[e >> 3], e & 7), xb[e], d);
-                        term = sw[j] * d;
+                        term = swj * d;
                     }
                 }
-                trow[bi * tstride] = term;
+                tcol[bi] = term;
             }
         }
-    }
-    __syncthreads();
-
-    if (EPI == kEpiSiluMul) {
-        if (tid < p.rpw) {
-            const int grow = row0 + tid;
-            if (grow < p.mats[0].rows) {
-                const float* tg = terms + tid * tstride;
-                const float* tu = terms + (p.rpw + tid) * tstride;
-                float g = 0.0f, u = 0.0f;
-                for (int b = 0; b < bpr; b++) g += tg[b];
-                for (int b = 0; b < bpr; b++) u += tu[b];
-                p.outs[0][grow] = fast_silu_vec(g) * u;
-            }
-        }
-        return;
-    }
-
-    const K4Mat& M = p.mats[s];
-    float* out = p.outs[s];
+    };
     unsigned long long best = 0;
-    for (int t = tid; t < p.rpw * B; t += kThreads) {
-        const int r = t / B;
-        const int bi = t - r * B;
-        const int grow = row0 + r;
-        if (grow >= M.rows) continue;
-        const float* tr = terms + t * tstride;
-        float sum = 0.0f;
-        for (int b = 0; b < bpr; b++) sum += tr[b];
-        if (EPI == kEpiResAdd) {
-            out[grow] = out[grow] + sum;
-        } else {
-            out[(size_t)bi * M.rows + grow] = sum;
-            if (EPI == kEpiArgmax) {
-                unsigned long long k = argmax_key(sum, grow);
-                best = k > best ? k : best;
+    // Ordered row sums of one tile's terms and the epilogue.
+    auto finish_tile = [&](const TileRegs& R) {
+        const int row0 = R.row0;
+        if (EPI == kEpiSiluMul) {
+            if (tid < p.rpw) {
+                const int grow = row0 + tid;
+                if (grow < p.mats[0].rows) {
+                    const float g = ordered_sum(terms + tid, tp, bpr);
+                    const float u = ordered_sum(terms + p.rpw + tid, tp, bpr);
+                    p.outs[0][grow] = fast_silu_vec(g) * u;
+                }
             }
+        } else {
+            const int rows = pick_mat(p, R.ms).rows;
+            float* out = pick_out(p, R.ms);
+            for (int t = tid; t < p.rpw * B; t += kThreads) {
+                const int r = t / B;
+                const int bi = t - r * B;
+                const int grow = row0 + r;
+                if (grow >= rows) continue;
+                const float sum = ordered_sum(terms + t, tp, bpr);
+                if (EPI == kEpiResAdd) {
+                    out[grow] = R.resid + sum;
+                } else {
+                    out[(size_t)bi * rows + grow] = sum;
+                    if (EPI == kEpiArgmax) {
+                        const unsigned long long k = argmax_key(sum, grow);
+                        best = k > best ? k : best;
+                    }
+                }
+            }
+        }
+    };
+
+    const int G = (int)gridDim.x;
+    TileRegs A, Bq;
+    PHASE_SLOT();
+    PHASE(0);
+    load_tile(A, blockIdx.x);
+    const bool two = (int)blockIdx.x + G < p.ntiles;
+    if (two) load_tile(Bq, blockIdx.x + G);
+    PHASE(1);
+    if (MODE == kModeW4A8) {
+        for (int i = tid * 16; i < qbytes; i += kThreads * 16)
+            *reinterpret_cast<uint4*>(sq + i) = *reinterpret_cast<const uint4*>(p.qx + i);
+        for (int i = tid; i < B * bpr; i += kThreads) sxs[i] = p.xs[i];
+        __syncthreads();
+    } else if (MODE == kModeW4A8Fused) {
+        const int np = bpr * 32;
+        for (int bi = 0; bi < B; bi++)
+            wg_quantize_vec(p.x + (size_t)bi * p.cols, p.norm_w, p.eps, p.cols, p.isa, terms, terms + np, sq + bi * np,
+                            sxs + bi * bpr, nullptr);
+    }
+    PHASE(2);
+    // Consume `cur`, refill it with the tile two steps ahead, finish the tile.
+    auto step = [&](TileRegs& cur) -> bool {
+        compute_tile(cur);
+        __syncthreads();
+        const TileRegs done_meta = cur;  // tile identity and residual for the epilogue
+        const int ahead = cur.tile + 2 * G;
+        if (ahead < p.ntiles) load_tile(cur, ahead);
+        else cur.tile = -1;
+        PHASE(3);
+        finish_tile(done_meta);
+        PHASE(4);
+        __syncthreads();
+        return true;
+    };
+    step(A);
+    if (two) {
+        while (true) {
+            step(Bq);
+            if (A.tile < 0) break;
+            step(A);
+            if (Bq.tile < 0) break;
         }
     }
     if (EPI == kEpiArgmax) {
@@ -388,55 +618,409 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvParams p) {
     }
 }
 
-// Rows per workgroup: as many 32-weight blocks as 256 lanes x 8 passes hold,
-// then fewer while the grid is under ~2 workgroups per CU (small matrices).
-static int choose_rpw(int total_rows, int bpr, int nsub, int batch, size_t fixed_smem, size_t smem_cap) {
-    int rpw = (kThreads * kMaxPairs) / (bpr * nsub);
+// ---------------------------------------------------------------------------
+// k4 GEMV, lane-chain form (rows whose block count is 8 * BPL).
+//
+// Eight lanes own one output row; lane j holds blocks [j*BPL, (j+1)*BPL) of
+// it in registers (BPL 128-bit nibble loads; the 8 lanes of a row cover its
+// bytes contiguously).  The CPU's ordered block sum ((t0 + t1) + t2) + ... is
+// kept exactly: lane j adds its own terms in order after receiving the running
+// sum of lane j-1 through a DPP row_shr:1 move -- seven hand-offs, no LDS and
+// no barrier.  A 256-lane workgroup covers 32 rows per unit and keeps two
+// units of weight loads in flight while it computes.
+
+__device__ __forceinline__ float dpp_shr1(float v) {  // lane i <- lane i-1 (within 16; lane 0 of a row gets 0)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_shl7(float v) {  // lane i <- lane i+7 (within 16): j=0 <- j=7 of its group
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x107, 0xF, 0xF, true));
+}
+template <int K>
+__device__ __forceinline__ float dpp_shr(float v) {  // lane i <- lane i-K within its row of 16 (K = 1..15)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + K, 0xF, 0xF, true));
+}
+
+// Gather the 8 lanes' value of one row group into lane j == 7: lane 7 receives
+// lane jj's value through a DPP row_shr:(7-jj) move.
+template <int JJ>
+__device__ __forceinline__ float from_lane(float v) {
+    if constexpr (JJ == 7) return v;
+    else return dpp_shr<7 - JJ>(v);
+}
+
+// Lane j of a row's 8 lanes owns blocks j, j+8, j+16, ... (BPL of them): each
+// load instruction of the 8 lanes reads 128 contiguous bytes of the row.  The
+// CPU's ordered block sum walks the lanes cyclically: block b is added by lane
+// b % 8 to the running sum it receives from lane (b-1) % 8 (DPP row_shr:1, and
+// row_shl:7 for the wrap from lane 7 to lane 0).
+template <int EPI, int BPL, int NB, int NW>
+__global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int NT = NW * 64;
+    constexpr int NSUB = EPI == kEpiSiluMul ? 2 : 1;
+    constexpr int RPU = 8 * NW;  // rows per unit
+    constexpr int NQ = BPL / 4;  // u32 words of u6 bytes per lane (bytes j*BPL .. j*BPL+BPL-1 of the row)
+    constexpr int NS = BPL / 2;  // u32 words of f16 super-scales per row (BPL supers)
+    const int bpr = 8 * BPL;
+    int8_t* sq = reinterpret_cast<int8_t*>(smem);
+    float* sxs = reinterpret_cast<float*>(smem + NB * bpr * 32);
+    float* work = sxs + NB * bpr;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int j = lane & 7;
+    const int gbase = lane & ~7;                    // first lane of this row's group
+    const int rsub = (tid >> 6) * 8 + (lane >> 3);  // row within the unit
+
+    struct Unit {
+        uint4 w[NSUB][BPL];    // nibbles of blocks j, j+8, ...
+        uint32_t sub[NSUB][NQ];
+        uint32_t sup[NSUB][NS];
+        int unit, ms, row;
+        float resid;
+    };
+    auto load_unit = [&](Unit& R, int unit) {
+        R.unit = unit;
+        int ms = 0, first = 0;
+        if (EPI != kEpiSiluMul) {
+            if (p.nmat > 1 && unit >= p.wg_begin[1]) { ms = 1; first = p.wg_begin[1]; }
+            if (p.nmat > 2 && unit >= p.wg_begin[2]) { ms = 2; first = p.wg_begin[2]; }
+        }
+        R.ms = ms;
+        const int row = (unit - first) * RPU + rsub;
+        R.row = row;
+#pragma unroll
+        for (int k = 0; k < NSUB; k++) {
+            const K4Mat M = pick_mat(p, NSUB == 2 ? k : ms);
+            const bool ok = row < M.rows;
+            const size_t r0 = (size_t)row * bpr;
+#pragma unroll
+            for (int q = 0; q < BPL; q++) {
+                u32x4 v = {0, 0, 0, 0};
+                if (ok) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(M.nib) + r0 + j + 8 * q);
+                R.w[k][q] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+            const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + r0 + j * BPL);
+            const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + (size_t)row * BPL);
+#pragma unroll
+            for (int m = 0; m < NQ; m++) R.sub[k][m] = ok ? sw[m] : 0u;
+#pragma unroll
+            for (int m = 0; m < NS; m++) R.sup[k][m] = ok ? su[m] : 0u;
+        }
+        R.resid = 0.0f;
+        if (EPI == kEpiResAdd && j == 7 && row < p.mats[0].rows) R.resid = p.outs[0][row];
+    };
+    // u6 byte of block b = j + 8q: held by lane b / BPL of the group, word (b % BPL) / 4.
+    auto sub_byte = [&](const Unit& R, int k, int q) -> uint32_t {
+        const int b = j + 8 * q;
+        const int src = gbase + b / BPL;
+        const int wi = (b % BPL) >> 2;
+        uint32_t got = 0;
+#pragma unroll
+        for (int m = 0; m < NQ; m++) {
+            const uint32_t v = (uint32_t)__shfl((int)R.sub[k][m], src, 64);
+            got = m == wi ? v : got;
+        }
+        return (got >> (8 * (b & 3))) & 0xFFu;
+    };
+    // Ordered row sum of matrix k, batch column bi; valid in lane j == 7.
+    auto row_sum = [&](const Unit& R, int k, int bi) -> float {
+        float t[BPL];
+#pragma unroll
+        for (int q = 0; q < BPL; q++) {
+            const int b = j + 8 * q;
+            const uint32_t supw = R.sup[k][q >> 1];
+            const float sw = k4_scale((uint16_t)((q & 1) ? (supw >> 16) : (supw & 0xFFFFu)), (uint8_t)sub_byte(R, k, q));
+            const float xsv = sxs[bi * bpr + b];
+            float term = 0.0f;
+            if (sw != 0.0f && xsv != 0.0f) {
+                const int8_t* xb = sq + (bi * bpr + b) * 32;
+                const uint4 xe = *reinterpret_cast<const uint4*>(xb);
+                const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
+                term = (float)k4_block_dot(R.w[k][q], xe, xo) * (sw * xsv);
+            }
+            t[q] = term;
+        }
+        // Block b = jj + 8q lives in lane jj: lane 7 gathers them and adds in block order.
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < BPL; q++) {
+            s = s + from_lane<0>(t[q]);
+            s = s + from_lane<1>(t[q]);
+            s = s + from_lane<2>(t[q]);
+            s = s + from_lane<3>(t[q]);
+            s = s + from_lane<4>(t[q]);
+            s = s + from_lane<5>(t[q]);
+            s = s + from_lane<6>(t[q]);
+            s = s + from_lane<7>(t[q]);
+        }
+        return s;
+    };
+
+    const int G = (int)gridDim.x;
+    Unit A, Bq;
+    PHASE_SLOT();
+    PHASE(0);
+    // Activation loads first: they must not queue behind the weight stream.
+    float pv[16], pg[16];
+    uint4 qpre[4];
+    const int qbytes = NB * bpr * 32;
+    if (p.qx) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = (tid + r * NT) * 16;
+            if (i < qbytes) qpre[r] = *reinterpret_cast<const uint4*>(p.qx + i);
+        }
+    } else if (NB == 1) {
+        wg_quantize_vec_load(p.x, p.norm_w, p.cols, pv, pg);
+    }
+    load_unit(A, blockIdx.x);
+    const bool two = (int)blockIdx.x + G < p.ntiles;
+    if (two) load_unit(Bq, blockIdx.x + G);
+    if (p.qx) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = (tid + r * NT) * 16;
+            if (i < qbytes) *reinterpret_cast<uint4*>(sq + i) = qpre[r];
+        }
+        for (int i = (tid + 4 * NT) * 16; i < qbytes; i += NT * 16)
+            *reinterpret_cast<uint4*>(sq + i) = *reinterpret_cast<const uint4*>(p.qx + i);
+        for (int i = tid; i < NB * bpr; i += NT) sxs[i] = p.xs[i];
+        __syncthreads();
+    } else if (NB == 1) {
+        wg_quantize_vec_pre<NT>(p.x, p.norm_w, p.eps, p.cols, p.isa, work, work + bpr * 32, sq, sxs, nullptr, pv, pg);
+    } else {
+        for (int bi = 0; bi < NB; bi++)
+            wg_quantize_vec<NT>(p.x + (size_t)bi * p.cols, p.norm_w, p.eps, p.cols, p.isa, work, work + bpr * 32,
+                                sq + bi * bpr * 32, sxs + bi * bpr, nullptr);
+    }
+    PHASE(1);
+    unsigned long long best = 0;
+    int nstep = 0;
+    auto step = [&](Unit& cur) {
+        float res[NSUB][NB];
+#pragma unroll
+        for (int k = 0; k < NSUB; k++)
+#pragma unroll
+            for (int bi = 0; bi < NB; bi++) res[k][bi] = row_sum(cur, k, bi);
+        const int row = cur.row, ms = cur.ms;
+        const float resid = cur.resid;
+        const int ahead = cur.unit + 2 * G;
+        if (ahead < p.ntiles) load_unit(cur, ahead);  // refill while the results are written
+        else cur.unit = -1;
+        nstep++;
+        if (nstep <= 6) PHASE(1 + nstep);
+        if (j != 7) return;
+        if (EPI == kEpiSiluMul) {
+            if (row < p.mats[0].rows) p.outs[0][row] = fast_silu_vec(res[0][0]) * res[1][0];
+        } else {
+            const int rows = pick_mat(p, ms).rows;
+            if (row >= rows) return;
+            float* out = pick_out(p, ms);
+            if (EPI == kEpiResAdd) {
+                out[row] = resid + res[0][0];
+            } else {
+#pragma unroll
+                for (int bi = 0; bi < NB; bi++) out[(size_t)bi * rows + row] = res[0][bi];
+                if (EPI == kEpiArgmax) {
+                    const unsigned long long key = argmax_key(res[0][0], row);
+                    best = key > best ? key : best;
+                }
+            }
+        }
+    };
+    step(A);
+    if (two) {
+        while (true) {
+            step(Bq);
+            if (A.unit < 0) break;
+            step(A);
+            if (Bq.unit < 0) break;
+        }
+    }
+    if (EPI == kEpiArgmax) {
+        __shared__ unsigned long long red[NW];
+        for (int off = 32; off > 0; off >>= 1) {
+            unsigned long long o = __shfl_down(best, off, 64);
+            best = o > best ? o : best;
+        }
+        if ((tid & 63) == 0) red[tid >> 6] = best;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long m = red[0];
+            for (int i = 1; i < NW; i++) m = red[i] > m ? red[i] : m;
+            atomicMax(p.key, m);
+        }
+    }
+}
+
+// Workgroups of kernel `fn` (with `smem` bytes of LDS) that fit on the whole
+// device at once; cached per kernel instance and LDS size class.
+template <typename K>
+static int resident_wgs(K fn, size_t smem) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), kThreads, smem) !=
+            hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    return per_cu * cus;
+}
+
+// Rows per tile: the fewest rows that still give one tile per resident
+// workgroup (small matrices are latency-bound: spread them out), capped by the
+// 256 lanes x 8 blocks a single load pass covers and by the LDS budget.
+static int choose_rpw(int total_rows, int bpr, int nsub, int batch, size_t fixed_smem, size_t smem_cap, int slots) {
+    int rmax = (kThreads * kMaxPairs) / (bpr * nsub);
+    if (rmax < 1) rmax = 1;
+    while (rmax > 1 && fixed_smem + (size_t)((nsub * rmax * batch) | 1) * bpr * 4 > smem_cap) rmax--;
+    int rpw = (total_rows + slots - 1) / slots;
     if (rpw < 1) rpw = 1;
-    while (rpw > 1 && (total_rows + rpw - 1) / rpw < 512) rpw = (rpw + 1) / 2;
-    while (rpw > 1 && fixed_smem + (size_t)nsub * rpw * batch * (bpr + 1) * 4 > smem_cap) rpw = (rpw + 1) / 2;
-    return rpw;
+    return rpw < rmax ? rpw : rmax;
+}
+
+static bool lane_gemv_disabled() {
+    static bool v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_TILES");
+        return e && atoi(e) != 0;
+    }();
+    return v;
+}
+
+static int lane_small_rows() {
+    static int v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_SMALL_ROWS");
+        return e ? atoi(e) : 16384;
+    }();
+    return v;
+}
+
+static int gemv_max_wgs() {
+    static int v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_MAX_WGS");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <int MODE, int EPI>
+static hipError_t launch_gemv_epi(GemvParams& p, hipStream_t stream) {
+    constexpr int nsub = EPI == kEpiSiluMul ? 2 : 1;
+    if (nsub * p.bpr > kThreads * kMaxPairs) return hipErrorInvalidValue;  // cols > 65536 (per matrix)
+    auto kern = k4_gemv_kernel<MODE, EPI>;
+    int total_rows = 0;
+    for (int i = 0; i < p.nmat; i++) total_rows += p.mats[i].rows;
+    if (EPI == kEpiSiluMul) total_rows = p.mats[0].rows;
+    const size_t fixed = MODE != kModeW4A32 ? (size_t)p.batch * p.bpr * 36 : 0;
+    const size_t cap = 64 * 1024;
+    const size_t stage = MODE == kModeW4A8Fused && p.norm_w ? ((size_t)p.bpr * 32 + 17) * 4 : 17 * 4;
+    // residency measured at the largest LDS footprint this launch can have
+    int slots = resident_wgs(kern, fixed + (stage > 16 * 1024 ? stage : 16 * 1024));
+    if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
+    p.rpw = choose_rpw(total_rows, p.bpr, nsub, p.batch, fixed, cap, slots);
+    size_t work = (size_t)((nsub * p.rpw * p.batch) | 1) * p.bpr * 4;
+    work = work > stage ? work : stage;
+    const size_t smem = fixed + work;
+    if (smem > cap) return hipErrorInvalidValue;
+    int ntiles = 0;
+    if (EPI == kEpiSiluMul) {
+        p.wg_begin[0] = 0;
+        ntiles = (p.mats[0].rows + p.rpw - 1) / p.rpw;
+    } else {
+        for (int i = 0; i < p.nmat; i++) {
+            p.wg_begin[i] = ntiles;
+            ntiles += (p.mats[i].rows + p.rpw - 1) / p.rpw;
+        }
+    }
+    p.wg_begin[p.nmat] = ntiles;
+    p.ntiles = ntiles;
+    // At most one resident wave of workgroups; the tiles are dealt out evenly.
+    const int per = (ntiles + slots - 1) / slots;
+    const int grid = (ntiles + per - 1) / per;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, p);
+    return hipGetLastError();
+}
+
+template <int EPI, int BPL, int NB, int NW>
+static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
+    auto kern = k4_gemv_lane_kernel<EPI, BPL, NB, NW>;
+    constexpr int RPU = 8 * NW;
+    const size_t stage = p.norm_w ? ((size_t)p.bpr * 32 + 17) * 4 : 17 * 4;
+    const size_t smem = (size_t)NB * p.bpr * 36 + stage;
+    if (smem > 64 * 1024) return hipErrorInvalidValue;
+    int units = 0;
+    if (EPI == kEpiSiluMul) {
+        p.wg_begin[0] = 0;
+        units = (p.mats[0].rows + RPU - 1) / RPU;
+    } else {
+        for (int i = 0; i < p.nmat; i++) {
+            p.wg_begin[i] = units;
+            units += (p.mats[i].rows + RPU - 1) / RPU;
+        }
+    }
+    p.wg_begin[p.nmat] = units;
+    p.ntiles = units;
+    p.rpw = RPU;
+    int slots = resident_wgs(kern, smem);
+    if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
+    const int per = (units + slots - 1) / slots;
+    const int grid = (units + per - 1) / per;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), smem, stream, p);
+    return hipGetLastError();
+}
+
+// Small matrices (latency-bound): one-wave workgroups, 8 rows each, so many
+// CUs share the few MB.  Large ones: four-wave workgroups streaming many units.
+template <int EPI, int BPL, int NB>
+static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
+    int rows = 0;
+    for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
+    if (rows <= lane_small_rows()) return launch_lane_gemv<EPI, BPL, NB, 1>(p, stream);
+    return launch_lane_gemv<EPI, BPL, NB, 4>(p, stream);
+}
+
+template <int EPI, int NB>
+static hipError_t try_lane_gemv(GemvParams& p, hipStream_t stream, bool* used) {
+    *used = true;
+    switch (p.bpr) {
+        case 32: return launch_lane_gemv_sized<EPI, 4, NB>(p, stream);
+        case 64: return launch_lane_gemv_sized<EPI, 8, NB>(p, stream);
+        case 96: return launch_lane_gemv_sized<EPI, 12, NB>(p, stream);
+        default: *used = false; return hipSuccess;
+    }
+}
+
+// Lane-chain kernel for the shapes it is instantiated for, else the tile kernel.
+static hipError_t dispatch_lane_gemv(GemvParams& p, GemvEpi epi, hipStream_t stream, bool* used) {
+    *used = false;
+    if (lane_gemv_disabled() || p.cols != p.bpr * 32) return hipSuccess;
+    if (p.batch == 1) {
+        switch (epi) {
+            case kEpiStore: return try_lane_gemv<kEpiStore, 1>(p, stream, used);
+            case kEpiResAdd: return try_lane_gemv<kEpiResAdd, 1>(p, stream, used);
+            case kEpiSiluMul: return try_lane_gemv<kEpiSiluMul, 1>(p, stream, used);
+            case kEpiArgmax: return try_lane_gemv<kEpiArgmax, 1>(p, stream, used);
+            default: return hipSuccess;
+        }
+    }
+    if (p.batch == 8 && epi == kEpiStore) return try_lane_gemv<kEpiStore, 8>(p, stream, used);
+    return hipSuccess;
 }
 
 template <int MODE>
 static hipError_t launch_gemv(GemvParams& p, GemvEpi epi, hipStream_t stream) {
-    const int nsub = epi == kEpiSiluMul ? 2 : 1;
-    int total_rows = 0;
-    for (int i = 0; i < p.nmat; i++) total_rows += p.mats[i].rows;
-    if (epi == kEpiSiluMul) total_rows = p.mats[0].rows;
-    const size_t fixed = MODE == kModeW4A8 ? (size_t)p.batch * p.bpr * 36 : 0;
-    const size_t cap = 64 * 1024;
-    p.rpw = choose_rpw(total_rows, p.bpr, nsub, p.batch, fixed, cap);
-    const size_t smem = fixed + (size_t)nsub * p.rpw * p.batch * (p.bpr + 1) * 4;
-    if (smem > cap) return hipErrorInvalidValue;
-    int grid = 0;
-    if (epi == kEpiSiluMul) {
-        p.wg_begin[0] = 0;
-        grid = (p.mats[0].rows + p.rpw - 1) / p.rpw;
-    } else {
-        for (int i = 0; i < p.nmat; i++) {
-            p.wg_begin[i] = grid;
-            grid += (p.mats[i].rows + p.rpw - 1) / p.rpw;
-        }
-    }
-    p.wg_begin[p.nmat] = grid;
     switch (epi) {
-        case kEpiStore:
-            hipLaunchKernelGGL((k4_gemv_kernel<MODE, kEpiStore>), dim3(grid), dim3(kThreads), smem, stream, p);
-            break;
-        case kEpiResAdd:
-            hipLaunchKernelGGL((k4_gemv_kernel<MODE, kEpiResAdd>), dim3(grid), dim3(kThreads), smem, stream, p);
-            break;
-        case kEpiSiluMul:
-            hipLaunchKernelGGL((k4_gemv_kernel<MODE, kEpiSiluMul>), dim3(grid), dim3(kThreads), smem, stream, p);
-            break;
-        case kEpiArgmax:
-            hipLaunchKernelGGL((k4_gemv_kernel<MODE, kEpiArgmax>), dim3(grid), dim3(kThreads), smem, stream, p);
-            break;
-        default:
-            return hipErrorInvalidValue;
+        case kEpiStore: return launch_gemv_epi<MODE, kEpiStore>(p, stream);
+        case kEpiResAdd: return launch_gemv_epi<MODE, kEpiResAdd>(p, stream);
+        case kEpiSiluMul: return launch_gemv_epi<MODE, kEpiSiluMul>(p, stream);
+        case kEpiArgmax: return launch_gemv_epi<MODE, kEpiArgmax>(p, stream);
+        default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, int cols, const int8_t* qx,
@@ -461,7 +1045,40 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
     p.qx = qx;
     p.xs = xs;
     p.key = argmax_key;
+    bool used = false;
+    hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
+    if (used) return e;
     return launch_gemv<kModeW4A8>(p, epi, stream);
+}
+
+hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int nmat, int cols, const float* x,
+                                     const float* norm_w, float eps, int isa, int batch, GemvEpi epi,
+                                     unsigned long long* argmax_key, hipStream_t stream) {
+    if (!mats || !outs || nmat < 1 || nmat > 3 || cols <= 0 || !x || batch < 1 || batch > 8)
+        return hipErrorInvalidValue;
+    if (epi == kEpiSiluMul && (nmat != 2 || mats[0].rows != mats[1].rows || batch != 1)) return hipErrorInvalidValue;
+    if ((epi == kEpiResAdd || epi == kEpiArgmax) && batch != 1) return hipErrorInvalidValue;
+    if (epi == kEpiArgmax && (!argmax_key || nmat != 1)) return hipErrorInvalidValue;
+    GemvParams p = {};
+    for (int i = 0; i < nmat; i++) {
+        if (!mats[i].nib || !mats[i].sub || !mats[i].sup || mats[i].rows <= 0 || !outs[i]) return hipErrorInvalidValue;
+        p.mats[i] = mats[i];
+        p.outs[i] = outs[i];
+    }
+    p.nmat = nmat;
+    p.cols = cols;
+    p.bpr = (cols + 31) / 32;
+    p.spr = (p.bpr + 7) / 8;
+    p.batch = batch;
+    p.x = x;
+    p.norm_w = norm_w;
+    p.eps = eps;
+    p.isa = isa;
+    p.key = argmax_key;
+    bool used = false;
+    hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
+    if (used) return e;
+    return launch_gemv<kModeW4A8Fused>(p, epi, stream);
 }
 
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch, hipStream_t stream) {
@@ -482,16 +1099,63 @@ hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float*
 // ---------------------------------------------------------------------------
 // Decode attention (internal/backend/simd/attn.go:255-419, attnpool.go:77-153)
 
+static constexpr int kAttnKeys = 64;          // keys staged in LDS per chunk
+static constexpr int kAttnLdsScores = 4096;    // contexts up to this keep scores in LDS
+static constexpr int kAttnHdr = 800;           // q, k, v (256 each) + reduction scratch
+
+// Copy cache rows t0 .. t0+nk-1 of one kv head (hd floats each, row stride
+// `stride`) into LDS rows of pitch kp.  Every lane issues its (up to 8)
+// 128-bit loads before the first LDS write.  Row `cur_t`, when cur != null,
+// comes from LDS (`cur`) instead -- the fused decode's own, just-computed row.
+__device__ __forceinline__ void stage_rows(float* dst, int kp, const float* __restrict__ base, int stride, int t0,
+                                           int nk, int hd, const float* cur, int cur_t) {
+    const int hd4 = hd >> 2;
+    const int total4 = nk * hd4;
+    for (int e0 = 0; e0 < total4; e0 += kThreads * 8) {
+        float4 r[8];
+        int off[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int e = e0 + j * kThreads + threadIdx.x;
+            off[j] = -1;
+            if (e < total4) {
+                const int tl = e / hd4;
+                const int i4 = e - tl * hd4;
+                const int t = t0 + tl;
+                off[j] = tl * kp + 4 * i4;
+                if (cur && t == cur_t)
+                    r[j] = make_float4(cur[4 * i4], cur[4 * i4 + 1], cur[4 * i4 + 2], cur[4 * i4 + 3]);
+                else
+                    r[j] = *reinterpret_cast<const float4*>(base + (size_t)t * stride + 4 * i4);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (off[j] < 0) continue;
+            dst[off[j]] = r[j].x;
+            dst[off[j] + 1] = r[j].y;
+            dst[off[j] + 2] = r[j].z;
+            dst[off[j] + 3] = r[j].w;
+        }
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) {
-    __shared__ float sq[256], sk[256], sv[256], red[17];
-    __shared__ float smax[kThreads / 64];
-    __shared__ float ssum;
+    extern __shared__ __align__(16) float lds[];
+    float* sq = lds;
+    float* sk = lds + 256;
+    float* sv = lds + 512;
+    float* red = lds + 768;
+    const int hd = a.head_dim;
+    const int kp = hd + 1;  // odd pitch: lane t reads key row t without bank conflicts
+    float* kt = lds + kAttnHdr;
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
-    const int hd = a.head_dim;
     const int kvh = h * a.kv_heads / a.n_head;
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
-    float* scores = a.scores + (size_t)h * a.max_ctx;
+    float* scores = a.max_ctx <= kAttnLdsScores ? kt + kAttnKeys * kp : a.scores + (size_t)h * a.max_ctx;
+    PHASE_SLOT();
+    PHASE(0);
 
     for (int i = tid; i < hd; i += kThreads) {
         sq[i] = a.q[h * hd + i];
@@ -501,15 +1165,14 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
         }
     }
     __syncthreads();
+    PHASE(1);
     if (a.fused) {
         if (a.q_norm) {  // attn.go:265-286 per-head RMSNorm (q, then k)
-            float s = wg_sumsq_parity(sq, hd, a.isa, red);
-            float sc = rms_scale(s, hd, a.eps);
+            const float sc = rms_scale(wg_sumsq_parity(sq, hd, a.isa, red), hd, a.eps);
             for (int i = tid; i < hd; i += kThreads) sq[i] = (sq[i] * sc) * a.q_norm[i];
         }
         if (a.k_norm) {
-            float s = wg_sumsq_parity(sk, hd, a.isa, red);
-            float sc = rms_scale(s, hd, a.eps);
+            const float sc = rms_scale(wg_sumsq_parity(sk, hd, a.isa, red), hd, a.eps);
             for (int i = tid; i < hd; i += kThreads) sk[i] = (sk[i] * sc) * a.k_norm[i];
         }
         __syncthreads();
@@ -538,54 +1201,81 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
         }
     }
 
-    // scores_t = Dot(q, k_t) * scale
+    PHASE(2);
+    // scores_t = Dot(q, k_t) * scale: keys staged 64 at a time (coalesced), one lane per key.
     float lmax = -INFINITY;
-    for (int t = tid; t <= pos; t += kThreads) {
-        const float* kt = (a.fused && t == pos) ? sk : a.cache_k + (size_t)t * a.kv_stride + kvh * hd;
-        float sc = dot_parity(sq, kt, hd, a.isa) * a.scale;
-        scores[t] = sc;
-        lmax = fmaxf(lmax, sc);
+    const float* kbase = a.cache_k + kvh * hd;
+    for (int t0 = 0; t0 <= pos; t0 += kAttnKeys) {
+        const int nk = min(kAttnKeys, pos + 1 - t0);
+        __syncthreads();
+        stage_rows(kt, kp, kbase, a.kv_stride, t0, nk, hd, a.fused ? sk : nullptr, pos);
+        __syncthreads();
+        if (tid < nk) {
+            const float sc = dot_parity(sq, kt + tid * kp, hd, a.isa) * a.scale;
+            scores[t0 + tid] = sc;
+            lmax = fmaxf(lmax, sc);
+        }
     }
+    PHASE(3);
     for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_down(lmax, off, 64));
-    if ((tid & 63) == 0) smax[tid >> 6] = lmax;
+    if ((tid & 63) == 0) red[20 + (tid >> 6)] = lmax;
     __syncthreads();
-    float maxv = smax[0];
-    for (int i = 1; i < kThreads / 64; i++) maxv = fmaxf(maxv, smax[i]);
+    float maxv = red[20];
+    for (int i = 1; i < kThreads / 64; i++) maxv = fmaxf(maxv, red[20 + i]);
     // Softmax (ops.go:83-106): exponentials, ordered sum, x *= 1/sum
     for (int t = tid; t <= pos; t += kThreads) scores[t] = fast_exp_scalar(scores[t] - maxv);
     __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        for (int t = 0; t <= pos; t++) sum += scores[t];
-        ssum = sum;
-    }
+    if (tid == 0) red[24] = ordered_sum(scores, 1, pos + 1);
     __syncthreads();
-    const float sum = ssum;
+    const float sum = red[24];
     if (sum != 0.0f) {
         const float inv = 1.0f / sum;
         for (int t = tid; t <= pos; t += kThreads) scores[t] = scores[t] * inv;
     }
     __syncthreads();
-    // out_d = sum_t p_t * v_t,d in t order
-    for (int d = tid; d < hd; d += kThreads) {
-        float acc = 0.0f;
-        const float* vcol = a.cache_v + kvh * hd + d;
-        for (int t = 0; t <= pos; t++) {
-            float v = (a.fused && t == pos) ? sv[d] : vcol[(size_t)t * a.kv_stride];
-            acc += scores[t] * v;
+    // out_d = sum_t p_t * v_t,d in t order (no FMA): V staged 64 keys at a time
+    // (coalesced), then lane d walks the chunk in order.
+    PHASE(4);
+    float acc = 0.0f;
+    const float* vbase = a.cache_v + kvh * hd;
+    for (int t0 = 0; t0 <= pos; t0 += kAttnKeys) {
+        const int nk = min(kAttnKeys, pos + 1 - t0);
+        stage_rows(kt, kp, vbase, a.kv_stride, t0, nk, hd, a.fused ? sv : nullptr, pos);
+        __syncthreads();
+        if (tid < hd) {
+            const float* ps = scores + t0;
+            int tl = 0;
+            for (; tl + 8 <= nk; tl += 8) {
+                float pv[8], vv[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    pv[k] = ps[tl + k];
+                    vv[k] = kt[(tl + k) * kp + tid];
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) acc += pv[k] * vv[k];
+            }
+            for (; tl < nk; tl++) acc += ps[tl] * kt[tl * kp + tid];
         }
-        a.out[h * hd + d] = acc;
+        __syncthreads();
     }
+    if (tid < hd) a.out[h * hd + tid] = acc;
+    PHASE(5);
 }
 
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
-    if (!a.q || !a.cache_k || !a.cache_v || !a.scores || !a.out || a.n_head <= 0 || a.kv_heads <= 0 ||
-        a.head_dim <= 0 || a.head_dim > 256 || a.kv_stride < a.kv_heads * a.head_dim || a.max_ctx <= 0)
+    if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
+        a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || a.kv_stride < a.kv_heads * a.head_dim ||
+        a.max_ctx <= 0)
         return hipErrorInvalidValue;
+    if (((uintptr_t)a.cache_k | (uintptr_t)a.cache_v) & 15) return hipErrorInvalidValue;
     if (a.fused && (!a.k || !a.v)) return hipErrorInvalidValue;
     if (!a.pos_dev && (a.pos_host < 0 || a.pos_host >= a.max_ctx)) return hipErrorInvalidValue;
     if (a.rope_cos && (!a.rope_sin || (a.head_dim & 1))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), 0, stream, a);
+    const bool lds_scores = a.max_ctx <= kAttnLdsScores;
+    if (!lds_scores && !a.scores) return hipErrorInvalidValue;
+    const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kAttnKeys * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
+    hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), smem, stream, a);
     return hipGetLastError();
 }
 
@@ -803,3 +1493,12 @@ hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, in
 }
 
 }  // namespace mantle
+
+#ifdef MANTLE_PHASE_TRACE
+extern "C" int mantleHipDebugPhaseTrace(unsigned long long* out, int max_slots, unsigned* n) {
+    hipError_t e = hipMemcpyFromSymbol(n, HIP_SYMBOL(mantle::g_phase_n), sizeof(unsigned));
+    if (e != hipSuccess) return e;
+    int k = (int)(*n < (unsigned)max_slots ? *n : (unsigned)max_slots);
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(mantle::g_phase), sizeof(unsigned long long) * 8 * k);
+}
+#endif

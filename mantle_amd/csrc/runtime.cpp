@@ -73,11 +73,10 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
     TRY(launch_embed(m->embed, d, m->prompt, m->state, m->x, s));
     for (int l = 0; l < c.n_layers; l++) {
         const auto& L = m->layers[l];
-        // runtime_decode.go:107 RMSNorm + attn.go:180-205 shared int8 activation for Q, K, V
-        TRY(launch_quantize_vec(m->x, L.attn_norm, c.eps, d, 1, m->isa, m->qx, m->xs, nullptr, s));
+        // runtime_decode.go:107 RMSNorm + attn.go:180-205 one int8 activation for Q, K, V
         K4Mat qkv[3] = {L.wq, L.wk, L.wv};
         float* outs[3] = {q, k, v};
-        TRY(launch_k4_gemv_w4a8(qkv, outs, 3, d, m->qx, m->xs, 1, kEpiStore, nullptr, s));
+        TRY(launch_k4_gemv_w4a8_fused(qkv, outs, 3, d, m->x, L.attn_norm, c.eps, m->isa, 1, kEpiStore, nullptr, s));
         AttnArgs a{};
         a.q = q;
         a.k = k;
@@ -102,21 +101,18 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.isa = m->isa;
         TRY(launch_attention_decode(a, s));
         // attn.go:417 Wo on the re-quantised attention output, residual folded in
-        TRY(launch_quantize_vec(m->attn, nullptr, 0.0f, m->q_dim, 1, m->isa, m->qx, m->xs, nullptr, s));
         float* xo[1] = {m->x};
-        TRY(launch_k4_gemv_w4a8(&L.wo, xo, 1, m->q_dim, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
+        TRY(launch_k4_gemv_w4a8_fused(&L.wo, xo, 1, m->q_dim, m->attn, nullptr, 0.0f, m->isa, 1, kEpiResAdd, nullptr, s));
         // ffn.go:18-91: RMSNorm, up/gate on one int8 activation, SiLU*up, down + residual
-        TRY(launch_quantize_vec(m->x, L.ffn_norm, c.eps, d, 1, m->isa, m->qx, m->xs, nullptr, s));
         K4Mat gu[2] = {L.gate, L.up};
         float* ao[2] = {m->act, m->act};
-        TRY(launch_k4_gemv_w4a8(gu, ao, 2, d, m->qx, m->xs, 1, kEpiSiluMul, nullptr, s));
-        TRY(launch_quantize_vec(m->act, nullptr, 0.0f, c.ffn, 1, m->isa, m->qx, m->xs, nullptr, s));
-        TRY(launch_k4_gemv_w4a8(&L.down, xo, 1, c.ffn, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
+        TRY(launch_k4_gemv_w4a8_fused(gu, ao, 2, d, m->x, L.ffn_norm, c.eps, m->isa, 1, kEpiSiluMul, nullptr, s));
+        TRY(launch_k4_gemv_w4a8_fused(&L.down, xo, 1, c.ffn, m->act, nullptr, 0.0f, m->isa, 1, kEpiResAdd, nullptr, s));
     }
     // runtime_greedy.go:53-67: final RMSNorm, lm_head, argmax (first max wins)
-    TRY(launch_quantize_vec(m->x, m->final_norm, c.eps, d, 1, m->isa, m->qx, m->xs, nullptr, s));
     float* lo[1] = {m->logits};
-    TRY(launch_k4_gemv_w4a8(&m->lm_head, lo, 1, d, m->qx, m->xs, 1, kEpiArgmax, &m->state->argmax_key, s));
+    TRY(launch_k4_gemv_w4a8_fused(&m->lm_head, lo, 1, d, m->x, m->final_norm, c.eps, m->isa, 1, kEpiArgmax,
+                                  &m->state->argmax_key, s));
     TRY(launch_finish_step(m->state, m->out_tokens, s));
 #undef TRY
     return hipSuccess;
