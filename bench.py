@@ -72,24 +72,57 @@ def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30):
 
             for i in range(copies + 5):
                 launch(i)
-            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+            # back-to-back launches between two HIP events on the launch stream:
+            # the average is the kernel's duration plus the dispatch gap
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
-            for i, (e0, e1) in enumerate(evs):
-                e0.record(stream)
+            e0.record(stream)
+            for i in range(iters):
                 launch(i)
-                e1.record(stream)
+            e1.record(stream)
             torch.cuda.synchronize()
-            ms = np.array([e0.elapsed_time(e1) for e0, e1 in evs])
+            avg_s = e0.elapsed_time(e1) * 1e-3 / iters
+            # one launch per event pair, for the spread
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(32)]
+            for i, (a, b) in enumerate(evs):
+                a.record(stream)
+                launch(i)
+                b.record(stream)
+            torch.cuda.synchronize()
+            single = np.array([a.elapsed_time(b) for a, b in evs]) * 1e-3
             algo_bytes = psize + 4 * cols * batch + 4 * rows * batch
-            avg_s = float(ms.mean()) * 1e-3
-            med_s = float(np.median(ms)) * 1e-3
             out.append(dict(rows=rows, cols=cols, batch=batch, payload_bytes=psize, algo_bytes=algo_bytes,
-                            avg_us=avg_s * 1e6, median_us=med_s * 1e6, gbs=algo_bytes / avg_s / 1e9,
-                            frac=algo_bytes / avg_s / 1e9 / PEAK_HBM_GBS, rotation_copies=copies))
+                            avg_us=avg_s * 1e6, single_launch_median_us=float(np.median(single)) * 1e6,
+                            gbs=algo_bytes / avg_s / 1e9, frac=algo_bytes / avg_s / 1e9 / PEAK_HBM_GBS,
+                            rotation_copies=copies, launches=iters))
             log(f"gemv {rows}x{cols} B={batch}: {avg_s*1e6:.2f} us avg, {algo_bytes/avg_s/1e9:.0f} GB/s")
         del bufs, base
         torch.cuda.empty_cache()
     return out
+
+
+def copy_calibration(nbytes=256 << 20, reps=5):
+    """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {reps} x {nbytes} B device-to-device copies")
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the roofline kernel, as measured by the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", "k4_gemv_lm_head_151936x1024_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1].strip())
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(path, cfg, prompt, budget_s=15.0, max_tokens=24):
@@ -127,6 +160,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV microbench")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the lm_head GEMV microbench and a copy calibration (for rocprofv3 --pmc runs)")
     ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -137,15 +172,21 @@ def main():
     import torch
 
     import mantle_amd
+    from mantle_amd import mcf
     from mantle_amd.mcf import QWEN3_0_6B
-    from tests import models
+
+    if args.gemv_only:
+        g = gemv_microbench([(151936, 1024)], [1], iters=50)[0]
+        copy_calibration()
+        print(json.dumps({"gemv": g}), flush=True)
+        return
 
     os.makedirs(args.model_dir, exist_ok=True)
     path = os.path.join(args.model_dir, "qwen3_0_6b_k4_seed0.mcf")
     t0 = time.perf_counter()
-    models.pack(path, 0, QWEN3_0_6B)
+    mcf.pack_cached(path, 0, QWEN3_0_6B)
     log(f"model ready in {time.perf_counter() - t0:.1f} s: {path}")
-    prompt = models.prompt(PROMPT_LEN, QWEN3_0_6B["vocab"], 1)
+    prompt = mcf.uniform_tokens(PROMPT_LEN, QWEN3_0_6B["vocab"], 1)
     max_ctx = PROMPT_LEN + args.warmup + args.steps + 8
     rt = mantle_amd.new_backend("hip").load_model(path, max_context=max_ctx)
     try:
@@ -176,8 +217,8 @@ def main():
     roofline = None
     if head:
         roofline = dict(bound="hbm", achieved=round(head["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                        frac=round(head["frac"], 4), traffic=None,
-                        kernel="k4_gemv_kernel<W4A8,Store> 151936x1024 B=1",
+                        frac=round(head["frac"], 4), traffic=traffic_from_profile(),
+                        kernel="k4_gemv_lane_kernel<0,4,1,4> (W4A8 store, 4-wave workgroups) 151936x1024 B=1",
                         avg_launch_us=round(head["avg_us"], 3), algo_bytes_per_launch=head["algo_bytes"])
     cpu = None
     if not args.no_cpu:

@@ -135,6 +135,9 @@ int mantleHipMCFSection(const mantleHipMCF* f, uint32_t type, const uint8_t** da
  * internal/backend/core/interfaces.go:4-18) for the k4 decode path. */
 typedef struct mantleHipModel mantleHipModel;
 int mantleHipModelLoadMCF(const char* path, int maxContext, mantleHipModel** out);
+/* Same, from an MCF image the caller already holds in memory (Mantle keeps the file mmapped:
+ * pkg/mcf/reader.go:21-69); the image is only read during the call. */
+int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, int maxContext, mantleHipModel** out);
 void mantleHipModelClose(mantleHipModel* m);
 int mantleHipModelConfig(const mantleHipModel* m, mantleHipQwen3Config* out);
 /* Reset(): Pos = 0 (internal/backend/simd/runtime.go:293-333). */

@@ -63,6 +63,7 @@ _SIGS = {
     "mantleHipMCFFind": (I, [P, C.c_char_p]),
     "mantleHipMCFSection": (I, [P, C.c_uint32, C.POINTER(P), C.POINTER(U64)]),
     "mantleHipModelLoadMCF": (I, [C.c_char_p, I, C.POINTER(P)]),
+    "mantleHipModelLoadMCFImage": (I, [P, U64, I, C.POINTER(P)]),
     "mantleHipModelClose": (None, [P]),
     "mantleHipModelConfig": (I, [P, C.POINTER(Qwen3Config)]),
     "mantleHipModelReset": (I, [P]),

@@ -35,6 +35,14 @@ class Backend:
         call("mantleHipModelLoadMCF", path.encode(), int(max_context), C.byref(h))
         return Runtime(h, max_context)
 
+    def load_model_image(self, image, max_context: int = 4096, parity_isa: str = "avx512") -> "Runtime":
+        """LoadModel from an MCF image already in memory (bytes / numpy uint8)."""
+        call("mantleHipSetParityISA", ISA[parity_isa])
+        buf = np.frombuffer(image, dtype=np.uint8) if not isinstance(image, np.ndarray) else image
+        h = P()
+        call("mantleHipModelLoadMCFImage", buf.ctypes.data, C.c_uint64(buf.nbytes), int(max_context), C.byref(h))
+        return Runtime(h, max_context)
+
 
 class Runtime:
     def __init__(self, handle: P, max_context: int):

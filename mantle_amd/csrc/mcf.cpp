@@ -48,7 +48,7 @@ static uint64_t elem_size(uint16_t dt) {
 // Reader
 
 McfFile::~McfFile() {
-    if (base_) munmap(base_, size_);
+    if (base_ && owned_) munmap(base_, size_);
 }
 
 int McfFile::find(const std::string& name) const {
@@ -84,6 +84,26 @@ bool McfFile::open(const std::string& path, std::string* err) {
     ::close(fd);
     if (p == MAP_FAILED) return fail("mcf: mmap failed");
     base_ = (uint8_t*)p;
+    owned_ = true;
+    return parse(err);
+}
+
+bool McfFile::open_image(const uint8_t* data, uint64_t size, std::string* err) {
+    if (!data || size < kHeaderSize) {
+        if (err) *err = "mcf: image too small";
+        return false;
+    }
+    base_ = const_cast<uint8_t*>(data);
+    size_ = size;
+    owned_ = false;
+    return parse(err);
+}
+
+bool McfFile::parse(std::string* err) {
+    auto fail = [&](const char* m) {
+        if (err) *err = m;
+        return false;
+    };
     // Header (pkg/mcf/header.go)
     if (memcmp(base_, "MCF\0", 4) != 0) return fail("mcf: bad magic");
     uint16_t major = rd16(base_ + 4);

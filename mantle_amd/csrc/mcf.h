@@ -39,6 +39,9 @@ class McfFile {
   public:
     ~McfFile();
     bool open(const std::string& path, std::string* err);
+    // View an MCF image that is already in memory (e.g. the caller's mmap);
+    // the bytes must outlive this object.
+    bool open_image(const uint8_t* data, uint64_t size, std::string* err);
     const uint8_t* data() const { return base_; }
     uint64_t size() const { return size_; }
     const std::vector<McfTensor>& tensors() const { return tensors_; }
@@ -47,8 +50,10 @@ class McfFile {
     const McfSection* section(uint32_t type) const;
 
   private:
+    bool parse(std::string* err);
     uint8_t* base_ = nullptr;
     uint64_t size_ = 0;
+    bool owned_ = false;
     std::vector<McfTensor> tensors_;
     std::vector<McfSection> sections_;
 };

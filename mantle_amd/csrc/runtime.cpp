@@ -184,6 +184,8 @@ extern "C" void mantleHipModelClose(mantleHipModel* m) {
 
 // LoadModelMCF (internal/backend/simd/loader.go:51-80 + internal/backend/cuda/cuda.go:39-73,
 // internal/backend/cuda/ops.go:5214-5313 weight residency).
+static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const char* path);
+
 extern "C" int mantleHipModelLoadMCF(const char* path, int max_ctx, mantleHipModel** out) {
     if (!path || !out || max_ctx <= 0) return hipErrorInvalidValue;
     *out = nullptr;
@@ -193,6 +195,22 @@ extern "C" int mantleHipModelLoadMCF(const char* path, int max_ctx, mantleHipMod
         fprintf(stderr, "mantle_hip: %s: %s\n", path, err.c_str());
         return hipErrorInvalidValue;
     }
+    return load_model(f, max_ctx, out, path);
+}
+
+extern "C" int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, int max_ctx, mantleHipModel** out) {
+    if (!data || !out || max_ctx <= 0) return hipErrorInvalidValue;
+    *out = nullptr;
+    McfFile f;
+    std::string err;
+    if (!f.open_image(data, size, &err)) {
+        fprintf(stderr, "mantle_hip: MCF image: %s\n", err.c_str());
+        return hipErrorInvalidValue;
+    }
+    return load_model(f, max_ctx, out, "MCF image");
+}
+
+static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const char* path) {
     const McfSection* cs = f.section(kSecHFConfigJSON);
     if (!cs) {
         fprintf(stderr, "mantle_hip: %s: missing config.json section\n", path);

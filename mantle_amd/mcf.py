@@ -40,6 +40,30 @@ def pack_synthetic_qwen3(path: str, seed: int, threads: int | None = None, **cfg
     return path
 
 
+def pack_cached(path: str, seed: int, cfg: dict) -> str:
+    """pack_synthetic_qwen3 unless `path` already exists (written atomically)."""
+    if not os.path.exists(path):
+        tmp = path + ".part"
+        pack_synthetic_qwen3(tmp, seed, **cfg)
+        os.replace(tmp, path)
+    return path
+
+
+def splitmix64(x: int) -> int:
+    m = (1 << 64) - 1
+    z = (x + 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    return z ^ (z >> 31)
+
+
+def uniform_tokens(n: int, vocab: int, seed: int) -> list[int]:
+    """Uniform-random token ids: id_i = splitmix64(splitmix64(seed) + i) mod vocab
+    (BASELINE config 1 prompt: 31 ids, seed 1)."""
+    base = splitmix64(seed)
+    return [splitmix64((base + i) & ((1 << 64) - 1)) % vocab for i in range(n)]
+
+
 def payload_size(rows: int, cols: int) -> int:
     return int(lib().mantleHipK4PayloadSize(rows, cols))
 

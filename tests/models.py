@@ -11,11 +11,7 @@ TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=128, ffn=
 
 def pack(path: str, seed: int, cfg: dict) -> str:
     from mantle_amd import mcf
-    if not os.path.exists(path):
-        tmp = path + ".part"
-        mcf.pack_synthetic_qwen3(tmp, seed, **cfg)
-        os.replace(tmp, path)
-    return path
+    return mcf.pack_cached(path, seed, cfg)
 
 
 def oracle_model(path: str, cfg: dict, max_ctx: int, isa: int = 2):
@@ -34,15 +30,10 @@ def oracle_model(path: str, cfg: dict, max_ctx: int, isa: int = 2):
 
 
 def splitmix64(x: int) -> int:
-    m = (1 << 64) - 1
-    z = (x + 0x9E3779B97F4A7C15) & m
-    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
-    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
-    return z ^ (z >> 31)
+    from mantle_amd import mcf
+    return mcf.splitmix64(x)
 
 
 def prompt(n: int, vocab: int, seed: int) -> list[int]:
-    """Uniform-random token ids (31 tokens, seed 1):
-    id_i = splitmix64(splitmix64(seed) + i) mod vocab."""
-    base = splitmix64(seed)
-    return [splitmix64((base + i) & ((1 << 64) - 1)) % vocab for i in range(n)]
+    from mantle_amd import mcf
+    return mcf.uniform_tokens(n, vocab, seed)

@@ -61,6 +61,18 @@ def test_tiny_generate_graph_matches_eager(hip, tiny_path):
         om.close()
 
 
+def test_load_from_memory_image_matches_path(hip, tiny_path):
+    import mantle_amd
+    p = models.prompt(5, models.TINY["vocab"], 2)
+    a = mantle_amd.new_backend().load_model(tiny_path, max_context=32)
+    b = mantle_amd.new_backend().load_model_image(open(tiny_path, "rb").read(), max_context=32)
+    try:
+        assert a.generate_greedy(p, 12) == b.generate_greedy(p, 12)
+    finally:
+        a.close()
+        b.close()
+
+
 def test_context_limit_and_bad_token(hip, tiny_path):
     import mantle_amd
     rt = mantle_amd.new_backend().load_model(tiny_path, max_context=4)

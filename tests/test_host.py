@@ -154,6 +154,11 @@ def test_model_load_errors_without_gpu(tmp_path):
     assert mantle_amd.new_backend("HIP").name() == "hip"
 
 
+def test_model_image_rejects_corrupt_bytes():
+    with pytest.raises(_lib.HipError):
+        mantle_amd.new_backend().load_model_image(b"MCF\0" + b"\0" * 100)
+
+
 def test_bench_rejects_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode == 2 and "single-GPU" in r.stdout
