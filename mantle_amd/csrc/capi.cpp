@@ -140,6 +140,7 @@ int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const f
     a.kv_heads = kvHeads;
     a.head_dim = headDim;
     a.kv_stride = kvStride;
+    a.head_stride = headDim;  // Mantle's cache: row = pos * kvStride + kvHead * headDim
     a.max_ctx = pos + 1;
     a.scale = scale;
     a.fused = 0;

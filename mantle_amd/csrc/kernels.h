@@ -79,8 +79,9 @@ struct AttnArgs {
     const float* rope_sin;
     const int* pos_dev;    // device position (fused) ...
     int pos_host;          // ... or a host position when pos_dev is null
-    float* cache_k;        // [max_ctx][kv_stride]
+    float* cache_k;        // row t of kv head g at cache + g*head_stride + t*kv_stride
     float* cache_v;
+    int head_stride;       // head_dim for Mantle's [pos][kv_heads*head_dim] layout, max_ctx*head_dim head-major
     float* scores;         // [n_head][max_ctx] scratch
     float* out;            // [n_head*head_dim]
     int n_head, kv_heads, head_dim, kv_stride, max_ctx;

@@ -116,7 +116,70 @@ __device__ __forceinline__ float ordered_sum(const float* t, int stride, int n) 
 
 // Dot exactly as dotAVX512 / dotSIMD / dotScalar (internal/backend/simd/ops_avx512.go:27-90,
 // ops_avx2.go:25-51, ops.go:49-55).  One thread computes the whole dot.
-__device__ float dot_parity(const float* a, const float* b, int n, int isa) {
+// Compile-time length: every accumulator stays in a register.
+template <int N, int ISA>
+__device__ __forceinline__ float dot_parity_t(const float* a, const float* b) {
+    if constexpr (ISA == kIsaAvx512) {
+        float acc[64];
+#pragma unroll
+        for (int k = 0; k < 64; k++) acc[k] = 0.0f;
+        constexpr int n64 = (N / 64) * 64;
+        constexpr int n32 = n64 + ((N - n64) / 32) * 32;
+        constexpr int n16 = n32 + ((N - n32) / 16) * 16;
+#pragma unroll
+        for (int i = 0; i < n64; i += 64)
+#pragma unroll
+            for (int k = 0; k < 64; k++) acc[k] = __builtin_fmaf(a[i + k], b[i + k], acc[k]);
+#pragma unroll
+        for (int i = n64; i < n32; i += 32)
+#pragma unroll
+            for (int k = 0; k < 32; k++) acc[k] = __builtin_fmaf(a[i + k], b[i + k], acc[k]);
+#pragma unroll
+        for (int i = n32; i < n16; i += 16)
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc[k] = __builtin_fmaf(a[i + k], b[i + k], acc[k]);
+        float sum = acc[0];
+#pragma unroll
+        for (int k = 1; k < 64; k++) sum += acc[k];
+#pragma unroll
+        for (int i = n16; i < N; i++) sum += a[i] * b[i];
+        return sum;
+    } else if constexpr (ISA == kIsaAvx2) {
+        float a0[8], a1[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) { a0[l] = 0.0f; a1[l] = 0.0f; }
+        constexpr int n16 = (N / 16) * 16;
+        constexpr int n8 = n16 + ((N - n16) / 8) * 8;
+#pragma unroll
+        for (int i = 0; i < n16; i += 16) {
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                a0[l] = __builtin_fmaf(a[i + l], b[i + l], a0[l]);
+                a1[l] = __builtin_fmaf(a[i + 8 + l], b[i + 8 + l], a1[l]);
+            }
+        }
+#pragma unroll
+        for (int i = n16; i < n8; i += 8)
+#pragma unroll
+            for (int l = 0; l < 8; l++) a0[l] = __builtin_fmaf(a[i + l], b[i + l], a0[l]);
+#pragma unroll
+        for (int l = 0; l < 8; l++) a0[l] = a0[l] + a1[l];
+        float sum = a0[0];
+#pragma unroll
+        for (int l = 1; l < 8; l++) sum += a0[l];
+#pragma unroll
+        for (int i = n8; i < N; i++) sum += a[i] * b[i];
+        return sum;
+    } else {
+        float sum = 0.0f;
+#pragma unroll 16
+        for (int i = 0; i < N; i++) sum += a[i] * b[i];
+        return sum;
+    }
+}
+
+// Runtime-length version (any n), same orders; used off the common head dims.
+__device__ float dot_parity_n(const float* a, const float* b, int n, int isa) {
     if (isa == kIsaAvx512) {
         if (n == 0) return 0.0f;
         float acc[4][16];
@@ -176,6 +239,20 @@ __device__ float dot_parity(const float* a, const float* b, int n, int isa) {
     float sum = 0.0f;
     for (int i = 0; i < n; i++) sum += a[i] * b[i];
     return sum;
+}
+
+__device__ __forceinline__ float dot_parity(const float* a, const float* b, int n, int isa) {
+    if (n == 128) {
+        if (isa == kIsaAvx512) return dot_parity_t<128, kIsaAvx512>(a, b);
+        if (isa == kIsaAvx2) return dot_parity_t<128, kIsaAvx2>(a, b);
+        return dot_parity_t<128, kIsaScalar>(a, b);
+    }
+    if (n == 64) {
+        if (isa == kIsaAvx512) return dot_parity_t<64, kIsaAvx512>(a, b);
+        if (isa == kIsaAvx2) return dot_parity_t<64, kIsaAvx2>(a, b);
+        return dot_parity_t<64, kIsaScalar>(a, b);
+    }
+    return dot_parity_n(a, b, n, isa);
 }
 
 // ---------------------------------------------------------------------------
@@ -773,6 +850,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     } else if (NB == 1) {
         wg_quantize_vec_load(p.x, p.norm_w, p.cols, pv, pg);
     }
+    __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight stream
     load_unit(A, blockIdx.x);
     const bool two = (int)blockIdx.x + G < p.ntiles;
     if (two) load_unit(Bq, blockIdx.x + G);
@@ -1099,47 +1177,59 @@ hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float*
 // ---------------------------------------------------------------------------
 // Decode attention (internal/backend/simd/attn.go:255-419, attnpool.go:77-153)
 
-static constexpr int kAttnKeys = 64;          // keys staged in LDS per chunk
+static constexpr int kAttnKeys = 64;          // keys staged in LDS per chunk (head_dim <= 128)
 static constexpr int kAttnLdsScores = 4096;    // contexts up to this keep scores in LDS
-static constexpr int kAttnHdr = 800;           // q, k, v (256 each) + reduction scratch
+static constexpr int kAttnHdr = 832;           // q, k, v (256 each) + 64 reduction floats
 
-// Copy cache rows t0 .. t0+nk-1 of one kv head (hd floats each, row stride
-// `stride`) into LDS rows of pitch kp.  Every lane issues its (up to 8)
-// 128-bit loads before the first LDS write.  Row `cur_t`, when cur != null,
-// comes from LDS (`cur`) instead -- the fused decode's own, just-computed row.
-__device__ __forceinline__ void stage_rows(float* dst, int kp, const float* __restrict__ base, int stride, int t0,
-                                           int nk, int hd, const float* cur, int cur_t) {
+// Up to 8 float4 of one chunk of cache rows (keys t0 .. t0+nk-1 of one kv head)
+// per lane, held in registers so the loads of the next chunk are in flight
+// while this one is used.  Row `skip` (the fused step's own row) is not loaded.
+struct ChunkRegs {
+    float4 r[8];
+    int off[8];  // LDS offset (row * pitch + col), -1: nothing to store
+};
+
+__device__ __forceinline__ void chunk_issue(ChunkRegs& c, const float* __restrict__ base, int stride, int t0, int nk,
+                                            int hd, int kp, int skip) {
+    // Loads are unconditional (lanes past the chunk re-read row t0, column 0) so
+    // that no branch sits between them and their first use: the wait counts
+    // then only wait for the data actually needed.
     const int hd4 = hd >> 2;
     const int total4 = nk * hd4;
-    for (int e0 = 0; e0 < total4; e0 += kThreads * 8) {
-        float4 r[8];
-        int off[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int e = e0 + j * kThreads + threadIdx.x;
-            off[j] = -1;
-            if (e < total4) {
-                const int tl = e / hd4;
-                const int i4 = e - tl * hd4;
-                const int t = t0 + tl;
-                off[j] = tl * kp + 4 * i4;
-                if (cur && t == cur_t)
-                    r[j] = make_float4(cur[4 * i4], cur[4 * i4 + 1], cur[4 * i4 + 2], cur[4 * i4 + 3]);
-                else
-                    r[j] = *reinterpret_cast<const float4*>(base + (size_t)t * stride + 4 * i4);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (off[j] < 0) continue;
-            dst[off[j]] = r[j].x;
-            dst[off[j] + 1] = r[j].y;
-            dst[off[j] + 2] = r[j].z;
-            dst[off[j] + 3] = r[j].w;
-        }
+    for (int j = 0; j < 8; j++) {
+        const int e = j * kThreads + threadIdx.x;
+        const bool live = e < total4;
+        const int ee = live ? e : 0;
+        const int tl = ee / hd4;
+        const int i4 = ee - tl * hd4;
+        const int t = t0 + tl;
+        const int o = tl * kp + 4 * i4;
+        c.r[j] = *reinterpret_cast<const float4*>(base + (size_t)t * stride + 4 * i4);
+        c.off[j] = (!live || t == skip) ? -1 : o;
     }
 }
 
+__device__ __forceinline__ void chunk_store(const ChunkRegs& c, float* dst, int kp, const float* cur, int t0, int nk,
+                                            int skip, int hd) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int o = c.off[j];
+        if (o < 0) continue;
+        dst[o] = c.r[j].x;
+        dst[o + 1] = c.r[j].y;
+        dst[o + 2] = c.r[j].z;
+        dst[o + 3] = c.r[j].w;
+    }
+    // the fused step's own row comes from `cur` (written by another workgroup
+    // this same launch, so not read back from the cache)
+    if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
+}
+
+// Decode attention for one query head (internal/backend/simd/attn.go:255-419,
+// attnpool.go:77-153), bit-exact to the CPU order.  Every global load the head
+// needs first -- q, k, v, the RoPE row, the first K and V chunks -- is issued
+// at the start; later chunks are loaded one chunk ahead of their use.
 __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     float* sq = lds;
@@ -1148,73 +1238,112 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
     float* red = lds + 768;
     const int hd = a.head_dim;
     const int kp = hd + 1;  // odd pitch: lane t reads key row t without bank conflicts
+    const int kc = hd <= 128 ? kAttnKeys : (kThreads * 32) / hd;  // keys per chunk: <= 8 float4 per lane
     float* kt = lds + kAttnHdr;
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const int kvh = h * a.kv_heads / a.n_head;
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
-    float* scores = a.max_ctx <= kAttnLdsScores ? kt + kAttnKeys * kp : a.scores + (size_t)h * a.max_ctx;
+    float* scores = a.max_ctx <= kAttnLdsScores ? kt + kc * kp : a.scores + (size_t)h * a.max_ctx;
+    const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
+    const float* vbase = a.cache_v + (size_t)kvh * a.head_stride;
+    const int skip = a.fused ? pos : -1;
     PHASE_SLOT();
     PHASE(0);
 
-    for (int i = tid; i < hd; i += kThreads) {
-        sq[i] = a.q[h * hd + i];
-        if (a.fused) {
-            sk[i] = a.k[kvh * hd + i];
-            sv[i] = a.v[kvh * hd + i];
-        }
+    // ---- all first-needed loads in flight together
+    // (indices clamped instead of branched around, see chunk_issue)
+    const int half = hd / 2;
+    const int ti = tid < hd ? tid : 0;
+    const int th = tid < half ? tid : 0;
+    const float qv = a.q[h * hd + ti];
+    const float* kin = a.fused ? a.k : a.q;
+    const float* vin = a.fused ? a.v : a.q;
+    const float kv = kin[(a.fused ? kvh * hd : 0) + ti];
+    const float vv = vin[(a.fused ? kvh * hd : 0) + ti];
+    const float* cbase = a.rope_cos ? a.rope_cos + (size_t)pos * half : a.q;
+    const float* sbase = a.rope_sin ? a.rope_sin + (size_t)pos * half : a.q;
+    const float cs = cbase[th];
+    const float sn = sbase[th];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the chunk loads
+    ChunkRegs ck, cv;
+    const int nk0 = min(kc, pos + 1);
+    chunk_issue(ck, kbase, a.kv_stride, 0, nk0, hd, kp, skip);
+    chunk_issue(cv, vbase, a.kv_stride, 0, nk0, hd, kp, skip);
+    if (tid < hd) {
+        sq[tid] = qv;
+        sk[tid] = kv;
+        sv[tid] = vv;
     }
     __syncthreads();
     PHASE(1);
     if (a.fused) {
-        if (a.q_norm) {  // attn.go:265-286 per-head RMSNorm (q, then k)
-            const float sc = rms_scale(wg_sumsq_parity(sq, hd, a.isa, red), hd, a.eps);
-            for (int i = tid; i < hd; i += kThreads) sq[i] = (sq[i] * sc) * a.q_norm[i];
-        }
-        if (a.k_norm) {
-            const float sc = rms_scale(wg_sumsq_parity(sk, hd, a.isa, red), hd, a.eps);
-            for (int i = tid; i < hd; i += kThreads) sk[i] = (sk[i] * sc) * a.k_norm[i];
+        // attn.go:265-286 per-head RMSNorm: q's lane-striped sum on lanes 0..L-1,
+        // k's on lanes 64..64+L-1 (another wave), both at once.
+        const int lanes = a.isa == kIsaAvx512 ? 16 : (a.isa == kIsaAvx2 ? 8 : 0);
+        const int nfull = lanes ? (hd / lanes) * lanes : 0;
+        const bool qlane = lanes && tid < lanes;
+        const bool klane = lanes && tid >= 64 && tid < 64 + lanes;
+        if (qlane || klane) {
+            const float* src = qlane ? sq : sk;
+            const int l = qlane ? tid : tid - 64;
+            float acc = 0.0f;
+            for (int i = l; i < nfull; i += lanes) acc = __builtin_fmaf(src[i], src[i], acc);
+            red[(qlane ? 0 : 32) + l] = acc;
         }
         __syncthreads();
-        if (a.rope_cos) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
-            const int half = hd / 2;
-            const float* c = a.rope_cos + (size_t)pos * half;
-            const float* sn = a.rope_sin + (size_t)pos * half;
-            for (int i = tid; i < half; i += kThreads) {
-                float x0 = sq[i], x1 = sq[i + half];
-                sq[i] = x0 * c[i] - x1 * sn[i];
-                sq[i + half] = __builtin_fmaf(x0, sn[i], x1 * c[i]);
-                x0 = sk[i];
-                x1 = sk[i + half];
-                sk[i] = x0 * c[i] - x1 * sn[i];
-                sk[i + half] = __builtin_fmaf(x0, sn[i], x1 * c[i]);
+        if (tid == 0 || tid == 64) {
+            const float* src = tid == 0 ? sq : sk;
+            const float* pr = red + (tid == 0 ? 0 : 32);
+            float sum = 0.0f;
+            if (lanes) {
+                sum = pr[0];
+                for (int l = 1; l < lanes; l++) sum += pr[l];
             }
+            for (int i = nfull; i < hd; i++) sum += src[i] * src[i];
+            red[tid == 0 ? 16 : 48] = rms_scale(sum, hd, a.eps);
+        }
+        __syncthreads();
+        if (tid < hd) {
+            float q1 = sq[tid], k1 = sk[tid];
+            if (a.q_norm) q1 = (q1 * red[16]) * a.q_norm[tid];
+            if (a.k_norm) k1 = (k1 * red[48]) * a.k_norm[tid];
+            sq[tid] = q1;
+            sk[tid] = k1;
+        }
+        __syncthreads();
+        if (a.rope_cos && tid < half) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
+            float x0 = sq[tid], x1 = sq[tid + half];
+            sq[tid] = x0 * cs - x1 * sn;
+            sq[tid + half] = __builtin_fmaf(x0, sn, x1 * cs);
+            x0 = sk[tid];
+            x1 = sk[tid + half];
+            sk[tid] = x0 * cs - x1 * sn;
+            sk[tid + half] = __builtin_fmaf(x0, sn, x1 * cs);
         }
         __syncthreads();
         // ops_runtime.go:112-131 StoreKV: the first q-head of each kv group writes.
         const int first = (kvh * a.n_head + a.kv_heads - 1) / a.kv_heads;
-        if (h == first) {
-            for (int i = tid; i < hd; i += kThreads) {
-                a.cache_k[(size_t)pos * a.kv_stride + kvh * hd + i] = sk[i];
-                a.cache_v[(size_t)pos * a.kv_stride + kvh * hd + i] = sv[i];
-            }
+        if (h == first && tid < hd) {
+            a.cache_k[(size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride + tid] = sk[tid];
+            a.cache_v[(size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride + tid] = sv[tid];
         }
     }
-
     PHASE(2);
-    // scores_t = Dot(q, k_t) * scale: keys staged 64 at a time (coalesced), one lane per key.
+
+    // ---- scores_t = Dot(q, k_t) * scale, one lane per key of the staged chunk
     float lmax = -INFINITY;
-    const float* kbase = a.cache_k + kvh * hd;
-    for (int t0 = 0; t0 <= pos; t0 += kAttnKeys) {
-        const int nk = min(kAttnKeys, pos + 1 - t0);
+    for (int t0 = 0; t0 <= pos; t0 += kc) {
+        const int nk = min(kc, pos + 1 - t0);
+        chunk_store(ck, kt, kp, sk, t0, nk, skip, hd);
         __syncthreads();
-        stage_rows(kt, kp, kbase, a.kv_stride, t0, nk, hd, a.fused ? sk : nullptr, pos);
-        __syncthreads();
+        if (t0 + kc <= pos) chunk_issue(ck, kbase, a.kv_stride, t0 + kc, min(kc, pos + 1 - t0 - kc), hd, kp, skip);
         if (tid < nk) {
             const float sc = dot_parity(sq, kt + tid * kp, hd, a.isa) * a.scale;
             scores[t0 + tid] = sc;
             lmax = fmaxf(lmax, sc);
         }
+        __syncthreads();
     }
     PHASE(3);
     for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_down(lmax, off, 64));
@@ -1233,27 +1362,26 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
         for (int t = tid; t <= pos; t += kThreads) scores[t] = scores[t] * inv;
     }
     __syncthreads();
-    // out_d = sum_t p_t * v_t,d in t order (no FMA): V staged 64 keys at a time
-    // (coalesced), then lane d walks the chunk in order.
     PHASE(4);
+    // ---- out_d = sum_t p_t * v_t,d in t order (no FMA)
     float acc = 0.0f;
-    const float* vbase = a.cache_v + kvh * hd;
-    for (int t0 = 0; t0 <= pos; t0 += kAttnKeys) {
-        const int nk = min(kAttnKeys, pos + 1 - t0);
-        stage_rows(kt, kp, vbase, a.kv_stride, t0, nk, hd, a.fused ? sv : nullptr, pos);
+    for (int t0 = 0; t0 <= pos; t0 += kc) {
+        const int nk = min(kc, pos + 1 - t0);
+        chunk_store(cv, kt, kp, sv, t0, nk, skip, hd);
         __syncthreads();
+        if (t0 + kc <= pos) chunk_issue(cv, vbase, a.kv_stride, t0 + kc, min(kc, pos + 1 - t0 - kc), hd, kp, skip);
         if (tid < hd) {
             const float* ps = scores + t0;
             int tl = 0;
             for (; tl + 8 <= nk; tl += 8) {
-                float pv[8], vv[8];
+                float pv[8], vx[8];
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
                     pv[k] = ps[tl + k];
-                    vv[k] = kt[(tl + k) * kp + tid];
+                    vx[k] = kt[(tl + k) * kp + tid];
                 }
 #pragma unroll
-                for (int k = 0; k < 8; k++) acc += pv[k] * vv[k];
+                for (int k = 0; k < 8; k++) acc += pv[k] * vx[k];
             }
             for (; tl < nk; tl++) acc += ps[tl] * kt[tl * kp + tid];
         }
@@ -1265,16 +1393,21 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
 
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
-        a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || a.kv_stride < a.kv_heads * a.head_dim ||
-        a.max_ctx <= 0)
+        a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || (a.head_stride & 3) || a.max_ctx <= 0)
         return hipErrorInvalidValue;
+    // rows of one head must not overlap rows of the next: either interleaved
+    // ([pos][kv_heads*hd]) or head-major ([kv_head][max_ctx][hd])
+    const bool interleaved = a.head_stride == a.head_dim && a.kv_stride >= a.kv_heads * a.head_dim;
+    const bool head_major = a.kv_stride == a.head_dim && a.head_stride >= a.max_ctx * a.head_dim;
+    if (!interleaved && !head_major) return hipErrorInvalidValue;
     if (((uintptr_t)a.cache_k | (uintptr_t)a.cache_v) & 15) return hipErrorInvalidValue;
     if (a.fused && (!a.k || !a.v)) return hipErrorInvalidValue;
     if (!a.pos_dev && (a.pos_host < 0 || a.pos_host >= a.max_ctx)) return hipErrorInvalidValue;
     if (a.rope_cos && (!a.rope_sin || (a.head_dim & 1))) return hipErrorInvalidValue;
     const bool lds_scores = a.max_ctx <= kAttnLdsScores;
     if (!lds_scores && !a.scores) return hipErrorInvalidValue;
-    const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kAttnKeys * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
+    const int kc = a.head_dim <= 128 ? kAttnKeys : (kThreads * 32) / a.head_dim;
+    const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kc * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
     hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), smem, stream, a);
     return hipGetLastError();
 }

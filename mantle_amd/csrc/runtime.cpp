@@ -11,7 +11,8 @@
 //     device memory, so one decode step is a fixed sequence of kernel
 //     launches that never reads the host: it is captured once as a HIP
 //     graph and replayed per position;
-//   * the f32 KV cache is [layer][max_ctx][kv_heads*head_dim], contiguous per layer.
+//   * the f32 KV cache is head-major, [layer][kv_head][max_ctx][head_dim]: the
+//     keys a decode step reads for one kv head are one contiguous run.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -94,7 +95,8 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.n_head = c.n_heads;
         a.kv_heads = c.n_kv_heads;
         a.head_dim = c.head_dim;
-        a.kv_stride = m->kv_dim;
+        a.kv_stride = c.head_dim;                          // head-major cache:
+        a.head_stride = m->max_ctx * c.head_dim;           // [layer][kv_head][max_ctx][head_dim]
         a.max_ctx = m->max_ctx;
         a.scale = (float)(1.0 / sqrt((double)c.head_dim));  // attn.go:311-314
         a.fused = 1;
