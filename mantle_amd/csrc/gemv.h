@@ -1,0 +1,103 @@
+// gemv.h -- k4 GEMV launch parameters and host-side helpers shared by the
+// tile kernel (kernels.hip) and the lane-chain kernel (gemv_lane_*.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "kernels.h"
+#include "quant_device.h"
+
+namespace mantle {
+
+struct GemvParams {
+    K4Mat mats[3];
+    float* outs[3];
+    int wg_begin[4];  // first tile of each matrix
+    int ntiles;
+    int nmat;
+    int cols, bpr, spr, rpw, batch;
+    const int8_t* qx;
+    const float* xs;
+    const float* x;       // W4A32 / in-kernel-quantised fp32 input [batch][cols]
+    const float* norm_w;  // RMSNorm gains applied before quantisation (nullable)
+    float eps;
+    int isa;
+    unsigned long long* key;
+};
+
+// kModeW4A8: activation already quantised (qx/xs); kModeW4A32: fp32 activation
+// used as is; kModeW4A8Fused: every workgroup quantises the fp32 activation
+// itself (after RMSNorm when norm_w is set) while its weight loads are in flight.
+// Selects instead of a dynamic index into the by-value kernel argument: an
+// indexed p.mats[k] would make the compiler copy the whole struct to scratch.
+__device__ __forceinline__ K4Mat pick_mat(const GemvParams& p, int k) {
+    return k == 0 ? p.mats[0] : (k == 1 ? p.mats[1] : p.mats[2]);
+}
+__device__ __forceinline__ float* pick_out(const GemvParams& p, int k) {
+    return k == 0 ? p.outs[0] : (k == 1 ? p.outs[1] : p.outs[2]);
+}
+
+enum GemvMode : int { kModeW4A8 = 0, kModeW4A32 = 1, kModeW4A8Fused = 2 };
+// Lane-kernel prologue: activation pre-quantised (qx/xs), quantised in the
+// kernel, or RMSNorm then quantised in the kernel.
+enum LanePro : int { kProQx = 0, kProQuant = 1, kProNorm = 2 };
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    uint32_t u = __float_as_uint(v);
+    uint32_t s = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)s << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// Workgroups of kernel `fn` (with `smem` bytes of LDS) that fit on the whole
+// device at once; cached per kernel instance and LDS size class.
+template <typename K>
+static int resident_wgs(K fn, size_t smem) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), kThreads, smem) !=
+            hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    return per_cu * cus;
+}
+
+static inline bool lane_gemv_disabled() {
+    static bool v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_TILES");
+        return e && atoi(e) != 0;
+    }();
+    return v;
+}
+
+static inline int lane_small_rows() {
+    static int v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_SMALL_ROWS");
+        return e ? atoi(e) : 16384;
+    }();
+    return v;
+}
+
+static inline int gemv_max_wgs() {
+    static int v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_MAX_WGS");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+// Lane-chain GEMV entry points, one translation unit each (they compile in
+// parallel).  `pro` is a LanePro; *used is false when the lane kernel has no
+// instance for the shape and the caller must use the tile kernel.
+hipError_t lane_gemv_store(GemvParams& p, int pro, hipStream_t stream, bool* used);              // gemv_lane_store.hip
+hipError_t lane_gemv_fused(GemvParams& p, GemvEpi epi, int pro, hipStream_t stream, bool* used); // gemv_lane_fused.hip
+hipError_t lane_gemv_batch8(GemvParams& p, int pro, hipStream_t stream, bool* used);             // gemv_lane_b8.hip
+
+}  // namespace mantle

@@ -19,388 +19,15 @@
 #include <hip/hip_fp16.h>
 #include <stdlib.h>
 
-#include "device_common.h"
-#include "kernels.h"
+#include <algorithm>
+#include <array>
+#include <vector>
+
+#include "gemv.h"
+#include "phase_trace.h"
+#include "quant_device.h"
 
 namespace mantle {
-
-// Phase timestamps of workgroup 0 (100 MHz wall clock) for latency studies;
-// compiled only into a -DMANTLE_PHASE_TRACE build, never into the product.
-#ifdef MANTLE_PHASE_TRACE
-__device__ unsigned long long g_phase[8192 * 8];
-__device__ unsigned int g_phase_n;
-#define PHASE_SLOT()                                                            \
-    unsigned phase_slot_ = 0;                                                   \
-    if (blockIdx.x == 0 && threadIdx.x == 0) phase_slot_ = atomicAdd(&g_phase_n, 1u) & 8191u
-#define PHASE(k)                                                                \
-    do {                                                                        \
-        if (blockIdx.x == 0 && threadIdx.x == 0) g_phase[phase_slot_ * 8 + (k)] = wall_clock64(); \
-    } while (0)
-#else
-#define PHASE_SLOT() (void)0
-#define PHASE(k) (void)0
-#endif
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-static constexpr int kThreads = 256;
-static constexpr int kMaxPairs = 8;  // 32-weight blocks per lane per pass
-
-// Byte position of element e (0..31) of a block in the even/odd permuted
-// activation layout that k4_block_dot consumes.
-__device__ __forceinline__ int qx_perm(int e) { return ((e & 1) << 4) | ((e >> 3) << 2) | ((e >> 1) & 3); }
-
-// ---------------------------------------------------------------------------
-// Parity reductions (Mantle's archsimd lane orders)
-
-// Sum of squares exactly as rmsNormAVX512 / rmsNormSIMD / rmsNormScalar do it
-// (internal/backend/simd/ops_avx512.go:92-112, ops_avx2.go:54-77, ops.go:70-76):
-// lane l accumulates fma(x, x, acc) over i = l, l+L, ... (L = 16 / 8), then the L
-// partial sums are added left to right and the scalar tail follows.  Each lane
-// loads 8 operands ahead of its dependent FMA chain.  Whole workgroup; red >= 17 floats.
-__device__ float wg_sumsq_parity(const float* src, int n, int isa, float* red) {
-    const int lanes = isa == kIsaAvx512 ? 16 : (isa == kIsaAvx2 ? 8 : 0);
-    const int nfull = lanes ? (n / lanes) * lanes : 0;
-    const int tid = threadIdx.x;
-    if (lanes && tid < lanes) {
-        float acc = 0.0f;
-        int i = tid;
-        for (; i + 7 * lanes < nfull; i += 8 * lanes) {
-            float v[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = src[i + k * lanes];
-#pragma unroll
-            for (int k = 0; k < 8; k++) acc = __builtin_fmaf(v[k], v[k], acc);
-        }
-        for (; i < nfull; i += lanes) acc = __builtin_fmaf(src[i], src[i], acc);
-        red[tid] = acc;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        if (lanes) {
-            sum = red[0];
-            for (int l = 1; l < lanes; l++) sum += red[l];
-        }
-        int i = nfull;
-        for (; i + 8 <= n; i += 8) {
-            float v[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = src[i + k];
-#pragma unroll
-            for (int k = 0; k < 8; k++) sum += v[k] * v[k];
-        }
-        for (; i < n; i++) sum += src[i] * src[i];
-        red[16] = sum;
-    }
-    __syncthreads();
-    float r = red[16];
-    __syncthreads();
-    return r;
-}
-
-// sum = ((t[0] + t[s]) + t[2s]) + ... in order, loads issued 8 ahead of the adds.
-__device__ __forceinline__ float ordered_sum(const float* t, int stride, int n) {
-    float sum = 0.0f;
-    int b = 0;
-    for (; b + 16 <= n; b += 16) {
-        float v[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) v[k] = t[(b + k) * stride];
-#pragma unroll
-        for (int k = 0; k < 16; k++) sum += v[k];
-    }
-    for (; b < n; b++) sum += t[b * stride];
-    return sum;
-}
-
-// Dot exactly as dotAVX512 / dotSIMD / dotScalar (internal/backend/simd/ops_avx512.go:27-90,
-// ops_avx2.go:25-51, ops.go:49-55).  One thread computes the whole dot.
-// Compile-time length: every accumulator stays in a register.
-template <int N, int ISA>
-__device__ __forceinline__ float dot_parity_t(const float* a, const float* b) {
-    if constexpr (ISA == kIsaAvx512) {
-        float acc[64];
-#pragma unroll
-        for (int k = 0; k < 64; k++) acc[k] = 0.0f;
-        constexpr int n64 = (N / 64) * 64;
-        constexpr int n32 = n64 + ((N - n64) / 32) * 32;
-        constexpr int n16 = n32 + ((N - n32) / 16) * 16;
-#pragma unroll
-        for (int i = 0; i < n64; i += 64)
-#pragma unroll
-            for (int k = 0; k < 64; k++) acc[k] = __builtin_fmaf(a[i + k], b[i + k], acc[k]);
-#pragma unroll
-        for (int i = n64; i < n32; i += 32)
-#pragma unroll
-            for (int k = 0; k < 32; k++) acc[k] = __builtin_fmaf(a[i + k], b[i + k], acc[k]);
-#pragma unroll
-        for (int i = n32; i < n16; i += 16)
-#pragma unroll
-            for (int k = 0; k < 16; k++) acc[k] = __builtin_fmaf(a[i + k], b[i + k], acc[k]);
-        float sum = acc[0];
-#pragma unroll
-        for (int k = 1; k < 64; k++) sum += acc[k];
-#pragma unroll
-        for (int i = n16; i < N; i++) sum += a[i] * b[i];
-        return sum;
-    } else if constexpr (ISA == kIsaAvx2) {
-        float a0[8], a1[8];
-#pragma unroll
-        for (int l = 0; l < 8; l++) { a0[l] = 0.0f; a1[l] = 0.0f; }
-        constexpr int n16 = (N / 16) * 16;
-        constexpr int n8 = n16 + ((N - n16) / 8) * 8;
-#pragma unroll
-        for (int i = 0; i < n16; i += 16) {
-#pragma unroll
-            for (int l = 0; l < 8; l++) {
-                a0[l] = __builtin_fmaf(a[i + l], b[i + l], a0[l]);
-                a1[l] = __builtin_fmaf(a[i + 8 + l], b[i + 8 + l], a1[l]);
-            }
-        }
-#pragma unroll
-        for (int i = n16; i < n8; i += 8)
-#pragma unroll
-            for (int l = 0; l < 8; l++) a0[l] = __builtin_fmaf(a[i + l], b[i + l], a0[l]);
-#pragma unroll
-        for (int l = 0; l < 8; l++) a0[l] = a0[l] + a1[l];
-        float sum = a0[0];
-#pragma unroll
-        for (int l = 1; l < 8; l++) sum += a0[l];
-#pragma unroll
-        for (int i = n8; i < N; i++) sum += a[i] * b[i];
-        return sum;
-    } else {
-        float sum = 0.0f;
-#pragma unroll 16
-        for (int i = 0; i < N; i++) sum += a[i] * b[i];
-        return sum;
-    }
-}
-
-// Runtime-length version (any n), same orders; used off the common head dims.
-__device__ float dot_parity_n(const float* a, const float* b, int n, int isa) {
-    if (isa == kIsaAvx512) {
-        if (n == 0) return 0.0f;
-        float acc[4][16];
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int l = 0; l < 16; l++) acc[j][l] = 0.0f;
-        int i = 0;
-        for (; i + 64 <= n; i += 64) {
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int l = 0; l < 16; l++) acc[j][l] = __builtin_fmaf(a[i + 16 * j + l], b[i + 16 * j + l], acc[j][l]);
-        }
-        for (; i + 32 <= n; i += 32) {
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int l = 0; l < 16; l++) acc[j][l] = __builtin_fmaf(a[i + 16 * j + l], b[i + 16 * j + l], acc[j][l]);
-        }
-        for (; i + 16 <= n; i += 16) {
-#pragma unroll
-            for (int l = 0; l < 16; l++) acc[0][l] = __builtin_fmaf(a[i + l], b[i + l], acc[0][l]);
-        }
-        float sum = acc[0][0];
-#pragma unroll
-        for (int k = 1; k < 64; k++) sum += acc[k / 16][k % 16];
-        for (; i < n; i++) sum += a[i] * b[i];
-        return sum;
-    }
-    if (isa == kIsaAvx2) {
-        if (n == 0) return 0.0f;
-        float a0[8], a1[8];
-#pragma unroll
-        for (int l = 0; l < 8; l++) { a0[l] = 0.0f; a1[l] = 0.0f; }
-        int i = 0;
-        for (; i + 16 <= n; i += 16) {
-#pragma unroll
-            for (int l = 0; l < 8; l++) {
-                a0[l] = __builtin_fmaf(a[i + l], b[i + l], a0[l]);
-                a1[l] = __builtin_fmaf(a[i + 8 + l], b[i + 8 + l], a1[l]);
-            }
-        }
-        if (i + 8 <= n) {
-#pragma unroll
-            for (int l = 0; l < 8; l++) a0[l] = __builtin_fmaf(a[i + l], b[i + l], a0[l]);
-            i += 8;
-        }
-#pragma unroll
-        for (int l = 0; l < 8; l++) a0[l] = a0[l] + a1[l];
-        float sum = a0[0];
-#pragma unroll
-        for (int l = 1; l < 8; l++) sum += a0[l];
-        for (; i < n; i++) sum += a[i] * b[i];
-        return sum;
-    }
-    float sum = 0.0f;
-    for (int i = 0; i < n; i++) sum += a[i] * b[i];
-    return sum;
-}
-
-__device__ __forceinline__ float dot_parity(const float* a, const float* b, int n, int isa) {
-    if (n == 128) {
-        if (isa == kIsaAvx512) return dot_parity_t<128, kIsaAvx512>(a, b);
-        if (isa == kIsaAvx2) return dot_parity_t<128, kIsaAvx2>(a, b);
-        return dot_parity_t<128, kIsaScalar>(a, b);
-    }
-    if (n == 64) {
-        if (isa == kIsaAvx512) return dot_parity_t<64, kIsaAvx512>(a, b);
-        if (isa == kIsaAvx2) return dot_parity_t<64, kIsaAvx2>(a, b);
-        return dot_parity_t<64, kIsaScalar>(a, b);
-    }
-    return dot_parity_n(a, b, n, isa);
-}
-
-// ---------------------------------------------------------------------------
-// Activation quantiser (+ optional RMSNorm), one workgroup per row.
-
-// Load 16 values (half h of block b) of x, and of the gains when weight != null.
-__device__ __forceinline__ void load_half16(const float* __restrict__ x, const float* __restrict__ weight, int n,
-                                            int base, bool vec4, float (&v)[16], float (&g)[16]) {
-    if (vec4 && base + 16 <= n) {
-        const float4* x4 = reinterpret_cast<const float4*>(x + base);
-        const float4* w4 = reinterpret_cast<const float4*>(weight + base);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float4 t = x4[k];
-            v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w;
-            if (weight) {
-                const float4 u = w4[k];
-                g[4 * k] = u.x; g[4 * k + 1] = u.y; g[4 * k + 2] = u.z; g[4 * k + 3] = u.w;
-            }
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int idx = base + k;
-            v[k] = idx < n ? x[idx] : 0.0f;
-            if (weight) g[k] = idx < n ? weight[idx] : 0.0f;
-        }
-    }
-}
-
-// Stage one activation vector as Mantle's W4A8 operand: optional RMSNorm
-// (weight != null), then per-32-block int8 quantisation (quantizeVecBlocksInto,
-// internal/backend/simd/matvec_quant.go:746-797).  Two adjacent lanes own one
-// 32-element block (16 values each, loaded once up front); the block max is
-// one lane-pair exchange (max is exact in any order).  The RMS sum of squares
-// runs on 16 / 8 lanes in Mantle's lane-striped order over an LDS copy (vals,
-// ceil32(n) floats, only touched with weight).  Whole workgroup; red >= 17
-// floats; q_out / s_out may be LDS or global (q_out in the even/odd permuted
-// layout: dword j of the first 16 bytes holds elements 8j+0,2,4,6, of the
-// second 16 bytes elements 8j+1,3,5,7).
-// First-trip loads of wg_quantize_vec (this lane's 16 values and gains), so a
-// caller can put them in flight ahead of its own, larger loads.
-__device__ __forceinline__ void wg_quantize_vec_load(const float* __restrict__ x, const float* __restrict__ weight,
-                                                     int n, float (&v)[16], float (&g)[16]) {
-    const int halves = ((n + 31) >> 5) * 2;
-    const bool vec4 = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0;
-    if ((int)threadIdx.x < halves) load_half16(x, weight, n, threadIdx.x * 16, vec4, v, g);
-}
-
-template <int NT = kThreads>
-__device__ void wg_quantize_vec_pre(const float* __restrict__ x, const float* __restrict__ weight, float eps, int n,
-                                    int isa, float* vals, float* red, int8_t* q_out, float* s_out, float* norm_out,
-                                    float (&v)[16], float (&g)[16]) {
-    const int tid = threadIdx.x;
-    const int halves = ((n + 31) >> 5) * 2;
-    const bool vec4 = (n & 3) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0;
-    float scale = 1.0f;
-    if (weight) {
-        if (halves <= NT) {
-            if (tid < halves) {
-                float4* d4 = reinterpret_cast<float4*>(vals + tid * 16);
-#pragma unroll
-                for (int k = 0; k < 4; k++) d4[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-            }
-        } else {
-            for (int i = tid; i < halves * 16; i += NT) vals[i] = i < n ? x[i] : 0.0f;
-        }
-        __syncthreads();
-        const int lanes = isa == kIsaAvx512 ? 16 : (isa == kIsaAvx2 ? 8 : 0);
-        const int nfull = lanes ? (n / lanes) * lanes : 0;
-        if (lanes && tid < lanes) {
-            float acc = 0.0f;
-            int i = tid;
-            for (; i + 15 * lanes < nfull; i += 16 * lanes) {
-                float t[16];
-#pragma unroll
-                for (int k = 0; k < 16; k++) t[k] = vals[i + k * lanes];
-#pragma unroll
-                for (int k = 0; k < 16; k++) acc = __builtin_fmaf(t[k], t[k], acc);
-            }
-            for (; i < nfull; i += lanes) acc = __builtin_fmaf(vals[i], vals[i], acc);
-            red[tid] = acc;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
-            if (lanes) {
-                sum = red[0];
-                for (int l = 1; l < lanes; l++) sum += red[l];
-            }
-            for (int i = nfull; i < n; i++) sum += vals[i] * vals[i];
-            red[16] = rms_scale(sum, n, eps);
-        }
-        __syncthreads();
-        scale = red[16];
-    }
-    // halves is even and NT a multiple of 2: both lanes of a pair take the same trips.
-    for (int hh = tid; hh < ((halves + NT - 1) / NT) * NT; hh += NT) {
-        const bool live = hh < halves;
-        const int base = hh * 16;
-        if (hh != tid && live) load_half16(x, weight, n, base, vec4, v, g);
-        if (live && weight) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) v[k] = (v[k] * scale) * g[k];
-        }
-        if (live && norm_out)
-            for (int k = 0; k < 16 && base + k < n; k++) norm_out[base + k] = v[k];
-        float m = 0.0f;
-        if (live) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float a = v[k] < 0 ? -v[k] : v[k];
-                m = a > m ? a : m;
-            }
-        }
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        if (!live) continue;
-        uint32_t we[2] = {0, 0}, wo[2] = {0, 0};
-        float sc = 0.0f;
-        if (m != 0.0f) {
-            sc = m / 127.0f;
-            const float inv = 1.0f / sc;
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                int32_t q = go_round(v[k] * inv);
-                q = q > 127 ? 127 : (q < -127 ? -127 : q);
-                const uint32_t byte = (uint32_t)(uint8_t)(int8_t)q;
-                // element e = 16*half + k of the block: dword (e>>3) of the even/odd half
-                const int dw = (k >> 3), sh = ((k >> 1) & 3) * 8;
-                if (k & 1) wo[dw] |= byte << sh; else we[dw] |= byte << sh;
-            }
-        }
-        const int blk = hh >> 1, half = hh & 1;
-        uint2* qb = reinterpret_cast<uint2*>(q_out + blk * 32);
-        qb[half] = make_uint2(we[0], we[1]);      // even lanes: bytes 8*half .. +7
-        qb[2 + half] = make_uint2(wo[0], wo[1]);  // odd lanes: bytes 16 + 8*half .. +7
-        if (half == 0) s_out[blk] = sc;
-    }
-    __syncthreads();
-}
-
-template <int NT = kThreads>
-__device__ void wg_quantize_vec(const float* __restrict__ x, const float* __restrict__ weight, float eps, int n,
-                                int isa, float* vals, float* red, int8_t* q_out, float* s_out, float* norm_out) {
-    float v[16], g[16];
-    wg_quantize_vec_load(x, weight, n, v, g);
-    wg_quantize_vec_pre<NT>(x, weight, eps, n, isa, vals, red, q_out, s_out, norm_out, v, g);
-}
 
 __global__ __launch_bounds__(kThreads) void quantize_vec_kernel(const float* __restrict__ x, const float* __restrict__ weight,
                                                                   float eps, int n, int isa, int8_t* __restrict__ qx,
@@ -460,42 +87,6 @@ K4Mat k4_mat_from_payload(const uint8_t* payload, int rows, int cols) {
     m.nib = payload + data_off;
     m.rows = rows;
     return m;
-}
-
-struct GemvParams {
-    K4Mat mats[3];
-    float* outs[3];
-    int wg_begin[4];  // first tile of each matrix
-    int ntiles;
-    int nmat;
-    int cols, bpr, spr, rpw, batch;
-    const int8_t* qx;
-    const float* xs;
-    const float* x;       // W4A32 / in-kernel-quantised fp32 input [batch][cols]
-    const float* norm_w;  // RMSNorm gains applied before quantisation (nullable)
-    float eps;
-    int isa;
-    unsigned long long* key;
-};
-
-// kModeW4A8: activation already quantised (qx/xs); kModeW4A32: fp32 activation
-// used as is; kModeW4A8Fused: every workgroup quantises the fp32 activation
-// itself (after RMSNorm when norm_w is set) while its weight loads are in flight.
-// Selects instead of a dynamic index into the by-value kernel argument: an
-// indexed p.mats[k] would make the compiler copy the whole struct to scratch.
-__device__ __forceinline__ K4Mat pick_mat(const GemvParams& p, int k) {
-    return k == 0 ? p.mats[0] : (k == 1 ? p.mats[1] : p.mats[2]);
-}
-__device__ __forceinline__ float* pick_out(const GemvParams& p, int k) {
-    return k == 0 ? p.outs[0] : (k == 1 ? p.outs[1] : p.outs[2]);
-}
-
-enum GemvMode : int { kModeW4A8 = 0, kModeW4A32 = 1, kModeW4A8Fused = 2 };
-
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-    uint32_t u = __float_as_uint(v);
-    uint32_t s = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)s << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
 template <int MODE, int EPI>
@@ -695,261 +286,6 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvParams p) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// k4 GEMV, lane-chain form (rows whose block count is 8 * BPL).
-//
-// Eight lanes own one output row; lane j holds blocks [j*BPL, (j+1)*BPL) of
-// it in registers (BPL 128-bit nibble loads; the 8 lanes of a row cover its
-// bytes contiguously).  The CPU's ordered block sum ((t0 + t1) + t2) + ... is
-// kept exactly: lane j adds its own terms in order after receiving the running
-// sum of lane j-1 through a DPP row_shr:1 move -- seven hand-offs, no LDS and
-// no barrier.  A 256-lane workgroup covers 32 rows per unit and keeps two
-// units of weight loads in flight while it computes.
-
-__device__ __forceinline__ float dpp_shr1(float v) {  // lane i <- lane i-1 (within 16; lane 0 of a row gets 0)
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float dpp_shl7(float v) {  // lane i <- lane i+7 (within 16): j=0 <- j=7 of its group
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x107, 0xF, 0xF, true));
-}
-template <int K>
-__device__ __forceinline__ float dpp_shr(float v) {  // lane i <- lane i-K within its row of 16 (K = 1..15)
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + K, 0xF, 0xF, true));
-}
-
-// Gather the 8 lanes' value of one row group into lane j == 7: lane 7 receives
-// lane jj's value through a DPP row_shr:(7-jj) move.
-template <int JJ>
-__device__ __forceinline__ float from_lane(float v) {
-    if constexpr (JJ == 7) return v;
-    else return dpp_shr<7 - JJ>(v);
-}
-
-// Lane j of a row's 8 lanes owns blocks j, j+8, j+16, ... (BPL of them): each
-// load instruction of the 8 lanes reads 128 contiguous bytes of the row.  The
-// CPU's ordered block sum walks the lanes cyclically: block b is added by lane
-// b % 8 to the running sum it receives from lane (b-1) % 8 (DPP row_shr:1, and
-// row_shl:7 for the wrap from lane 7 to lane 0).
-template <int EPI, int BPL, int NB, int NW>
-__global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int NT = NW * 64;
-    constexpr int NSUB = EPI == kEpiSiluMul ? 2 : 1;
-    constexpr int RPU = 8 * NW;  // rows per unit
-    constexpr int NQ = BPL / 4;  // u32 words of u6 bytes per lane (bytes j*BPL .. j*BPL+BPL-1 of the row)
-    constexpr int NS = BPL / 2;  // u32 words of f16 super-scales per row (BPL supers)
-    const int bpr = 8 * BPL;
-    int8_t* sq = reinterpret_cast<int8_t*>(smem);
-    float* sxs = reinterpret_cast<float*>(smem + NB * bpr * 32);
-    float* work = sxs + NB * bpr;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int j = lane & 7;
-    const int gbase = lane & ~7;                    // first lane of this row's group
-    const int rsub = (tid >> 6) * 8 + (lane >> 3);  // row within the unit
-
-    struct Unit {
-        uint4 w[NSUB][BPL];    // nibbles of blocks j, j+8, ...
-        uint32_t sub[NSUB][NQ];
-        uint32_t sup[NSUB][NS];
-        int unit, ms, row;
-        float resid;
-    };
-    auto load_unit = [&](Unit& R, int unit) {
-        R.unit = unit;
-        int ms = 0, first = 0;
-        if (EPI != kEpiSiluMul) {
-            if (p.nmat > 1 && unit >= p.wg_begin[1]) { ms = 1; first = p.wg_begin[1]; }
-            if (p.nmat > 2 && unit >= p.wg_begin[2]) { ms = 2; first = p.wg_begin[2]; }
-        }
-        R.ms = ms;
-        const int row = (unit - first) * RPU + rsub;
-        R.row = row;
-#pragma unroll
-        for (int k = 0; k < NSUB; k++) {
-            const K4Mat M = pick_mat(p, NSUB == 2 ? k : ms);
-            const bool ok = row < M.rows;
-            const size_t r0 = (size_t)row * bpr;
-#pragma unroll
-            for (int q = 0; q < BPL; q++) {
-                u32x4 v = {0, 0, 0, 0};
-                if (ok) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(M.nib) + r0 + j + 8 * q);
-                R.w[k][q] = make_uint4(v.x, v.y, v.z, v.w);
-            }
-            const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + r0 + j * BPL);
-            const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + (size_t)row * BPL);
-#pragma unroll
-            for (int m = 0; m < NQ; m++) R.sub[k][m] = ok ? sw[m] : 0u;
-#pragma unroll
-            for (int m = 0; m < NS; m++) R.sup[k][m] = ok ? su[m] : 0u;
-        }
-        R.resid = 0.0f;
-        if (EPI == kEpiResAdd && j == 7 && row < p.mats[0].rows) R.resid = p.outs[0][row];
-    };
-    // u6 byte of block b = j + 8q: held by lane b / BPL of the group, word (b % BPL) / 4.
-    auto sub_byte = [&](const Unit& R, int k, int q) -> uint32_t {
-        const int b = j + 8 * q;
-        const int src = gbase + b / BPL;
-        const int wi = (b % BPL) >> 2;
-        uint32_t got = 0;
-#pragma unroll
-        for (int m = 0; m < NQ; m++) {
-            const uint32_t v = (uint32_t)__shfl((int)R.sub[k][m], src, 64);
-            got = m == wi ? v : got;
-        }
-        return (got >> (8 * (b & 3))) & 0xFFu;
-    };
-    // Ordered row sum of matrix k, batch column bi; valid in lane j == 7.
-    auto row_sum = [&](const Unit& R, int k, int bi) -> float {
-        float t[BPL];
-#pragma unroll
-        for (int q = 0; q < BPL; q++) {
-            const int b = j + 8 * q;
-            const uint32_t supw = R.sup[k][q >> 1];
-            const float sw = k4_scale((uint16_t)((q & 1) ? (supw >> 16) : (supw & 0xFFFFu)), (uint8_t)sub_byte(R, k, q));
-            const float xsv = sxs[bi * bpr + b];
-            float term = 0.0f;
-            if (sw != 0.0f && xsv != 0.0f) {
-                const int8_t* xb = sq + (bi * bpr + b) * 32;
-                const uint4 xe = *reinterpret_cast<const uint4*>(xb);
-                const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
-                term = (float)k4_block_dot(R.w[k][q], xe, xo) * (sw * xsv);
-            }
-            t[q] = term;
-        }
-        // Block b = jj + 8q lives in lane jj: lane 7 gathers them and adds in block order.
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < BPL; q++) {
-            s = s + from_lane<0>(t[q]);
-            s = s + from_lane<1>(t[q]);
-            s = s + from_lane<2>(t[q]);
-            s = s + from_lane<3>(t[q]);
-            s = s + from_lane<4>(t[q]);
-            s = s + from_lane<5>(t[q]);
-            s = s + from_lane<6>(t[q]);
-            s = s + from_lane<7>(t[q]);
-        }
-        return s;
-    };
-
-    const int G = (int)gridDim.x;
-    Unit A, Bq;
-    PHASE_SLOT();
-    PHASE(0);
-    // Activation loads first: they must not queue behind the weight stream.
-    float pv[16], pg[16];
-    uint4 qpre[4];
-    const int qbytes = NB * bpr * 32;
-    if (p.qx) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = (tid + r * NT) * 16;
-            if (i < qbytes) qpre[r] = *reinterpret_cast<const uint4*>(p.qx + i);
-        }
-    } else if (NB == 1) {
-        wg_quantize_vec_load(p.x, p.norm_w, p.cols, pv, pg);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight stream
-    load_unit(A, blockIdx.x);
-    const bool two = (int)blockIdx.x + G < p.ntiles;
-    if (two) load_unit(Bq, blockIdx.x + G);
-    if (p.qx) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = (tid + r * NT) * 16;
-            if (i < qbytes) *reinterpret_cast<uint4*>(sq + i) = qpre[r];
-        }
-        for (int i = (tid + 4 * NT) * 16; i < qbytes; i += NT * 16)
-            *reinterpret_cast<uint4*>(sq + i) = *reinterpret_cast<const uint4*>(p.qx + i);
-        for (int i = tid; i < NB * bpr; i += NT) sxs[i] = p.xs[i];
-        __syncthreads();
-    } else if (NB == 1) {
-        wg_quantize_vec_pre<NT>(p.x, p.norm_w, p.eps, p.cols, p.isa, work, work + bpr * 32, sq, sxs, nullptr, pv, pg);
-    } else {
-        for (int bi = 0; bi < NB; bi++)
-            wg_quantize_vec<NT>(p.x + (size_t)bi * p.cols, p.norm_w, p.eps, p.cols, p.isa, work, work + bpr * 32,
-                                sq + bi * bpr * 32, sxs + bi * bpr, nullptr);
-    }
-    PHASE(1);
-    unsigned long long best = 0;
-    int nstep = 0;
-    auto step = [&](Unit& cur) {
-        float res[NSUB][NB];
-#pragma unroll
-        for (int k = 0; k < NSUB; k++)
-#pragma unroll
-            for (int bi = 0; bi < NB; bi++) res[k][bi] = row_sum(cur, k, bi);
-        const int row = cur.row, ms = cur.ms;
-        const float resid = cur.resid;
-        const int ahead = cur.unit + 2 * G;
-        if (ahead < p.ntiles) load_unit(cur, ahead);  // refill while the results are written
-        else cur.unit = -1;
-        nstep++;
-        if (nstep <= 6) PHASE(1 + nstep);
-        if (j != 7) return;
-        if (EPI == kEpiSiluMul) {
-            if (row < p.mats[0].rows) p.outs[0][row] = fast_silu_vec(res[0][0]) * res[1][0];
-        } else {
-            const int rows = pick_mat(p, ms).rows;
-            if (row >= rows) return;
-            float* out = pick_out(p, ms);
-            if (EPI == kEpiResAdd) {
-                out[row] = resid + res[0][0];
-            } else {
-#pragma unroll
-                for (int bi = 0; bi < NB; bi++) out[(size_t)bi * rows + row] = res[0][bi];
-                if (EPI == kEpiArgmax) {
-                    const unsigned long long key = argmax_key(res[0][0], row);
-                    best = key > best ? key : best;
-                }
-            }
-        }
-    };
-    step(A);
-    if (two) {
-        while (true) {
-            step(Bq);
-            if (A.unit < 0) break;
-            step(A);
-            if (Bq.unit < 0) break;
-        }
-    }
-    if (EPI == kEpiArgmax) {
-        __shared__ unsigned long long red[NW];
-        for (int off = 32; off > 0; off >>= 1) {
-            unsigned long long o = __shfl_down(best, off, 64);
-            best = o > best ? o : best;
-        }
-        if ((tid & 63) == 0) red[tid >> 6] = best;
-        __syncthreads();
-        if (tid == 0) {
-            unsigned long long m = red[0];
-            for (int i = 1; i < NW; i++) m = red[i] > m ? red[i] : m;
-            atomicMax(p.key, m);
-        }
-    }
-}
-
-// Workgroups of kernel `fn` (with `smem` bytes of LDS) that fit on the whole
-// device at once; cached per kernel instance and LDS size class.
-template <typename K>
-static int resident_wgs(K fn, size_t smem) {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn), kThreads, smem) !=
-            hipSuccess ||
-        per_cu <= 0)
-        per_cu = 1;
-    return per_cu * cus;
-}
-
 // Rows per tile: the fewest rows that still give one tile per resident
 // workgroup (small matrices are latency-bound: spread them out), capped by the
 // 256 lanes x 8 blocks a single load pass covers and by the LDS budget.
@@ -960,30 +296,6 @@ static int choose_rpw(int total_rows, int bpr, int nsub, int batch, size_t fixed
     int rpw = (total_rows + slots - 1) / slots;
     if (rpw < 1) rpw = 1;
     return rpw < rmax ? rpw : rmax;
-}
-
-static bool lane_gemv_disabled() {
-    static bool v = [] {
-        const char* e = getenv("MANTLE_HIP_GEMV_TILES");
-        return e && atoi(e) != 0;
-    }();
-    return v;
-}
-
-static int lane_small_rows() {
-    static int v = [] {
-        const char* e = getenv("MANTLE_HIP_GEMV_SMALL_ROWS");
-        return e ? atoi(e) : 16384;
-    }();
-    return v;
-}
-
-static int gemv_max_wgs() {
-    static int v = [] {
-        const char* e = getenv("MANTLE_HIP_GEMV_MAX_WGS");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
 }
 
 template <int MODE, int EPI>
@@ -1024,71 +336,25 @@ static hipError_t launch_gemv_epi(GemvParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int EPI, int BPL, int NB, int NW>
-static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
-    auto kern = k4_gemv_lane_kernel<EPI, BPL, NB, NW>;
-    constexpr int RPU = 8 * NW;
-    const size_t stage = p.norm_w ? ((size_t)p.bpr * 32 + 17) * 4 : 17 * 4;
-    const size_t smem = (size_t)NB * p.bpr * 36 + stage;
-    if (smem > 64 * 1024) return hipErrorInvalidValue;
-    int units = 0;
-    if (EPI == kEpiSiluMul) {
-        p.wg_begin[0] = 0;
-        units = (p.mats[0].rows + RPU - 1) / RPU;
-    } else {
-        for (int i = 0; i < p.nmat; i++) {
-            p.wg_begin[i] = units;
-            units += (p.mats[i].rows + RPU - 1) / RPU;
-        }
-    }
-    p.wg_begin[p.nmat] = units;
-    p.ntiles = units;
-    p.rpw = RPU;
-    int slots = resident_wgs(kern, smem);
-    if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
-    const int per = (units + slots - 1) / slots;
-    const int grid = (units + per - 1) / per;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), smem, stream, p);
-    return hipGetLastError();
-}
-
-// Small matrices (latency-bound): one-wave workgroups, 8 rows each, so many
-// CUs share the few MB.  Large ones: four-wave workgroups streaming many units.
-template <int EPI, int BPL, int NB>
-static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
-    int rows = 0;
-    for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
-    if (rows <= lane_small_rows()) return launch_lane_gemv<EPI, BPL, NB, 1>(p, stream);
-    return launch_lane_gemv<EPI, BPL, NB, 4>(p, stream);
-}
-
-template <int EPI, int NB>
-static hipError_t try_lane_gemv(GemvParams& p, hipStream_t stream, bool* used) {
-    *used = true;
-    switch (p.bpr) {
-        case 32: return launch_lane_gemv_sized<EPI, 4, NB>(p, stream);
-        case 64: return launch_lane_gemv_sized<EPI, 8, NB>(p, stream);
-        case 96: return launch_lane_gemv_sized<EPI, 12, NB>(p, stream);
-        default: *used = false; return hipSuccess;
-    }
-}
-
-// Lane-chain kernel for the shapes it is instantiated for, else the tile kernel.
+// Lane-chain kernel for the shapes and prologue / epilogue pairs it is
+// instantiated for, else the tile kernel.  In-kernel quantisation reads x (and
+// the gains) as float4: both must be 16-byte aligned.
 static hipError_t dispatch_lane_gemv(GemvParams& p, GemvEpi epi, hipStream_t stream, bool* used) {
     *used = false;
     if (lane_gemv_disabled() || p.cols != p.bpr * 32) return hipSuccess;
-    if (p.batch == 1) {
-        switch (epi) {
-            case kEpiStore: return try_lane_gemv<kEpiStore, 1>(p, stream, used);
-            case kEpiResAdd: return try_lane_gemv<kEpiResAdd, 1>(p, stream, used);
-            case kEpiSiluMul: return try_lane_gemv<kEpiSiluMul, 1>(p, stream, used);
-            case kEpiArgmax: return try_lane_gemv<kEpiArgmax, 1>(p, stream, used);
-            default: return hipSuccess;
-        }
+    int pro = kProQx;
+    if (!p.qx) {
+        if (((uintptr_t)p.x | (uintptr_t)p.norm_w) & 15) return hipSuccess;
+        pro = p.norm_w ? kProNorm : kProQuant;
     }
-    if (p.batch == 8 && epi == kEpiStore) return try_lane_gemv<kEpiStore, 8>(p, stream, used);
+    if (p.batch == 1) {
+        if (epi == kEpiStore) return lane_gemv_store(p, pro, stream, used);
+        return lane_gemv_fused(p, epi, pro, stream, used);
+    }
+    if (p.batch == 8 && epi == kEpiStore) return lane_gemv_batch8(p, pro, stream, used);
     return hipSuccess;
 }
+
 
 template <int MODE>
 static hipError_t launch_gemv(GemvParams& p, GemvEpi epi, hipStream_t stream) {
@@ -1628,10 +894,33 @@ hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, in
 }  // namespace mantle
 
 #ifdef MANTLE_PHASE_TRACE
+namespace mantle {
+MANTLE_PHASE_READER(phase_read_kernels)
+int phase_read_lane_store(unsigned long long*, int, unsigned*);
+int phase_read_lane_fused(unsigned long long*, int, unsigned*);
+int phase_read_lane_b8(unsigned long long*, int, unsigned*);
+}  // namespace mantle
+// All translation units' stamps, ordered by launch start.
 extern "C" int mantleHipDebugPhaseTrace(unsigned long long* out, int max_slots, unsigned* n) {
-    hipError_t e = hipMemcpyFromSymbol(n, HIP_SYMBOL(mantle::g_phase_n), sizeof(unsigned));
-    if (e != hipSuccess) return e;
-    int k = (int)(*n < (unsigned)max_slots ? *n : (unsigned)max_slots);
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(mantle::g_phase), sizeof(unsigned long long) * 8 * k);
+    int (*readers[])(unsigned long long*, int, unsigned*) = {mantle::phase_read_kernels, mantle::phase_read_lane_store,
+                                                             mantle::phase_read_lane_fused, mantle::phase_read_lane_b8};
+    std::vector<std::array<unsigned long long, 8>> rows;
+    for (auto rd : readers) {
+        std::vector<unsigned long long> buf((size_t)8192 * 8);
+        unsigned k = 0;
+        int e = rd(buf.data(), 8192, &k);
+        if (e) return e;
+        for (unsigned i = 0; i < k && i < 8192; i++) {
+            std::array<unsigned long long, 8> r;
+            for (int c = 0; c < 8; c++) r[c] = buf[i * 8 + c];
+            rows.push_back(r);
+        }
+    }
+    std::sort(rows.begin(), rows.end(), [](const auto& a, const auto& b) { return a[0] < b[0]; });
+    const size_t m = rows.size() < (size_t)max_slots ? rows.size() : (size_t)max_slots;
+    for (size_t i = 0; i < m; i++)
+        for (int c = 0; c < 8; c++) out[i * 8 + c] = rows[i][c];
+    *n = (unsigned)m;
+    return 0;
 }
 #endif

@@ -8,6 +8,11 @@ import numpy as np
 TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=128, ffn=512, vocab=3000,
             rope_base=1e6, eps=1e-6, tie_embeddings=1)
 
+# Two blocks at Qwen3-0.6B's row widths (1024 / 2048 / 3072 columns): every
+# GEMV of the step takes the lane-chain kernel, with its fused RMSNorm.
+LANE = dict(n_layers=2, d_model=1024, n_heads=16, n_kv_heads=8, head_dim=128, ffn=3072, vocab=2048,
+            rope_base=1e6, eps=1e-6, tie_embeddings=1)
+
 
 def pack(path: str, seed: int, cfg: dict) -> str:
     from mantle_amd import mcf

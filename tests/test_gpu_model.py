@@ -15,22 +15,33 @@ def tiny_path(tmp_models):
     return models.pack(str(tmp_models / "tiny.mcf"), 0, models.TINY)
 
 
-@pytest.mark.parametrize("isa", ["avx512", "avx2"])
-def test_tiny_greedy_logits_bitexact(hip, tiny_path, isa):
+@pytest.fixture(scope="module")
+def lane_path(tmp_models):
+    return models.pack(str(tmp_models / "lane.mcf"), 3, models.LANE)
+
+
+@pytest.mark.parametrize("isa", ["avx512", "avx2", "scalar"])
+@pytest.mark.parametrize("shape", ["tiny", "lane"])
+def test_greedy_logits_bitexact(hip, tiny_path, lane_path, shape, isa):
+    """Every step's logits and residual stream bit-identical to the oracle in
+    each of Mantle's three reduction orders; "tiny" runs the tile GEMV, "lane"
+    (1024-wide rows) the lane-chain GEMV with its fused RMSNorm prologue."""
     import mantle_amd
-    isa_id = {"avx512": 2, "avx2": 1}[isa]
-    rt = mantle_amd.new_backend("hip").load_model(tiny_path, max_context=96, parity_isa=isa)
-    om = models.oracle_model(tiny_path, models.TINY, 96, isa_id)
+    isa_id = {"avx512": 2, "avx2": 1, "scalar": 0}[isa]
+    path, cfg = (tiny_path, models.TINY) if shape == "tiny" else (lane_path, models.LANE)
+    rt = mantle_amd.new_backend("hip").load_model(path, max_context=96, parity_isa=isa)
+    om = models.oracle_model(path, cfg, 96, isa_id)
+    steps = 40 if shape == "tiny" else 12
     try:
         tok = 17
-        for step in range(40):
+        for step in range(steps):
             logits = rt.forward_token(tok)
             nxt, want = om.forward_greedy(tok, want_logits=True)
             np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
             np.testing.assert_array_equal(rt.hidden().view(np.uint32), om.hidden().view(np.uint32))
             assert int(np.argmax(logits)) == nxt
             tok = nxt
-        assert rt.pos == 40
+        assert rt.pos == steps
     finally:
         rt.close()
         om.close()
