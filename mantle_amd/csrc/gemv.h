@@ -25,6 +25,8 @@ struct GemvParams {
     float eps;
     int isa;
     unsigned long long* key;
+    int8_t* q_out;   // kEpiSiluMul: output also quantised (32-row units) ...
+    float* q_scale;  // ... with these block scales
 };
 
 // kModeW4A8: activation already quantised (qx/xs); kModeW4A32: fp32 activation
@@ -81,6 +83,15 @@ static inline int lane_small_rows() {
     static int v = [] {
         const char* e = getenv("MANTLE_HIP_GEMV_SMALL_ROWS");
         return e ? atoi(e) : 16384;
+    }();
+    return v;
+}
+
+// Lanes per row of the lane GEMV on small matrices (8 or 16).
+static inline int lane_small_lpr() {
+    static int v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_SMALL_LPR");
+        return e && atoi(e) == 8 ? 8 : 16;
     }();
     return v;
 }

@@ -9,60 +9,61 @@
 namespace mantle {
 
 // ---------------------------------------------------------------------------
-// k4 GEMV, lane-chain form (rows whose block count is 8 * BPL).
+// k4 GEMV, lane-group form.
 //
-// Eight lanes own one output row; lane j holds blocks [j*BPL, (j+1)*BPL) of
-// it in registers (BPL 128-bit nibble loads; the 8 lanes of a row cover its
-// bytes contiguously).  The CPU's ordered block sum ((t0 + t1) + t2) + ... is
-// kept exactly: lane j adds its own terms in order after receiving the running
-// sum of lane j-1 through a DPP row_shr:1 move -- seven hand-offs, no LDS and
-// no barrier.  A 256-lane workgroup covers 32 rows per unit and keeps two
-// units of weight loads in flight while it computes.
+// LPR lanes (8 or 16) own one output row; lane j holds blocks j, j+LPR,
+// j+2*LPR, ... (BPL of them) in registers, so each load instruction of a row's
+// lanes reads LPR*16 contiguous nibble bytes.  The CPU's ordered block sum
+// ((t0 + t1) + t2) + ... is kept exactly: the row's last lane gathers every
+// term through DPP row_shr moves (all LPR lanes sit in one 16-lane DPP row)
+// and adds them in block order -- no LDS, no barrier.  Eight lanes per row
+// keep the load count per row low for large matrices; sixteen halve the loads
+// each wave must issue, which is what bounds the latency of small ones.
 
-__device__ __forceinline__ float dpp_shr1(float v) {  // lane i <- lane i-1 (within 16; lane 0 of a row gets 0)
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float dpp_shl7(float v) {  // lane i <- lane i+7 (within 16): j=0 <- j=7 of its group
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x107, 0xF, 0xF, true));
-}
 template <int K>
 __device__ __forceinline__ float dpp_shr(float v) {  // lane i <- lane i-K within its row of 16 (K = 1..15)
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + K, 0xF, 0xF, true));
 }
 
-// Gather the 8 lanes' value of one row group into lane j == 7: lane 7 receives
-// lane jj's value through a DPP row_shr:(7-jj) move.
-template <int JJ>
+// Lane LPR-1 of a row group receives lane JJ's value (DPP row_shr:(LPR-1-JJ)).
+template <int JJ, int LPR>
 __device__ __forceinline__ float from_lane(float v) {
-    if constexpr (JJ == 7) return v;
-    else return dpp_shr<7 - JJ>(v);
+    if constexpr (JJ == LPR - 1) return v;
+    else return dpp_shr<LPR - 1 - JJ>(v);
 }
 
-// Lane j of a row's 8 lanes owns blocks j, j+8, j+16, ... (BPL of them): each
-// load instruction of the 8 lanes reads 128 contiguous bytes of the row.  The
-// CPU's ordered block sum walks the lanes cyclically: block b is added by lane
-// b % 8 to the running sum it receives from lane (b-1) % 8 (DPP row_shr:1, and
-// row_shl:7 for the wrap from lane 7 to lane 0).
-template <int EPI, int BPL, int NB, int NW, int PRO>
+template <int LPR, int JJ = 0>
+__device__ __forceinline__ float gather_add(float s, float t) {
+    if constexpr (JJ == LPR) return s;
+    else return gather_add<LPR, JJ + 1>(s + from_lane<JJ, LPR>(t), t);
+}
+
+template <int EPI, int LPR, int BPL, int NB, int NW, int PRO>
 __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
+    static_assert(LPR == 8 || LPR == 16, "8 or 16 lanes per row");
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NT = NW * 64;
     constexpr int NSUB = EPI == kEpiSiluMul ? 2 : 1;
-    constexpr int RPU = 8 * NW;  // rows per unit
-    constexpr int NQ = BPL / 4;  // u32 words of u6 bytes per lane (bytes j*BPL .. j*BPL+BPL-1 of the row)
-    constexpr int NS = BPL / 2;  // u32 words of f16 super-scales per row (BPL supers)
-    const int bpr = 8 * BPL;
+    constexpr int RPW = 64 / LPR;   // rows per wave
+    constexpr int RPU = RPW * NW;   // rows per unit
+    constexpr int BPR = LPR * BPL;  // blocks per row
+    // LPR 8: the u6 bytes of a row arrive as u32 words (lane j: bytes j*BPL ..
+    // j*BPL+BPL-1) and the f16 supers as words; LPR 16: one byte / half each.
+    constexpr int NQ = LPR == 8 ? BPL / 4 : BPL;
+    constexpr int NS = LPR == 8 ? BPL / 2 : BPL;
+    static_assert(LPR == 16 || BPL % 4 == 0, "8-lane rows take 4k blocks per lane");
+    const int bpr = BPR;
     int8_t* sq = reinterpret_cast<int8_t*>(smem);
     float* sxs = reinterpret_cast<float*>(smem + NB * bpr * 32);
     float* work = sxs + NB * bpr;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int j = lane & 7;
-    const int gbase = lane & ~7;                    // first lane of this row's group
-    const int rsub = (tid >> 6) * 8 + (lane >> 3);  // row within the unit
+    const int j = lane % LPR;
+    const int gbase = lane - j;                          // first lane of this row's group
+    const int rsub = (tid >> 6) * RPW + lane / LPR;      // row within the unit
 
     struct Unit {
-        uint4 w[NSUB][BPL];    // nibbles of blocks j, j+8, ...
+        uint4 w[NSUB][BPL];  // nibbles of blocks j, j+LPR, ...
         uint32_t sub[NSUB][NQ];
         uint32_t sup[NSUB][NS];
         int unit, ms, row;
@@ -86,40 +87,60 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
 #pragma unroll
             for (int q = 0; q < BPL; q++) {
                 u32x4 v = {0, 0, 0, 0};
-                if (ok) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(M.nib) + r0 + j + 8 * q);
+                if (ok) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(M.nib) + r0 + j + LPR * q);
                 R.w[k][q] = make_uint4(v.x, v.y, v.z, v.w);
             }
-            const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + r0 + j * BPL);
-            const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + (size_t)row * BPL);
+            if constexpr (LPR == 8) {
+                const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + r0 + j * BPL);
+                const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + (size_t)row * BPL);
 #pragma unroll
-            for (int m = 0; m < NQ; m++) R.sub[k][m] = ok ? sw[m] : 0u;
+                for (int m = 0; m < NQ; m++) R.sub[k][m] = ok ? sw[m] : 0u;
 #pragma unroll
-            for (int m = 0; m < NS; m++) R.sup[k][m] = ok ? su[m] : 0u;
+                for (int m = 0; m < NS; m++) R.sup[k][m] = ok ? su[m] : 0u;
+            } else {
+                // block b = j + 16q: u6 byte b, super (b / 8) = 2q + j / 8 of the row's bpr / 8
+#pragma unroll
+                for (int q = 0; q < BPL; q++) R.sub[k][q] = ok ? (uint32_t)M.sub[r0 + j + 16 * q] : 0u;
+#pragma unroll
+                for (int q = 0; q < BPL; q++)
+                    R.sup[k][q] = ok ? (uint32_t)M.sup[(size_t)row * (BPR / 8) + 2 * q + (j >> 3)] : 0u;
+            }
         }
         R.resid = 0.0f;
-        if (EPI == kEpiResAdd && j == 7 && row < p.mats[0].rows) R.resid = p.outs[0][row];
+        if (EPI == kEpiResAdd && j == LPR - 1 && row < p.mats[0].rows) R.resid = p.outs[0][row];
     };
-    // u6 byte of block b = j + 8q: held by lane b / BPL of the group, word (b % BPL) / 4.
+    // LPR 8: u6 byte of block b = j + 8q is held by lane b / BPL of the group, word (b % BPL) / 4.
     auto sub_byte = [&](const Unit& R, int k, int q) -> uint32_t {
-        const int b = j + 8 * q;
-        const int src = gbase + b / BPL;
-        const int wi = (b % BPL) >> 2;
-        uint32_t got = 0;
+        if constexpr (LPR == 16) {
+            return R.sub[k][q];
+        } else {
+            const int b = j + 8 * q;
+            const int src = gbase + b / BPL;
+            const int wi = (b % BPL) >> 2;
+            uint32_t got = 0;
 #pragma unroll
-        for (int m = 0; m < NQ; m++) {
-            const uint32_t v = (uint32_t)__shfl((int)R.sub[k][m], src, 64);
-            got = m == wi ? v : got;
+            for (int m = 0; m < NQ; m++) {
+                const uint32_t v = (uint32_t)__shfl((int)R.sub[k][m], src, 64);
+                got = m == wi ? v : got;
+            }
+            return (got >> (8 * (b & 3))) & 0xFFu;
         }
-        return (got >> (8 * (b & 3))) & 0xFFu;
     };
-    // Ordered row sum of matrix k, batch column bi; valid in lane j == 7.
+    auto super_half = [&](const Unit& R, int k, int q) -> uint16_t {
+        if constexpr (LPR == 16) {
+            return (uint16_t)R.sup[k][q];
+        } else {
+            const uint32_t supw = R.sup[k][q >> 1];
+            return (uint16_t)((q & 1) ? (supw >> 16) : (supw & 0xFFFFu));
+        }
+    };
+    // Ordered row sum of matrix k, batch column bi; valid in lane j == LPR-1.
     auto row_sum = [&](const Unit& R, int k, int bi) -> float {
         float t[BPL];
 #pragma unroll
         for (int q = 0; q < BPL; q++) {
-            const int b = j + 8 * q;
-            const uint32_t supw = R.sup[k][q >> 1];
-            const float sw = k4_scale((uint16_t)((q & 1) ? (supw >> 16) : (supw & 0xFFFFu)), (uint8_t)sub_byte(R, k, q));
+            const int b = j + LPR * q;
+            const float sw = k4_scale(super_half(R, k, q), (uint8_t)sub_byte(R, k, q));
             const float xsv = sxs[bi * bpr + b];
             float term = 0.0f;
             if (sw != 0.0f && xsv != 0.0f) {
@@ -130,19 +151,10 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
             }
             t[q] = term;
         }
-        // Block b = jj + 8q lives in lane jj: lane 7 gathers them and adds in block order.
+        // Block b = jj + LPR*q lives in lane jj: the last lane adds them in block order.
         float s = 0.0f;
 #pragma unroll
-        for (int q = 0; q < BPL; q++) {
-            s = s + from_lane<0>(t[q]);
-            s = s + from_lane<1>(t[q]);
-            s = s + from_lane<2>(t[q]);
-            s = s + from_lane<3>(t[q]);
-            s = s + from_lane<4>(t[q]);
-            s = s + from_lane<5>(t[q]);
-            s = s + from_lane<6>(t[q]);
-            s = s + from_lane<7>(t[q]);
-        }
+        for (int q = 0; q < BPL; q++) s = gather_add<LPR>(s, t[q]);
         return s;
     };
 
@@ -152,16 +164,23 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     PHASE(0);
     // Activation loads first: they must not queue behind the weight stream.
     // Every trip's loads are issued here, so the prologue waits for HBM once.
-    constexpr int HALVES = 16 * BPL;  // 16-value halves of one activation row
+    constexpr int HALVES = 2 * BPR;  // 16-value halves of one activation row
     constexpr int TRIPS = (HALVES + NT - 1) / NT;
-    constexpr int QV = (NB * BPL * 256 / 16 + NT - 1) / NT;  // 16-byte pieces of qx per lane
+    constexpr int QV = (NB * BPR * 2 + NT - 1) / NT;  // 16-byte pieces of qx per lane
     float pv[PRO == kProQx ? 1 : TRIPS][16], pg[PRO == kProNorm ? TRIPS : 1][16];
+    constexpr int XV = (NB * BPR + NT - 1) / NT;  // block scales per lane
     uint4 qpre[PRO == kProQx ? QV : 1];
+    float xpre[PRO == kProQx ? XV : 1];
     if constexpr (PRO == kProQx) {
 #pragma unroll
         for (int r = 0; r < QV; r++) {
             const int i = (tid + r * NT) * 16;
             if (i < NB * bpr * 32) qpre[r] = *reinterpret_cast<const uint4*>(p.qx + i);
+        }
+#pragma unroll
+        for (int r = 0; r < XV; r++) {
+            const int i = tid + r * NT;
+            if (i < NB * bpr) xpre[r] = p.xs[i];
         }
     } else if constexpr (NB == 1) {
 #pragma unroll
@@ -189,19 +208,25 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     load_unit(A, blockIdx.x);
     const bool two = (int)blockIdx.x + G < p.ntiles;
     if (two) load_unit(Bq, blockIdx.x + G);
+    PHASE(1);
     if constexpr (PRO == kProQx) {
+        PHASE_AFTER(2, qpre[0].x);
 #pragma unroll
         for (int r = 0; r < QV; r++) {
             const int i = (tid + r * NT) * 16;
             if (i < NB * bpr * 32) *reinterpret_cast<uint4*>(sq + i) = qpre[r];
         }
-        for (int i = tid; i < NB * bpr; i += NT) sxs[i] = p.xs[i];
+#pragma unroll
+        for (int r = 0; r < XV; r++) {
+            const int i = tid + r * NT;
+            if (i < NB * bpr) sxs[i] = xpre[r];
+        }
         __syncthreads();
     } else if constexpr (NB == 1) {
-        PHASE_AFTER(1, pv[0][0]);
+        PHASE_AFTER(2, pv[0][0]);
         float scale = 1.0f;
         if constexpr (PRO == kProNorm) {
-            constexpr int NCOL = BPL * 256;
+            constexpr int NCOL = BPR * 32;
 #pragma unroll
             for (int t = 0; t < TRIPS; t++) {
                 const int hh = tid + t * NT;
@@ -209,7 +234,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
             }
             __syncthreads();
             scale = wg_rms_scale_t<NCOL, NW>(work, p.eps, p.isa, work + 16 * rms_stage_pitch(NCOL));
-            PHASE(2);
+            PHASE(6);
         }
 #pragma unroll
         for (int t = 0; t < TRIPS; t++) {
@@ -236,17 +261,40 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         for (int k = 0; k < NSUB; k++)
 #pragma unroll
             for (int bi = 0; bi < NB; bi++) res[k][bi] = row_sum(cur, k, bi);
-        const int row = cur.row, ms = cur.ms;
+        const int row = cur.row, ms = cur.ms, unit = cur.unit;
         const float resid = cur.resid;
         const int ahead = cur.unit + 2 * G;
         if (ahead < p.ntiles) load_unit(cur, ahead);  // refill while the results are written
         else cur.unit = -1;
         nstep++;
         if (nstep == 1) PHASE(4);
-        if (j != 7) return;
-        if (EPI == kEpiSiluMul) {
-            if (row < p.mats[0].rows) p.outs[0][row] = fast_silu_vec(res[0][0]) * res[1][0];
+        if constexpr (EPI == kEpiSiluMul) {
+            const int rows = p.mats[0].rows;
+            float y = 0.0f;
+            if (j == LPR - 1 && row < rows) {
+                y = fast_silu_vec(res[0][0]) * res[1][0];
+                p.outs[0][row] = y;
+            }
+            if constexpr (RPU == 32) {
+                // A unit is 32 consecutive rows: exactly one int8 block of the
+                // next GEMV's activation, quantised here instead of by every
+                // workgroup of that GEMV.
+                if (p.q_out) {
+                    float* slot = work;  // the prologue's staging is no longer read
+                    if (j == LPR - 1) slot[rsub] = y;
+                    __syncthreads();
+                    if (tid < 32) {
+                        float sc;
+                        const int32_t q = quant_lane32(slot[tid], &sc);
+                        // rows past the matrix hold y = 0: their bytes are 0
+                        p.q_out[unit * 32 + qx_perm(tid)] = (int8_t)q;
+                        if (tid == 0) p.q_scale[unit] = sc;
+                    }
+                    __syncthreads();
+                }
+            }
         } else {
+            if (j != LPR - 1) return;
             const int rows = pick_mat(p, ms).rows;
             if (row >= rows) return;
             float* out = pick_out(p, ms);
@@ -288,11 +336,11 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     }
 }
 
-template <int EPI, int BPL, int NB, int NW, int PRO>
+template <int EPI, int LPR, int BPL, int NB, int NW, int PRO>
 static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
-    auto kern = k4_gemv_lane_kernel<EPI, BPL, NB, NW, PRO>;
-    constexpr int RPU = 8 * NW;
-    const size_t stage = PRO == kProNorm ? ((size_t)16 * rms_stage_pitch(p.bpr * 32) + 4) * 4 : 17 * 4;
+    auto kern = k4_gemv_lane_kernel<EPI, LPR, BPL, NB, NW, PRO>;
+    constexpr int RPU = (64 / LPR) * NW;
+    const size_t stage = PRO == kProNorm ? ((size_t)16 * rms_stage_pitch(p.bpr * 32) + 4) * 4 : 40 * 4;
     const size_t smem = (size_t)NB * p.bpr * 36 + stage;
     if (smem > 64 * 1024) return hipErrorInvalidValue;
     int units = 0;
@@ -316,23 +364,32 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Small matrices (latency-bound): one-wave workgroups, 8 rows each, so many
-// CUs share the few MB.  Large ones: four-wave workgroups streaming many units.
-template <int EPI, int BPL, int NB, int PRO>
+// Large matrices (the logits): 8 lanes per row, four-wave workgroups streaming
+// many units.  Small ones are latency-bound, and what bounds them is the loads
+// each wave must issue before its data starts to arrive: 16 lanes per row and
+// one-wave workgroups of 4 rows spread them over every CU.  The quantising
+// SiLU epilogue needs 32-row units: 16 lanes per row in eight-wave workgroups.
+template <int EPI, int BPR, int NB, int PRO>
 static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
     int rows = 0;
     for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
-    if (rows <= lane_small_rows()) return launch_lane_gemv<EPI, BPL, NB, 1, PRO>(p, stream);
-    return launch_lane_gemv<EPI, BPL, NB, 4, PRO>(p, stream);
+    const bool q32 = EPI == kEpiSiluMul && p.q_out;
+    if (rows > lane_small_rows()) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO>(p, stream);
+    if (lane_small_lpr() == 8) {
+        if (q32) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO>(p, stream);
+        return launch_lane_gemv<EPI, 8, BPR / 8, NB, 1, PRO>(p, stream);
+    }
+    if (q32) return launch_lane_gemv<EPI, 16, BPR / 16, NB, 8, PRO>(p, stream);
+    return launch_lane_gemv<EPI, 16, BPR / 16, NB, 1, PRO>(p, stream);
 }
 
 template <int EPI, int NB, int PRO>
 static hipError_t try_lane_gemv(GemvParams& p, hipStream_t stream, bool* used) {
     *used = true;
     switch (p.bpr) {
-        case 32: return launch_lane_gemv_sized<EPI, 4, NB, PRO>(p, stream);
-        case 64: return launch_lane_gemv_sized<EPI, 8, NB, PRO>(p, stream);
-        case 96: return launch_lane_gemv_sized<EPI, 12, NB, PRO>(p, stream);
+        case 32: return launch_lane_gemv_sized<EPI, 32, NB, PRO>(p, stream);
+        case 64: return launch_lane_gemv_sized<EPI, 64, NB, PRO>(p, stream);
+        case 96: return launch_lane_gemv_sized<EPI, 96, NB, PRO>(p, stream);
         default: *used = false; return hipSuccess;
     }
 }

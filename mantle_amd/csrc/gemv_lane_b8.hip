@@ -6,14 +6,22 @@
 
 namespace mantle {
 
+template <int PRO>
+static hipError_t launch_lane_gemv_b8(GemvParams& p, hipStream_t stream) {
+    int rows = 0;
+    for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
+    if (rows <= lane_small_rows()) return launch_lane_gemv<kEpiStore, 8, 4, 8, 1, PRO>(p, stream);
+    return launch_lane_gemv<kEpiStore, 8, 4, 8, 4, PRO>(p, stream);
+}
+
 hipError_t lane_gemv_batch8(GemvParams& p, int pro, hipStream_t stream, bool* used) {
     *used = false;
     if (p.bpr != 32) return hipSuccess;
     *used = true;
     switch (pro) {
-        case kProQx: return launch_lane_gemv_sized<kEpiStore, 4, 8, kProQx>(p, stream);
-        case kProQuant: return launch_lane_gemv_sized<kEpiStore, 4, 8, kProQuant>(p, stream);
-        case kProNorm: return launch_lane_gemv_sized<kEpiStore, 4, 8, kProNorm>(p, stream);
+        case kProQx: return launch_lane_gemv_b8<kProQx>(p, stream);
+        case kProQuant: return launch_lane_gemv_b8<kProQuant>(p, stream);
+        case kProNorm: return launch_lane_gemv_b8<kProNorm>(p, stream);
         default: *used = false; return hipSuccess;
     }
 }

@@ -8,6 +8,7 @@ namespace mantle {
 hipError_t lane_gemv_fused(GemvParams& p, GemvEpi epi, int pro, hipStream_t stream, bool* used) {
     *used = false;
     switch (epi * 4 + pro) {
+        case kEpiResAdd * 4 + kProQx: return try_lane_gemv<kEpiResAdd, 1, kProQx>(p, stream, used);
         case kEpiResAdd * 4 + kProQuant: return try_lane_gemv<kEpiResAdd, 1, kProQuant>(p, stream, used);
         case kEpiResAdd * 4 + kProNorm: return try_lane_gemv<kEpiResAdd, 1, kProNorm>(p, stream, used);
         case kEpiSiluMul * 4 + kProQuant: return try_lane_gemv<kEpiSiluMul, 1, kProQuant>(p, stream, used);

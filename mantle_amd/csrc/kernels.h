@@ -49,10 +49,13 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
                                unsigned long long* argmax_key, hipStream_t stream);
 // Same arithmetic, but each workgroup quantises the fp32 activation x itself
 // (after Mantle's RMSNorm with norm_w when non-null): no separate quantiser
-// launch, and the weight loads are issued before the prologue runs.
+// launch, and the weight loads are issued before the prologue runs.  With
+// kEpiSiluMul, q_out / q_scale (nullable) also receive the output as int8
+// blocks, the operand of the next W4A8 GEMV.
 hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int nmat, int cols, const float* x,
                                      const float* norm_w, float eps, int isa, int batch, GemvEpi epi,
-                                     unsigned long long* argmax_key, hipStream_t stream);
+                                     unsigned long long* argmax_key, hipStream_t stream, int8_t* q_out = nullptr,
+                                     float* q_scale = nullptr);
 // y = W * x with fp32 x (W4A32; tolerance-checked, not bit-exact).
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch,
                                 hipStream_t stream);
@@ -88,6 +91,8 @@ struct AttnArgs {
     float scale;
     int fused;             // 1: norm/rope/append inside, 0: q and cache are final
     int isa;
+    int8_t* q_out;         // optional: out also as Mantle's int8 blocks (permuted layout) ...
+    float* q_scale;        // ... and their scales, for the next W4A8 GEMV (head_dim % 32 == 0)
 };
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 

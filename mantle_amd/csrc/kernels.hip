@@ -397,12 +397,14 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
 
 hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int nmat, int cols, const float* x,
                                      const float* norm_w, float eps, int isa, int batch, GemvEpi epi,
-                                     unsigned long long* argmax_key, hipStream_t stream) {
+                                     unsigned long long* argmax_key, hipStream_t stream, int8_t* q_out,
+                                     float* q_scale) {
     if (!mats || !outs || nmat < 1 || nmat > 3 || cols <= 0 || !x || batch < 1 || batch > 8)
         return hipErrorInvalidValue;
     if (epi == kEpiSiluMul && (nmat != 2 || mats[0].rows != mats[1].rows || batch != 1)) return hipErrorInvalidValue;
     if ((epi == kEpiResAdd || epi == kEpiArgmax) && batch != 1) return hipErrorInvalidValue;
     if (epi == kEpiArgmax && (!argmax_key || nmat != 1)) return hipErrorInvalidValue;
+    if ((q_out || q_scale) && (epi != kEpiSiluMul || !q_out || !q_scale)) return hipErrorInvalidValue;
     GemvParams p = {};
     for (int i = 0; i < nmat; i++) {
         if (!mats[i].nib || !mats[i].sub || !mats[i].sup || mats[i].rows <= 0 || !outs[i]) return hipErrorInvalidValue;
@@ -419,10 +421,15 @@ hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int 
     p.eps = eps;
     p.isa = isa;
     p.key = argmax_key;
+    p.q_out = q_out;
+    p.q_scale = q_scale;
     bool used = false;
     hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
     if (used) return e;
-    return launch_gemv<kModeW4A8Fused>(p, epi, stream);
+    e = launch_gemv<kModeW4A8Fused>(p, epi, stream);
+    if (e != hipSuccess || !q_out) return e;
+    // the tile kernel has no quantising epilogue: a separate quantiser launch
+    return launch_quantize_vec(outs[0], nullptr, 0.0f, mats[0].rows, 1, isa, q_out, q_scale, nullptr, stream);
 }
 
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch, hipStream_t stream) {
@@ -654,6 +661,17 @@ __global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) 
         __syncthreads();
     }
     if (tid < hd) a.out[h * hd + tid] = acc;
+    if (a.q_out) {
+        // The head's output is hd/32 whole int8 blocks of the Wo activation:
+        // quantise them here rather than in every workgroup of the Wo GEMV.
+        float sc;
+        const int32_t qv = quant_lane32(tid < hd ? acc : 0.0f, &sc);
+        if (tid < hd) {
+            const int gi = h * hd + tid;
+            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
+            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+        }
+    }
     PHASE(5);
 }
 
@@ -668,6 +686,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!interleaved && !head_major) return hipErrorInvalidValue;
     if (((uintptr_t)a.cache_k | (uintptr_t)a.cache_v) & 15) return hipErrorInvalidValue;
     if (a.fused && (!a.k || !a.v)) return hipErrorInvalidValue;
+    if (a.q_out && (!a.q_scale || (a.head_dim & 31))) return hipErrorInvalidValue;
     if (!a.pos_dev && (a.pos_host < 0 || a.pos_host >= a.max_ctx)) return hipErrorInvalidValue;
     if (a.rope_cos && (!a.rope_sin || (a.head_dim & 1))) return hipErrorInvalidValue;
     const bool lds_scores = a.max_ctx <= kAttnLdsScores;

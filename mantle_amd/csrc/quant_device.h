@@ -272,6 +272,35 @@ __device__ __forceinline__ void wg_quantize_vec_load(const float* __restrict__ x
     if ((int)threadIdx.x < halves) load_half16(x, weight, n, threadIdx.x * 16, vec4, v, g);
 }
 
+// Mantle's per-block int8 quantiser arithmetic (quantizeVecBlocksInto,
+// internal/backend/simd/matvec_quant.go:746-797) for a block whose max |v| is
+// m: scale = m / 127 (0 for an all-zero block), q = clamp(round(v * (1 /
+// scale)), +-127), round half away from zero.
+__device__ __forceinline__ float quant_block_inv(float m, float* scale) {
+    if (m == 0.0f) {
+        *scale = 0.0f;
+        return 0.0f;
+    }
+    const float sc = m / 127.0f;
+    *scale = sc;
+    return 1.0f / sc;
+}
+__device__ __forceinline__ int32_t quant_value(float v, float inv) {
+    const int32_t q = go_round(v * inv);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// One value per lane, 32 consecutive lanes = one block (lanes 0-31 and 32-63
+// of a wave are two blocks): block max through five xor exchanges, then q of
+// this lane's value and the block scale.
+__device__ __forceinline__ int32_t quant_lane32(float v, float* scale) {
+    float m = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    const float inv = quant_block_inv(m, scale);
+    return quant_value(v, inv);
+}
+
 // Quantise one 16-value half (half hh & 1 of block hh >> 1) of an activation
 // row into Mantle's int8 block layout (quantizeVecBlocksInto,
 // internal/backend/simd/matvec_quant.go:746-797): the block max is one
@@ -293,15 +322,12 @@ __device__ __forceinline__ void quantize_half16(const float (&v)[16], bool live,
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     if (!live) return;
     uint32_t we[2] = {0, 0}, wo[2] = {0, 0};
-    float sc = 0.0f;
+    float sc;
+    const float inv = quant_block_inv(m, &sc);
     if (m != 0.0f) {
-        sc = m / 127.0f;
-        const float inv = 1.0f / sc;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            int32_t q = go_round(v[k] * inv);
-            q = q > 127 ? 127 : (q < -127 ? -127 : q);
-            const uint32_t byte = (uint32_t)(uint8_t)(int8_t)q;
+            const uint32_t byte = (uint32_t)(uint8_t)(int8_t)quant_value(v[k], inv);
             // element e = 16*half + k of the block: dword (e>>3) of the even/odd half
             const int dw = (k >> 3), sh = ((k >> 1) & 3) * 8;
             if (k & 1) wo[dw] |= byte << sh; else we[dw] |= byte << sh;

@@ -101,15 +101,25 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.scale = (float)(1.0 / sqrt((double)c.head_dim));  // attn.go:311-314
         a.fused = 1;
         a.isa = m->isa;
+        const bool qattn = (c.head_dim & 31) == 0;  // whole int8 blocks per head
+        a.q_out = qattn ? m->qx : nullptr;
+        a.q_scale = qattn ? m->xs : nullptr;
         TRY(launch_attention_decode(a, s));
-        // attn.go:417 Wo on the re-quantised attention output, residual folded in
+        // attn.go:417 Wo on the re-quantised attention output (quantised by the
+        // attention kernel), residual folded in
         float* xo[1] = {m->x};
-        TRY(launch_k4_gemv_w4a8_fused(&L.wo, xo, 1, m->q_dim, m->attn, nullptr, 0.0f, m->isa, 1, kEpiResAdd, nullptr, s));
-        // ffn.go:18-91: RMSNorm, up/gate on one int8 activation, SiLU*up, down + residual
+        if (qattn)
+            TRY(launch_k4_gemv_w4a8(&L.wo, xo, 1, m->q_dim, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
+        else
+            TRY(launch_k4_gemv_w4a8_fused(&L.wo, xo, 1, m->q_dim, m->attn, nullptr, 0.0f, m->isa, 1, kEpiResAdd,
+                                          nullptr, s));
+        // ffn.go:18-91: RMSNorm, up/gate on one int8 activation, SiLU*up (also
+        // quantised for down), down + residual
         K4Mat gu[2] = {L.gate, L.up};
         float* ao[2] = {m->act, m->act};
-        TRY(launch_k4_gemv_w4a8_fused(gu, ao, 2, d, m->x, L.ffn_norm, c.eps, m->isa, 1, kEpiSiluMul, nullptr, s));
-        TRY(launch_k4_gemv_w4a8_fused(&L.down, xo, 1, c.ffn, m->act, nullptr, 0.0f, m->isa, 1, kEpiResAdd, nullptr, s));
+        TRY(launch_k4_gemv_w4a8_fused(gu, ao, 2, d, m->x, L.ffn_norm, c.eps, m->isa, 1, kEpiSiluMul, nullptr, s,
+                                      m->qx, m->xs));
+        TRY(launch_k4_gemv_w4a8(&L.down, xo, 1, c.ffn, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
     }
     // runtime_greedy.go:53-67: final RMSNorm, lm_head, argmax (first max wins)
     float* lo[1] = {m->logits};
