@@ -79,35 +79,41 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         R.ms = ms;
         const int row = (unit - first) * RPU + rsub;
         R.row = row;
+        // Loads are unconditional: a row past the matrix re-reads its last row
+        // (never stored), so no branch or wait sits between the loads.  Offsets
+        // are 32-bit from a uniform base (SGPR base + VGPR offset + immediate).
 #pragma unroll
         for (int k = 0; k < NSUB; k++) {
             const K4Mat M = pick_mat(p, NSUB == 2 ? k : ms);
-            const bool ok = row < M.rows;
-            const size_t r0 = (size_t)row * bpr;
+            const uint32_t rc = (uint32_t)(row < M.rows ? row : M.rows - 1);
+            const unsigned char* nb = reinterpret_cast<const unsigned char*>(M.nib) + (rc * BPR + j) * 16u;
 #pragma unroll
             for (int q = 0; q < BPL; q++) {
-                u32x4 v = {0, 0, 0, 0};
-                if (ok) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(M.nib) + r0 + j + LPR * q);
+                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nb + q * LPR * 16));
                 R.w[k][q] = make_uint4(v.x, v.y, v.z, v.w);
             }
             if constexpr (LPR == 8) {
-                const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + r0 + j * BPL);
-                const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + (size_t)row * BPL);
+                const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + rc * BPR + j * BPL);
+                const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + rc * BPL);
 #pragma unroll
-                for (int m = 0; m < NQ; m++) R.sub[k][m] = ok ? sw[m] : 0u;
+                for (int m = 0; m < NQ; m++) R.sub[k][m] = sw[m];
 #pragma unroll
-                for (int m = 0; m < NS; m++) R.sup[k][m] = ok ? su[m] : 0u;
+                for (int m = 0; m < NS; m++) R.sup[k][m] = su[m];
             } else {
                 // block b = j + 16q: u6 byte b, super (b / 8) = 2q + j / 8 of the row's bpr / 8
+                const uint8_t* sb = M.sub + rc * BPR + j;
+                const uint16_t* sp = M.sup + rc * (BPR / 8) + (j >> 3);
 #pragma unroll
-                for (int q = 0; q < BPL; q++) R.sub[k][q] = ok ? (uint32_t)M.sub[r0 + j + 16 * q] : 0u;
+                for (int q = 0; q < BPL; q++) R.sub[k][q] = sb[16 * q];
 #pragma unroll
-                for (int q = 0; q < BPL; q++)
-                    R.sup[k][q] = ok ? (uint32_t)M.sup[(size_t)row * (BPR / 8) + 2 * q + (j >> 3)] : 0u;
+                for (int q = 0; q < BPL; q++) R.sup[k][q] = sp[2 * q];
             }
         }
         R.resid = 0.0f;
-        if (EPI == kEpiResAdd && j == LPR - 1 && row < p.mats[0].rows) R.resid = p.outs[0][row];
+        if constexpr (EPI == kEpiResAdd) {
+            const int rows0 = p.mats[0].rows;
+            R.resid = p.outs[0][row < rows0 ? row : rows0 - 1];
+        }
     };
     // LPR 8: u6 byte of block b = j + 8q is held by lane b / BPL of the group, word (b % BPL) / 4.
     auto sub_byte = [&](const Unit& R, int k, int q) -> uint32_t {
@@ -169,24 +175,26 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     constexpr int QV = (NB * BPR * 2 + NT - 1) / NT;  // 16-byte pieces of qx per lane
     float pv[PRO == kProQx ? 1 : TRIPS][16], pg[PRO == kProNorm ? TRIPS : 1][16];
     constexpr int XV = (NB * BPR + NT - 1) / NT;  // block scales per lane
-    uint4 qpre[PRO == kProQx ? QV : 1];
+    u32x4 qpre[PRO == kProQx ? QV : 1];
     float xpre[PRO == kProQx ? XV : 1];
     if constexpr (PRO == kProQx) {
+        // unconditional (clamped) loads; the surplus is not stored
 #pragma unroll
         for (int r = 0; r < QV; r++) {
             const int i = (tid + r * NT) * 16;
-            if (i < NB * bpr * 32) qpre[r] = *reinterpret_cast<const uint4*>(p.qx + i);
+            qpre[r] = *reinterpret_cast<const u32x4*>(p.qx + (i < NB * BPR * 32 ? i : 0));
         }
 #pragma unroll
         for (int r = 0; r < XV; r++) {
             const int i = tid + r * NT;
-            if (i < NB * bpr) xpre[r] = p.xs[i];
+            xpre[r] = p.xs[i < NB * BPR ? i : 0];
         }
     } else if constexpr (NB == 1) {
 #pragma unroll
         for (int t = 0; t < TRIPS; t++) {
-            const int hh = tid + t * NT;
-            if (HALVES % NT == 0 || hh < HALVES) {
+            // unconditional: lanes past the row re-read half 0 (not used)
+            const int hh = HALVES % NT == 0 || tid + t * NT < HALVES ? tid + t * NT : 0;
+            {
                 const float4* x4 = reinterpret_cast<const float4*>(p.x + hh * 16);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
@@ -214,7 +222,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
 #pragma unroll
         for (int r = 0; r < QV; r++) {
             const int i = (tid + r * NT) * 16;
-            if (i < NB * bpr * 32) *reinterpret_cast<uint4*>(sq + i) = qpre[r];
+            if (i < NB * bpr * 32) *reinterpret_cast<u32x4*>(sq + i) = qpre[r];
         }
 #pragma unroll
         for (int r = 0; r < XV; r++) {
