@@ -1,0 +1,629 @@
+// attention.hip -- batch-1 decode attention for Mantle's k4 decode path
+// (internal/backend/simd/attn.go:255-419, attnpool.go:77-153), bit-exact to
+// the CPU order: per-head q/k RMSNorm, RoPE, KV append, scores in Mantle's
+// dot order, softmax with its ordered sum, and the V sum in key order.
+//
+// Two kernels, one workgroup per query head:
+//  * attention_decode_v4 (head_dim 64 or 128): the q, k and v
+//    vectors are prepared by one wave each with no block barrier; K is staged
+//    in LDS chunk by chunk (pitch head_dim + 4: float4 traffic, no bank
+//    conflicts) and the scores are one key per lane of wave 0; waves 2-3
+//    stream V from HBM into a register ring from the start and do the V sum.
+//  * attention_decode_kernel: any head_dim <= 256 (the general fallback).
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "device_common.h"
+#include "kernels.h"
+#include "phase_trace.h"
+#include "quant_device.h"
+
+namespace mantle {
+
+static constexpr int kAttnKeys = 64;          // keys staged in LDS per chunk (head_dim <= 128)
+static constexpr int kAttnLdsScores = 4096;    // contexts up to this keep scores in LDS
+static constexpr int kAttnHdr = 832;           // q, k, v (256 each) + 64 reduction floats
+
+// Up to 8 float4 of one chunk of cache rows (keys t0 .. t0+nk-1 of one kv head)
+// per lane, held in registers so the loads of the next chunk are in flight
+// while this one is used.  Row `skip` (the fused step's own row) is not loaded.
+typedef float f32x4 __attribute__((ext_vector_type(4)));  // a native vector: no struct copies through scratch
+
+struct ChunkRegs {
+    f32x4 r[8];
+    int off[8];  // LDS offset (row * pitch + col), -1: nothing to store
+};
+
+__device__ __forceinline__ void chunk_issue(ChunkRegs& c, const float* __restrict__ base, int stride, int t0, int nk,
+                                            int hd, int kp, int skip) {
+    // Loads are unconditional (lanes past the chunk re-read row t0, column 0) so
+    // that no branch sits between them and their first use: the wait counts
+    // then only wait for the data actually needed.
+    const int hd4 = hd >> 2;
+    const int total4 = nk * hd4;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int e = j * kThreads + threadIdx.x;
+        const bool live = e < total4;
+        const int ee = live ? e : 0;
+        const int tl = ee / hd4;
+        const int i4 = ee - tl * hd4;
+        const int t = t0 + tl;
+        const int o = tl * kp + 4 * i4;
+        c.r[j] = *reinterpret_cast<const f32x4*>(base + (size_t)t * stride + 4 * i4);
+        c.off[j] = (!live || t == skip) ? -1 : o;
+    }
+}
+
+// chunk_issue with the head size known at compile time (no integer division).
+template <int HD>
+__device__ __forceinline__ void chunk_issue_t(ChunkRegs& c, const float* __restrict__ base, int stride, int t0, int nk,
+                                              int hd, int kp, int skip) {
+    constexpr int hd4 = HD / 4;
+    const int total4 = nk * hd4;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int e = j * kThreads + threadIdx.x;
+        const bool live = e < total4;
+        const int ee = live ? e : 0;
+        const int tl = ee / hd4;
+        const int i4 = ee - tl * hd4;
+        const int t = t0 + tl;
+        const int o = tl * kp + 4 * i4;
+        c.r[j] = *reinterpret_cast<const f32x4*>(base + (size_t)t * stride + 4 * i4);
+        c.off[j] = (!live || t == skip) ? -1 : o;
+    }
+}
+
+__device__ __forceinline__ void chunk_store(const ChunkRegs& c, float* dst, int kp, const float* cur, int t0, int nk,
+                                            int skip, int hd) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int o = c.off[j];
+        if (o < 0) continue;
+        dst[o] = c.r[j].x;
+        dst[o + 1] = c.r[j].y;
+        dst[o + 2] = c.r[j].z;
+        dst[o + 3] = c.r[j].w;
+    }
+    // the fused step's own row comes from `cur` (written by another workgroup
+    // this same launch, so not read back from the cache)
+    if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
+}
+
+// Decode attention for one query head, any head_dim <= 256 (internal/backend/simd/attn.go:255-419,
+// attnpool.go:77-153), bit-exact to the CPU order.  Every global load the head
+// needs first -- q, k, v, the RoPE row, the first K and V chunks -- is issued
+// at the start; later chunks are loaded one chunk ahead of their use.
+__global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    float* sq = lds;
+    float* sk = lds + 256;
+    float* sv = lds + 512;
+    float* red = lds + 768;
+    const int hd = a.head_dim;
+    const int kp = hd + 1;  // odd pitch: lane t reads key row t without bank conflicts
+    const int kc = hd <= 128 ? kAttnKeys : (kThreads * 32) / hd;  // keys per chunk: <= 8 float4 per lane
+    float* kt = lds + kAttnHdr;
+    const int h = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int kvh = h * a.kv_heads / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    float* scores = a.max_ctx <= kAttnLdsScores ? kt + kc * kp : a.scores + (size_t)h * a.max_ctx;
+    const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
+    const float* vbase = a.cache_v + (size_t)kvh * a.head_stride;
+    const int skip = a.fused ? pos : -1;
+    PHASE_SLOT();
+    PHASE(0);
+
+    // ---- all first-needed loads in flight together
+    // (indices clamped instead of branched around, see chunk_issue)
+    const int half = hd / 2;
+    const int ti = tid < hd ? tid : 0;
+    const int th = tid < half ? tid : 0;
+    const float qv = a.q[h * hd + ti];
+    const float* kin = a.fused ? a.k : a.q;
+    const float* vin = a.fused ? a.v : a.q;
+    const float kv = kin[(a.fused ? kvh * hd : 0) + ti];
+    const float vv = vin[(a.fused ? kvh * hd : 0) + ti];
+    const float* cbase = a.rope_cos ? a.rope_cos + (size_t)pos * half : a.q;
+    const float* sbase = a.rope_sin ? a.rope_sin + (size_t)pos * half : a.q;
+    const float cs = cbase[th];
+    const float sn = sbase[th];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the chunk loads
+    ChunkRegs ck, cv;
+    const int nk0 = min(kc, pos + 1);
+    chunk_issue(ck, kbase, a.kv_stride, 0, nk0, hd, kp, skip);
+    chunk_issue(cv, vbase, a.kv_stride, 0, nk0, hd, kp, skip);
+    if (tid < hd) {
+        sq[tid] = qv;
+        sk[tid] = kv;
+        sv[tid] = vv;
+    }
+    __syncthreads();
+    PHASE(1);
+    if (a.fused) {
+        // attn.go:265-286 per-head RMSNorm: q's lane-striped sum on lanes 0..L-1,
+        // k's on lanes 64..64+L-1 (another wave), both at once.
+        const int lanes = a.isa == kIsaAvx512 ? 16 : (a.isa == kIsaAvx2 ? 8 : 0);
+        const int nfull = lanes ? (hd / lanes) * lanes : 0;
+        const bool qlane = lanes && tid < lanes;
+        const bool klane = lanes && tid >= 64 && tid < 64 + lanes;
+        if (qlane || klane) {
+            const float* src = qlane ? sq : sk;
+            const int l = qlane ? tid : tid - 64;
+            float acc = 0.0f;
+            for (int i = l; i < nfull; i += lanes) acc = __builtin_fmaf(src[i], src[i], acc);
+            red[(qlane ? 0 : 32) + l] = acc;
+        }
+        __syncthreads();
+        if (tid == 0 || tid == 64) {
+            const float* src = tid == 0 ? sq : sk;
+            const float* pr = red + (tid == 0 ? 0 : 32);
+            float sum = 0.0f;
+            if (lanes) {
+                sum = pr[0];
+                for (int l = 1; l < lanes; l++) sum += pr[l];
+            }
+            for (int i = nfull; i < hd; i++) sum += src[i] * src[i];
+            red[tid == 0 ? 16 : 48] = rms_scale(sum, hd, a.eps);
+        }
+        __syncthreads();
+        if (tid < hd) {
+            float q1 = sq[tid], k1 = sk[tid];
+            if (a.q_norm) q1 = (q1 * red[16]) * a.q_norm[tid];
+            if (a.k_norm) k1 = (k1 * red[48]) * a.k_norm[tid];
+            sq[tid] = q1;
+            sk[tid] = k1;
+        }
+        __syncthreads();
+        if (a.rope_cos && tid < half) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
+            float x0 = sq[tid], x1 = sq[tid + half];
+            sq[tid] = x0 * cs - x1 * sn;
+            sq[tid + half] = __builtin_fmaf(x0, sn, x1 * cs);
+            x0 = sk[tid];
+            x1 = sk[tid + half];
+            sk[tid] = x0 * cs - x1 * sn;
+            sk[tid + half] = __builtin_fmaf(x0, sn, x1 * cs);
+        }
+        __syncthreads();
+        // ops_runtime.go:112-131 StoreKV: the first q-head of each kv group writes.
+        const int first = (kvh * a.n_head + a.kv_heads - 1) / a.kv_heads;
+        if (h == first && tid < hd) {
+            a.cache_k[(size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride + tid] = sk[tid];
+            a.cache_v[(size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride + tid] = sv[tid];
+        }
+    }
+    PHASE(2);
+
+    // ---- scores_t = Dot(q, k_t) * scale, one lane per key of the staged chunk
+    float lmax = -INFINITY;
+    for (int t0 = 0; t0 <= pos; t0 += kc) {
+        const int nk = min(kc, pos + 1 - t0);
+        chunk_store(ck, kt, kp, sk, t0, nk, skip, hd);
+        __syncthreads();
+        if (t0 + kc <= pos) chunk_issue(ck, kbase, a.kv_stride, t0 + kc, min(kc, pos + 1 - t0 - kc), hd, kp, skip);
+        if (tid < nk) {
+            const float sc = dot_parity(sq, kt + tid * kp, hd, a.isa) * a.scale;
+            scores[t0 + tid] = sc;
+            lmax = fmaxf(lmax, sc);
+        }
+        __syncthreads();
+    }
+    PHASE(3);
+    for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_down(lmax, off, 64));
+    if ((tid & 63) == 0) red[20 + (tid >> 6)] = lmax;
+    __syncthreads();
+    float maxv = red[20];
+    for (int i = 1; i < kThreads / 64; i++) maxv = fmaxf(maxv, red[20 + i]);
+    // Softmax (ops.go:83-106): exponentials, ordered sum, x *= 1/sum
+    for (int t = tid; t <= pos; t += kThreads) scores[t] = fast_exp_scalar(scores[t] - maxv);
+    __syncthreads();
+    if (tid == 0) red[24] = ordered_sum(scores, 1, pos + 1);
+    __syncthreads();
+    const float sum = red[24];
+    if (sum != 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int t = tid; t <= pos; t += kThreads) scores[t] = scores[t] * inv;
+    }
+    __syncthreads();
+    PHASE(4);
+    // ---- out_d = sum_t p_t * v_t,d in t order (no FMA)
+    float acc = 0.0f;
+    for (int t0 = 0; t0 <= pos; t0 += kc) {
+        const int nk = min(kc, pos + 1 - t0);
+        chunk_store(cv, kt, kp, sv, t0, nk, skip, hd);
+        __syncthreads();
+        if (t0 + kc <= pos) chunk_issue(cv, vbase, a.kv_stride, t0 + kc, min(kc, pos + 1 - t0 - kc), hd, kp, skip);
+        if (tid < hd) {
+            const float* ps = scores + t0;
+            int tl = 0;
+            for (; tl + 8 <= nk; tl += 8) {
+                float pv[8], vx[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    pv[k] = ps[tl + k];
+                    vx[k] = kt[(tl + k) * kp + tid];
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) acc += pv[k] * vx[k];
+            }
+            for (; tl < nk; tl++) acc += ps[tl] * kt[tl * kp + tid];
+        }
+        __syncthreads();
+    }
+    if (tid < hd) a.out[h * hd + tid] = acc;
+    if (a.q_out) {
+        // The head's output is hd/32 whole int8 blocks of the Wo activation:
+        // quantise them here rather than in every workgroup of the Wo GEMV.
+        float sc;
+        const int32_t qv = quant_lane32(tid < hd ? acc : 0.0f, &sc);
+        if (tid < hd) {
+            const int gi = h * hd + tid;
+            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
+            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+        }
+    }
+    PHASE(5);
+}
+
+
+// ---------------------------------------------------------------------------
+// Attention v4
+
+// Dot of two LDS vectors read as float4, exactly as dotAVX512 / dotSIMD /
+// dotScalar (internal/backend/simd/ops_avx512.go:27-90, ops_avx2.go:25-51,
+// ops.go:49-55); N a multiple of 16, so no scalar tail.
+template <int N, int ISA>
+__device__ __forceinline__ float dot_parity_v4(const float4* a, const float4* b) {
+    static_assert(N % 16 == 0, "length must be a multiple of 16");
+    auto el = [](const float4& v, int c) { return c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w)); };
+    if constexpr (ISA == kIsaAvx512) {
+        constexpr int n64 = (N / 64) * 64;
+        constexpr int n32 = n64 + ((N - n64) / 32) * 32;
+        float acc[64];
+#pragma unroll
+        for (int k = 0; k < 64; k++) acc[k] = 0.0f;
+#pragma unroll
+        for (int i4 = 0; i4 < N / 4; i4++) {
+            const float4 x = a[i4], y = b[i4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int i = 4 * i4 + c;
+                const int k = i < n64 ? (i & 63) : (i < n32 ? i - n64 : i - n32);
+                acc[k] = __builtin_fmaf(el(x, c), el(y, c), acc[k]);
+            }
+        }
+        float sum = acc[0];
+#pragma unroll
+        for (int k = 1; k < 64; k++) sum += acc[k];
+        return sum;
+    } else if constexpr (ISA == kIsaAvx2) {
+        constexpr int n16 = (N / 16) * 16;
+        float a0[8], a1[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) { a0[l] = 0.0f; a1[l] = 0.0f; }
+#pragma unroll
+        for (int i4 = 0; i4 < N / 4; i4++) {
+            const float4 x = a[i4], y = b[i4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int i = 4 * i4 + c;
+                const int l = i & 7;
+                if (i < n16 && (i & 8)) a1[l] = __builtin_fmaf(el(x, c), el(y, c), a1[l]);
+                else a0[l] = __builtin_fmaf(el(x, c), el(y, c), a0[l]);
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < 8; l++) a0[l] = a0[l] + a1[l];
+        float sum = a0[0];
+#pragma unroll
+        for (int l = 1; l < 8; l++) sum += a0[l];
+        return sum;
+    } else {
+        float sum = 0.0f;
+#pragma unroll
+        for (int i4 = 0; i4 < N / 4; i4++) {
+            const float4 x = a[i4], y = b[i4];
+            sum += x.x * y.x;
+            sum += x.y * y.y;
+            sum += x.z * y.z;
+            sum += x.w * y.w;
+        }
+        return sum;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float dot_v4_isa(const float4* a, const float4* b, int isa) {
+    if (isa == kIsaAvx512) return dot_parity_v4<N, kIsaAvx512>(a, b);
+    if (isa == kIsaAvx2) return dot_parity_v4<N, kIsaAvx2>(a, b);
+    return dot_parity_v4<N, kIsaScalar>(a, b);
+}
+
+// chunk_store for a pitch that is a multiple of 4: one float4 store per value.
+__device__ __forceinline__ void chunk_store_v4(const ChunkRegs& c, float* dst, int kp, const float* cur, int t0,
+                                               int nk, int skip, int hd) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int o = c.off[j];
+        if (o < 0) continue;
+        *reinterpret_cast<f32x4*>(dst + o) = c.r[j];
+    }
+    if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
+}
+
+static constexpr int kAttnV4Hdr = 704;  // sq, sk, sv (128 each), two 128-float wave stagings, 64 reduction
+
+// RMS scale of one head vector held two values per lane (x0 = element i,
+// x1 = element i + hd/2, lanes i < hd/2), in Mantle's lane order (see
+// wg_rms_scale_t).  One wave, wave-private staging `buf` (hd floats).
+__device__ __forceinline__ float wave_rms_scale(float x0, float x1, int hd, float eps, int isa, float* buf) {
+    const int lane = threadIdx.x & 63, half = hd >> 1;
+    if (lane < half) {
+        buf[lane] = x0;
+        buf[lane + half] = x1;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float sum = 0.0f;
+    if (isa == kIsaAvx512 || isa == kIsaAvx2) {
+        const int L = isa == kIsaAvx512 ? 16 : 8;
+        float acc = 0.0f;
+        if (lane < L)
+            for (int i = lane; i < hd; i += L) acc = __builtin_fmaf(buf[i], buf[i], acc);
+        sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+        for (int l = 1; l < L; l++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), l));
+    } else {
+        for (int i = 0; i < hd; i++) sum += buf[i] * buf[i];
+    }
+    return rms_scale(sum, hd, eps);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    float* sq = lds;
+    float* sk = lds + 128;
+    float* sv = lds + 256;
+    float* wbuf = lds + 384;
+    float* red = lds + 640;
+    constexpr int hd = HD, half = HD / 2;
+    constexpr int kp = hd + 4;  // staged key pitch (floats)
+    constexpr int kc = kAttnKeys;
+    float* kt = lds + kAttnV4Hdr;
+    // Workgroup w runs on XCD w % 8.  Query heads that share a KV head are
+    // given workgroups on the same XCD, so the second reads K and V from that
+    // XCD's L2: head = group * (w % G) + w / G, G = n_head / group heads.
+    const int w = blockIdx.x;
+    const int grp = a.n_head / a.kv_heads;  // query heads per KV head
+    const int G = a.n_head / grp;
+    const int h = a.n_head % a.kv_heads == 0 ? grp * (w % G) + w / G : w;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = h * a.kv_heads / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const bool lds_scores = a.max_ctx <= kAttnLdsScores;
+    float* scores = lds_scores ? kt + kc * kp : a.scores + (size_t)h * a.max_ctx;
+    const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
+    const float* vbase = a.cache_v + (size_t)kvh * a.head_stride;
+    const int skip = a.fused ? pos : -1;
+    PHASE_SLOT();
+    PHASE(0);
+
+    // ---- every first-needed load in flight: this wave's vector pair (wave 0
+    // q, 1 k, 2 v), its norm gains and RoPE row, then the first K chunk.
+    // Loads are unconditional (wave-uniform sources, lanes clamped).
+    const int li = lane < half ? lane : 0;
+    const float* src = a.q + h * hd;
+    const float* nw = a.q_norm;
+    if (a.fused && wave == 1) { src = a.k + kvh * hd; nw = a.k_norm; }
+    if (a.fused && wave == 2) { src = a.v + kvh * hd; nw = nullptr; }
+    const bool has_norm = a.fused && wave < 2 && nw != nullptr;
+    const float* gsrc = has_norm ? nw : src;
+    const bool rope = a.fused && a.rope_cos != nullptr;
+    const float* cbase = rope ? a.rope_cos + (size_t)pos * half : src;
+    const float* sbase = rope ? a.rope_sin + (size_t)pos * half : src;
+    float x0 = src[li], x1 = src[li + half];
+    const float g0 = gsrc[li], g1 = gsrc[li + half];
+    const float cs = cbase[li], sn = sbase[li];
+    __builtin_amdgcn_sched_barrier(0);
+    // K chunks are loaded two ahead of their use (ck0: even chunks, ck1: odd)
+    ChunkRegs ck0, ck1;
+    chunk_issue_t<HD>(ck0, kbase, a.kv_stride, 0, min(kc, pos + 1), hd, kp, skip);
+    if (kc <= pos) chunk_issue_t<HD>(ck1, kbase, a.kv_stride, kc, min(kc, pos + 1 - kc), hd, kp, skip);
+    // Waves 2-3 own the V sum (lane d = tid - 128): they have nothing to do
+    // until the softmax is done, so they hold a ring of NG groups of VG keys'
+    // V values in registers, loaded from HBM from the start.
+    constexpr int VG = 32, NG = 5;
+    const bool pv_wave = wave >= 2;
+    const int d = pv_wave && tid - 128 < hd ? tid - 128 : 0;
+    const float* vcol = vbase + d;
+    const size_t vs = (size_t)a.kv_stride;
+    float vr[NG][VG];
+    auto vissue = [&](float (&r)[VG], int t0) {
+#pragma unroll
+        for (int k = 0; k < VG; k++) {
+            const int t = t0 + k <= pos ? t0 + k : pos;
+            r[k] = vcol[(size_t)t * vs];
+        }
+    };
+    if (pv_wave) {
+#pragma unroll
+        for (int g = 0; g < NG; g++)
+            if (g * VG <= pos) vissue(vr[g], g * VG);
+    }
+    PHASE(1);
+
+    if (wave < 3) {
+        if (has_norm) {  // attn.go:265-286 per-head RMSNorm
+            const float s = wave_rms_scale(x0, x1, hd, a.eps, a.isa, wbuf + wave * 128);
+            x0 = (x0 * s) * g0;
+            x1 = (x1 * s) * g1;
+        }
+        if (rope && wave < 2) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
+            const float y0 = x0 * cs - x1 * sn;
+            const float y1 = __builtin_fmaf(x0, sn, x1 * cs);
+            x0 = y0;
+            x1 = y1;
+        }
+        if (lane < half && (wave == 0 || a.fused)) {
+            float* dst = wave == 0 ? sq : (wave == 1 ? sk : sv);
+            dst[lane] = x0;
+            dst[lane + half] = x1;
+            // ops_runtime.go:112-131 StoreKV: the first q-head of each kv group appends
+            const int first = (kvh * a.n_head + a.kv_heads - 1) / a.kv_heads;
+            if (a.fused && wave > 0 && h == first) {
+                float* cache = (wave == 1 ? a.cache_k : a.cache_v) + (size_t)kvh * a.head_stride +
+                               (size_t)pos * a.kv_stride;
+                cache[lane] = x0;
+                cache[lane + half] = x1;
+            }
+        }
+    }
+    __syncthreads();
+    PHASE(2);
+
+    // ---- scores_t = Dot(q, k_t) * scale, one lane of wave 0 per key
+    float lmax = -INFINITY;
+    auto score_chunk = [&](ChunkRegs& ck, int t0) {
+        const int nk = min(kc, pos + 1 - t0);
+        chunk_store_v4(ck, kt, kp, sk, t0, nk, skip, hd);
+        __syncthreads();
+        const int tn = t0 + 2 * kc;  // the chunk two ahead reuses these registers
+        if (tn <= pos) chunk_issue_t<HD>(ck, kbase, a.kv_stride, tn, min(kc, pos + 1 - tn), hd, kp, skip);
+        if (tid < nk) {
+            const float sc = dot_v4_isa<HD>(reinterpret_cast<const float4*>(sq),
+                                            reinterpret_cast<const float4*>(kt + tid * kp), a.isa) * a.scale;
+            scores[t0 + tid] = sc;
+            lmax = fmaxf(lmax, sc);
+        }
+        __syncthreads();
+    };
+    for (int t0 = 0; t0 <= pos; t0 += 2 * kc) {
+        score_chunk(ck0, t0);
+        if (t0 + kc <= pos) score_chunk(ck1, t0 + kc);
+    }
+    PHASE(3);
+    // ---- softmax (ops.go:83-106): max, exponentials, ordered sum, x *= 1/sum
+    if (wave == 0) {
+        for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_down(lmax, off, 64));
+    }
+    const float maxv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(lmax)));
+    if (wave == 0 && lane == 0) red[0] = maxv;
+    __syncthreads();
+    const float mx = red[0];
+    for (int t = tid; t <= pos; t += kThreads) scores[t] = fast_exp_scalar(scores[t] - mx);
+    __syncthreads();
+    if (tid == 0) red[1] = ordered_sum(scores, 1, pos + 1);
+    __syncthreads();
+    const float sum = red[1];
+    if (sum != 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int t = tid; t <= pos; t += kThreads) scores[t] = scores[t] * inv;
+    }
+    __syncthreads();
+    PHASE(4);
+
+    // ---- out_d = sum_t p_t * v_t,d in t order (no FMA), on waves 2-3; the
+    // ring refills group g with keys g + NG groups ahead as it is consumed.
+    // The step's own V row comes from LDS (another workgroup appends it).
+    float acc = 0.0f;
+    if (pv_wave) {
+        const float own = sv[d];
+        for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const int t0 = (g0 + gi) * VG;
+                if (t0 <= pos) {
+                    // the group's probabilities first (float4 reads; LDS scores are
+                    // padded to a multiple of VG), then the adds, branch-free
+                    // (keys past pos leave acc unchanged) so the ring stays in registers
+                    float pg[VG];
+                    if (lds_scores) {
+#pragma unroll
+                        for (int i4 = 0; i4 < VG / 4; i4++) {
+                            const f32x4 p4 = *reinterpret_cast<const f32x4*>(scores + t0 + 4 * i4);
+                            pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < VG; k++) pg[k] = scores[t0 + k <= pos ? t0 + k : pos];
+                    }
+                    if (t0 + VG <= pos) {
+                        // a whole group below pos (the step's own row is pos): plain adds
+#pragma unroll
+                        for (int k = 0; k < VG; k++) acc = acc + pg[k] * vr[gi][k];
+                    } else {
+                        // the last group: keys up to pos, the own row from LDS
+#pragma unroll
+                        for (int k = 0; k < VG; k++) {
+                            const int t = t0 + k;
+                            const float v = t == skip ? own : vr[gi][k];
+                            const float nacc = acc + pg[k] * v;
+                            acc = t <= pos ? nacc : acc;
+                        }
+                    }
+                    if (t0 + NG * VG <= pos) vissue(vr[gi], t0 + NG * VG);
+                }
+            }
+        }
+        if (tid - 128 < hd) a.out[h * hd + d] = acc;
+    }
+    if (a.q_out && pv_wave) {
+        // The head's output is hd/32 whole int8 blocks of the Wo activation:
+        // quantise them here rather than in every workgroup of the Wo GEMV.
+        float sc;
+        const bool live = tid - 128 < hd;
+        const int32_t qv = quant_lane32(live ? acc : 0.0f, &sc);
+        if (live) {
+            const int gi = h * hd + d;
+            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
+            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+        }
+    }
+#ifdef MANTLE_PHASE_TRACE
+    __syncthreads();  // the stamp below then marks the whole workgroup's end
+#endif
+    PHASE(5);
+}
+
+hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
+    if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
+        a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || (a.head_stride & 3) || a.max_ctx <= 0)
+        return hipErrorInvalidValue;
+    // rows of one head must not overlap rows of the next: either interleaved
+    // ([pos][kv_heads*hd]) or head-major ([kv_head][max_ctx][hd])
+    const bool interleaved = a.head_stride == a.head_dim && a.kv_stride >= a.kv_heads * a.head_dim;
+    const bool head_major = a.kv_stride == a.head_dim && a.head_stride >= a.max_ctx * a.head_dim;
+    if (!interleaved && !head_major) return hipErrorInvalidValue;
+    if (((uintptr_t)a.cache_k | (uintptr_t)a.cache_v) & 15) return hipErrorInvalidValue;
+    if (a.fused && (!a.k || !a.v)) return hipErrorInvalidValue;
+    if (a.q_out && (!a.q_scale || (a.head_dim & 31))) return hipErrorInvalidValue;
+    if (!a.pos_dev && (a.pos_host < 0 || a.pos_host >= a.max_ctx)) return hipErrorInvalidValue;
+    if (a.rope_cos && (!a.rope_sin || (a.head_dim & 1))) return hipErrorInvalidValue;
+    const bool lds_scores = a.max_ctx <= kAttnLdsScores;
+    if (!lds_scores && !a.scores) return hipErrorInvalidValue;
+    static const bool force_general = [] {
+        const char* e = getenv("MANTLE_HIP_ATTN_GENERAL");
+        return e && atoi(e) != 0;
+    }();
+    if ((a.head_dim == 128 || a.head_dim == 64) && !force_general) {
+        const size_t smem = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4) +
+                                             (lds_scores ? (a.max_ctx + 31) / 32 * 32 : 0));
+        if (a.head_dim == 128)
+            hipLaunchKernelGGL(attention_decode_v4<128>, dim3(a.n_head), dim3(kThreads), smem, stream, a);
+        else
+            hipLaunchKernelGGL(attention_decode_v4<64>, dim3(a.n_head), dim3(kThreads), smem, stream, a);
+        return hipGetLastError();
+    }
+    const int kc = a.head_dim <= 128 ? kAttnKeys : (kThreads * 32) / a.head_dim;
+    const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kc * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
+    hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), smem, stream, a);
+    return hipGetLastError();
+}
+
+#ifdef MANTLE_PHASE_TRACE
+MANTLE_PHASE_READER(phase_read_attention)
+#endif
+
+}  // namespace mantle

@@ -448,256 +448,6 @@ hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float*
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention (internal/backend/simd/attn.go:255-419, attnpool.go:77-153)
-
-static constexpr int kAttnKeys = 64;          // keys staged in LDS per chunk (head_dim <= 128)
-static constexpr int kAttnLdsScores = 4096;    // contexts up to this keep scores in LDS
-static constexpr int kAttnHdr = 832;           // q, k, v (256 each) + 64 reduction floats
-
-// Up to 8 float4 of one chunk of cache rows (keys t0 .. t0+nk-1 of one kv head)
-// per lane, held in registers so the loads of the next chunk are in flight
-// while this one is used.  Row `skip` (the fused step's own row) is not loaded.
-struct ChunkRegs {
-    float4 r[8];
-    int off[8];  // LDS offset (row * pitch + col), -1: nothing to store
-};
-
-__device__ __forceinline__ void chunk_issue(ChunkRegs& c, const float* __restrict__ base, int stride, int t0, int nk,
-                                            int hd, int kp, int skip) {
-    // Loads are unconditional (lanes past the chunk re-read row t0, column 0) so
-    // that no branch sits between them and their first use: the wait counts
-    // then only wait for the data actually needed.
-    const int hd4 = hd >> 2;
-    const int total4 = nk * hd4;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int e = j * kThreads + threadIdx.x;
-        const bool live = e < total4;
-        const int ee = live ? e : 0;
-        const int tl = ee / hd4;
-        const int i4 = ee - tl * hd4;
-        const int t = t0 + tl;
-        const int o = tl * kp + 4 * i4;
-        c.r[j] = *reinterpret_cast<const float4*>(base + (size_t)t * stride + 4 * i4);
-        c.off[j] = (!live || t == skip) ? -1 : o;
-    }
-}
-
-__device__ __forceinline__ void chunk_store(const ChunkRegs& c, float* dst, int kp, const float* cur, int t0, int nk,
-                                            int skip, int hd) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int o = c.off[j];
-        if (o < 0) continue;
-        dst[o] = c.r[j].x;
-        dst[o + 1] = c.r[j].y;
-        dst[o + 2] = c.r[j].z;
-        dst[o + 3] = c.r[j].w;
-    }
-    // the fused step's own row comes from `cur` (written by another workgroup
-    // this same launch, so not read back from the cache)
-    if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
-}
-
-// Decode attention for one query head (internal/backend/simd/attn.go:255-419,
-// attnpool.go:77-153), bit-exact to the CPU order.  Every global load the head
-// needs first -- q, k, v, the RoPE row, the first K and V chunks -- is issued
-// at the start; later chunks are loaded one chunk ahead of their use.
-__global__ __launch_bounds__(kThreads) void attention_decode_kernel(AttnArgs a) {
-    extern __shared__ __align__(16) float lds[];
-    float* sq = lds;
-    float* sk = lds + 256;
-    float* sv = lds + 512;
-    float* red = lds + 768;
-    const int hd = a.head_dim;
-    const int kp = hd + 1;  // odd pitch: lane t reads key row t without bank conflicts
-    const int kc = hd <= 128 ? kAttnKeys : (kThreads * 32) / hd;  // keys per chunk: <= 8 float4 per lane
-    float* kt = lds + kAttnHdr;
-    const int h = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int kvh = h * a.kv_heads / a.n_head;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
-    float* scores = a.max_ctx <= kAttnLdsScores ? kt + kc * kp : a.scores + (size_t)h * a.max_ctx;
-    const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
-    const float* vbase = a.cache_v + (size_t)kvh * a.head_stride;
-    const int skip = a.fused ? pos : -1;
-    PHASE_SLOT();
-    PHASE(0);
-
-    // ---- all first-needed loads in flight together
-    // (indices clamped instead of branched around, see chunk_issue)
-    const int half = hd / 2;
-    const int ti = tid < hd ? tid : 0;
-    const int th = tid < half ? tid : 0;
-    const float qv = a.q[h * hd + ti];
-    const float* kin = a.fused ? a.k : a.q;
-    const float* vin = a.fused ? a.v : a.q;
-    const float kv = kin[(a.fused ? kvh * hd : 0) + ti];
-    const float vv = vin[(a.fused ? kvh * hd : 0) + ti];
-    const float* cbase = a.rope_cos ? a.rope_cos + (size_t)pos * half : a.q;
-    const float* sbase = a.rope_sin ? a.rope_sin + (size_t)pos * half : a.q;
-    const float cs = cbase[th];
-    const float sn = sbase[th];
-    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the chunk loads
-    ChunkRegs ck, cv;
-    const int nk0 = min(kc, pos + 1);
-    chunk_issue(ck, kbase, a.kv_stride, 0, nk0, hd, kp, skip);
-    chunk_issue(cv, vbase, a.kv_stride, 0, nk0, hd, kp, skip);
-    if (tid < hd) {
-        sq[tid] = qv;
-        sk[tid] = kv;
-        sv[tid] = vv;
-    }
-    __syncthreads();
-    PHASE(1);
-    if (a.fused) {
-        // attn.go:265-286 per-head RMSNorm: q's lane-striped sum on lanes 0..L-1,
-        // k's on lanes 64..64+L-1 (another wave), both at once.
-        const int lanes = a.isa == kIsaAvx512 ? 16 : (a.isa == kIsaAvx2 ? 8 : 0);
-        const int nfull = lanes ? (hd / lanes) * lanes : 0;
-        const bool qlane = lanes && tid < lanes;
-        const bool klane = lanes && tid >= 64 && tid < 64 + lanes;
-        if (qlane || klane) {
-            const float* src = qlane ? sq : sk;
-            const int l = qlane ? tid : tid - 64;
-            float acc = 0.0f;
-            for (int i = l; i < nfull; i += lanes) acc = __builtin_fmaf(src[i], src[i], acc);
-            red[(qlane ? 0 : 32) + l] = acc;
-        }
-        __syncthreads();
-        if (tid == 0 || tid == 64) {
-            const float* src = tid == 0 ? sq : sk;
-            const float* pr = red + (tid == 0 ? 0 : 32);
-            float sum = 0.0f;
-            if (lanes) {
-                sum = pr[0];
-                for (int l = 1; l < lanes; l++) sum += pr[l];
-            }
-            for (int i = nfull; i < hd; i++) sum += src[i] * src[i];
-            red[tid == 0 ? 16 : 48] = rms_scale(sum, hd, a.eps);
-        }
-        __syncthreads();
-        if (tid < hd) {
-            float q1 = sq[tid], k1 = sk[tid];
-            if (a.q_norm) q1 = (q1 * red[16]) * a.q_norm[tid];
-            if (a.k_norm) k1 = (k1 * red[48]) * a.k_norm[tid];
-            sq[tid] = q1;
-            sk[tid] = k1;
-        }
-        __syncthreads();
-        if (a.rope_cos && tid < half) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
-            float x0 = sq[tid], x1 = sq[tid + half];
-            sq[tid] = x0 * cs - x1 * sn;
-            sq[tid + half] = __builtin_fmaf(x0, sn, x1 * cs);
-            x0 = sk[tid];
-            x1 = sk[tid + half];
-            sk[tid] = x0 * cs - x1 * sn;
-            sk[tid + half] = __builtin_fmaf(x0, sn, x1 * cs);
-        }
-        __syncthreads();
-        // ops_runtime.go:112-131 StoreKV: the first q-head of each kv group writes.
-        const int first = (kvh * a.n_head + a.kv_heads - 1) / a.kv_heads;
-        if (h == first && tid < hd) {
-            a.cache_k[(size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride + tid] = sk[tid];
-            a.cache_v[(size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride + tid] = sv[tid];
-        }
-    }
-    PHASE(2);
-
-    // ---- scores_t = Dot(q, k_t) * scale, one lane per key of the staged chunk
-    float lmax = -INFINITY;
-    for (int t0 = 0; t0 <= pos; t0 += kc) {
-        const int nk = min(kc, pos + 1 - t0);
-        chunk_store(ck, kt, kp, sk, t0, nk, skip, hd);
-        __syncthreads();
-        if (t0 + kc <= pos) chunk_issue(ck, kbase, a.kv_stride, t0 + kc, min(kc, pos + 1 - t0 - kc), hd, kp, skip);
-        if (tid < nk) {
-            const float sc = dot_parity(sq, kt + tid * kp, hd, a.isa) * a.scale;
-            scores[t0 + tid] = sc;
-            lmax = fmaxf(lmax, sc);
-        }
-        __syncthreads();
-    }
-    PHASE(3);
-    for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_down(lmax, off, 64));
-    if ((tid & 63) == 0) red[20 + (tid >> 6)] = lmax;
-    __syncthreads();
-    float maxv = red[20];
-    for (int i = 1; i < kThreads / 64; i++) maxv = fmaxf(maxv, red[20 + i]);
-    // Softmax (ops.go:83-106): exponentials, ordered sum, x *= 1/sum
-    for (int t = tid; t <= pos; t += kThreads) scores[t] = fast_exp_scalar(scores[t] - maxv);
-    __syncthreads();
-    if (tid == 0) red[24] = ordered_sum(scores, 1, pos + 1);
-    __syncthreads();
-    const float sum = red[24];
-    if (sum != 0.0f) {
-        const float inv = 1.0f / sum;
-        for (int t = tid; t <= pos; t += kThreads) scores[t] = scores[t] * inv;
-    }
-    __syncthreads();
-    PHASE(4);
-    // ---- out_d = sum_t p_t * v_t,d in t order (no FMA)
-    float acc = 0.0f;
-    for (int t0 = 0; t0 <= pos; t0 += kc) {
-        const int nk = min(kc, pos + 1 - t0);
-        chunk_store(cv, kt, kp, sv, t0, nk, skip, hd);
-        __syncthreads();
-        if (t0 + kc <= pos) chunk_issue(cv, vbase, a.kv_stride, t0 + kc, min(kc, pos + 1 - t0 - kc), hd, kp, skip);
-        if (tid < hd) {
-            const float* ps = scores + t0;
-            int tl = 0;
-            for (; tl + 8 <= nk; tl += 8) {
-                float pv[8], vx[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    pv[k] = ps[tl + k];
-                    vx[k] = kt[(tl + k) * kp + tid];
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) acc += pv[k] * vx[k];
-            }
-            for (; tl < nk; tl++) acc += ps[tl] * kt[tl * kp + tid];
-        }
-        __syncthreads();
-    }
-    if (tid < hd) a.out[h * hd + tid] = acc;
-    if (a.q_out) {
-        // The head's output is hd/32 whole int8 blocks of the Wo activation:
-        // quantise them here rather than in every workgroup of the Wo GEMV.
-        float sc;
-        const int32_t qv = quant_lane32(tid < hd ? acc : 0.0f, &sc);
-        if (tid < hd) {
-            const int gi = h * hd + tid;
-            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
-            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
-        }
-    }
-    PHASE(5);
-}
-
-hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
-    if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
-        a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || (a.head_stride & 3) || a.max_ctx <= 0)
-        return hipErrorInvalidValue;
-    // rows of one head must not overlap rows of the next: either interleaved
-    // ([pos][kv_heads*hd]) or head-major ([kv_head][max_ctx][hd])
-    const bool interleaved = a.head_stride == a.head_dim && a.kv_stride >= a.kv_heads * a.head_dim;
-    const bool head_major = a.kv_stride == a.head_dim && a.head_stride >= a.max_ctx * a.head_dim;
-    if (!interleaved && !head_major) return hipErrorInvalidValue;
-    if (((uintptr_t)a.cache_k | (uintptr_t)a.cache_v) & 15) return hipErrorInvalidValue;
-    if (a.fused && (!a.k || !a.v)) return hipErrorInvalidValue;
-    if (a.q_out && (!a.q_scale || (a.head_dim & 31))) return hipErrorInvalidValue;
-    if (!a.pos_dev && (a.pos_host < 0 || a.pos_host >= a.max_ctx)) return hipErrorInvalidValue;
-    if (a.rope_cos && (!a.rope_sin || (a.head_dim & 1))) return hipErrorInvalidValue;
-    const bool lds_scores = a.max_ctx <= kAttnLdsScores;
-    if (!lds_scores && !a.scores) return hipErrorInvalidValue;
-    const int kc = a.head_dim <= 128 ? kAttnKeys : (kThreads * 32) / a.head_dim;
-    const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kc * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
-    hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), smem, stream, a);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
 // Token embedding (rowToQuant, internal/backend/core/quant_stub.go:51-85) and step bookkeeping.
 
 __global__ __launch_bounds__(kThreads) void embed_kernel(K4Mat emb, int cols, const int* __restrict__ prompt,
@@ -918,11 +668,13 @@ MANTLE_PHASE_READER(phase_read_kernels)
 int phase_read_lane_store(unsigned long long*, int, unsigned*);
 int phase_read_lane_fused(unsigned long long*, int, unsigned*);
 int phase_read_lane_b8(unsigned long long*, int, unsigned*);
+int phase_read_attention(unsigned long long*, int, unsigned*);
 }  // namespace mantle
 // All translation units' stamps, ordered by launch start.
 extern "C" int mantleHipDebugPhaseTrace(unsigned long long* out, int max_slots, unsigned* n) {
     int (*readers[])(unsigned long long*, int, unsigned*) = {mantle::phase_read_kernels, mantle::phase_read_lane_store,
-                                                             mantle::phase_read_lane_fused, mantle::phase_read_lane_b8};
+                                                             mantle::phase_read_lane_fused, mantle::phase_read_lane_b8,
+                                                             mantle::phase_read_attention};
     std::vector<std::array<unsigned long long, 8>> rows;
     for (auto rd : readers) {
         std::vector<unsigned long long> buf((size_t)8192 * 8);
