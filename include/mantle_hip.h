@@ -38,6 +38,16 @@ int mantleHipGetDeviceCount(int* out);
 /* Reduction order the parity kernels follow (internal/backend/simd/tensor_cpu.go:18-24). */
 int mantleHipSetParityISA(int isa);
 int mantleHipGetParityISA(void);
+/* Decode-attention kernel variant for head_dim 64 / 128: no counterpart in
+ * the reference (its CUDA backend has one attention kernel).  All variants are
+ * bit-identical; the split one spreads a head over several CUs (two launches),
+ * "single" keeps one workgroup per head, "general" is the any-head_dim kernel.
+ * A loaded model's captured step keeps the variant it was captured with. */
+#define MANTLE_HIP_ATTN_SPLIT 0
+#define MANTLE_HIP_ATTN_SINGLE 1
+#define MANTLE_HIP_ATTN_GENERAL 2
+int mantleHipSetAttentionPath(int path);
+int mantleHipGetAttentionPath(void);
 
 /* ---------------- k4 kernels ---------------- */
 /* W4A32 k4 GEMV; replaces mantleCudaQuantMatVecK4F32

@@ -34,6 +34,8 @@ _SIGS = {
     "mantleHipGetErrorString": (C.c_char_p, [I]),
     "mantleHipGetDeviceCount": (I, [C.POINTER(I)]),
     "mantleHipSetParityISA": (I, [I]),
+    "mantleHipSetAttentionPath": (I, [I]),
+    "mantleHipGetAttentionPath": (I, []),
     "mantleHipGetParityISA": (I, []),
     "mantleHipQuantMatVecK4F32": (I, [P, P, P, P, P, I, I, I, P]),
     "mantleHipQuantMatVecK4W4A8F32": (I, [P, P, P, P, P, I, I, I, I, P, P, P]),

@@ -12,6 +12,9 @@
 //  * attention_decode_kernel: any head_dim <= 256 (the general fallback).
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <string.h>
+
+#include <atomic>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -380,6 +383,76 @@ __device__ __forceinline__ float wave_rms_scale(float x0, float x1, int hd, floa
     return rms_scale(sum, hd, eps);
 }
 
+// The per-head vector prologue, one wave per vector: wave 0 q, wave 1 k,
+// wave 2 v (fused steps), lane i < hd/2 holding elements i and i + hd/2 (the
+// RoPE pair).  prep_load issues the loads (unconditional: wave-uniform
+// sources, lanes clamped); prep_finish applies the per-head RMSNorm and RoPE,
+// writes q / k / v to LDS and, when `append`, the step's K and V rows to the
+// cache (ops_runtime.go:112-131 StoreKV).
+struct PrepRegs {
+    float x0, x1, g0, g1, cs, sn;
+    bool has_norm, rope;
+};
+
+template <int HD>
+__device__ __forceinline__ PrepRegs prep_load(const AttnArgs& a, int h, int kvh, int pos) {
+    constexpr int half = HD / 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int li = lane < half ? lane : 0;
+    const float* src = a.q + h * HD;
+    const float* nw = a.q_norm;
+    if (a.fused && wave == 1) { src = a.k + kvh * HD; nw = a.k_norm; }
+    if (a.fused && wave == 2) { src = a.v + kvh * HD; nw = nullptr; }
+    PrepRegs r;
+    r.has_norm = a.fused && wave < 2 && nw != nullptr;
+    r.rope = a.fused && a.rope_cos != nullptr;
+    const float* gsrc = r.has_norm ? nw : src;
+    const float* cbase = r.rope ? a.rope_cos + (size_t)pos * half : src;
+    const float* sbase = r.rope ? a.rope_sin + (size_t)pos * half : src;
+    r.x0 = src[li];
+    r.x1 = src[li + half];
+    r.g0 = gsrc[li];
+    r.g1 = gsrc[li + half];
+    r.cs = cbase[li];
+    r.sn = sbase[li];
+    return r;
+}
+
+template <int HD>
+__device__ __forceinline__ void prep_finish(const AttnArgs& a, PrepRegs r, int kvh, int pos, bool append, float* sq,
+                                            float* sk, float* sv, float* wbuf) {
+    constexpr int half = HD / 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave >= 3) return;
+    float x0 = r.x0, x1 = r.x1;
+    if (r.has_norm) {  // attn.go:265-286 per-head RMSNorm
+        const float s = wave_rms_scale(x0, x1, HD, a.eps, a.isa, wbuf + wave * 128);
+        x0 = (x0 * s) * r.g0;
+        x1 = (x1 * s) * r.g1;
+    }
+    if (r.rope && wave < 2) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
+        const float y0 = x0 * r.cs - x1 * r.sn;
+        const float y1 = __builtin_fmaf(x0, r.sn, x1 * r.cs);
+        x0 = y0;
+        x1 = y1;
+    }
+    if (lane < half && (wave == 0 || a.fused)) {
+        float* dst = wave == 0 ? sq : (wave == 1 ? sk : sv);
+        dst[lane] = x0;
+        dst[lane + half] = x1;
+        if (a.fused && wave > 0 && append) {
+            float* cache = (wave == 1 ? a.cache_k : a.cache_v) + (size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride;
+            cache[lane] = x0;
+            cache[lane + half] = x1;
+        }
+    }
+}
+
+// The first query head of each KV group appends the step's K / V row.
+__device__ __forceinline__ bool first_of_group(const AttnArgs& a, int h, int kvh) {
+    return h == (kvh * a.n_head + a.kv_heads - 1) / a.kv_heads;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
@@ -388,7 +461,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
     float* sv = lds + 256;
     float* wbuf = lds + 384;
     float* red = lds + 640;
-    constexpr int hd = HD, half = HD / 2;
+    constexpr int hd = HD;
     constexpr int kp = hd + 4;  // staged key pitch (floats)
     constexpr int kc = kAttnKeys;
     float* kt = lds + kAttnV4Hdr;
@@ -413,19 +486,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
     // ---- every first-needed load in flight: this wave's vector pair (wave 0
     // q, 1 k, 2 v), its norm gains and RoPE row, then the first K chunk.
     // Loads are unconditional (wave-uniform sources, lanes clamped).
-    const int li = lane < half ? lane : 0;
-    const float* src = a.q + h * hd;
-    const float* nw = a.q_norm;
-    if (a.fused && wave == 1) { src = a.k + kvh * hd; nw = a.k_norm; }
-    if (a.fused && wave == 2) { src = a.v + kvh * hd; nw = nullptr; }
-    const bool has_norm = a.fused && wave < 2 && nw != nullptr;
-    const float* gsrc = has_norm ? nw : src;
-    const bool rope = a.fused && a.rope_cos != nullptr;
-    const float* cbase = rope ? a.rope_cos + (size_t)pos * half : src;
-    const float* sbase = rope ? a.rope_sin + (size_t)pos * half : src;
-    float x0 = src[li], x1 = src[li + half];
-    const float g0 = gsrc[li], g1 = gsrc[li + half];
-    const float cs = cbase[li], sn = sbase[li];
+    const PrepRegs pr = prep_load<HD>(a, h, kvh, pos);
     __builtin_amdgcn_sched_barrier(0);
     // K chunks are loaded two ahead of their use (ck0: even chunks, ck1: odd)
     ChunkRegs ck0, ck1;
@@ -454,32 +515,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
     }
     PHASE(1);
 
-    if (wave < 3) {
-        if (has_norm) {  // attn.go:265-286 per-head RMSNorm
-            const float s = wave_rms_scale(x0, x1, hd, a.eps, a.isa, wbuf + wave * 128);
-            x0 = (x0 * s) * g0;
-            x1 = (x1 * s) * g1;
-        }
-        if (rope && wave < 2) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
-            const float y0 = x0 * cs - x1 * sn;
-            const float y1 = __builtin_fmaf(x0, sn, x1 * cs);
-            x0 = y0;
-            x1 = y1;
-        }
-        if (lane < half && (wave == 0 || a.fused)) {
-            float* dst = wave == 0 ? sq : (wave == 1 ? sk : sv);
-            dst[lane] = x0;
-            dst[lane + half] = x1;
-            // ops_runtime.go:112-131 StoreKV: the first q-head of each kv group appends
-            const int first = (kvh * a.n_head + a.kv_heads - 1) / a.kv_heads;
-            if (a.fused && wave > 0 && h == first) {
-                float* cache = (wave == 1 ? a.cache_k : a.cache_v) + (size_t)kvh * a.head_stride +
-                               (size_t)pos * a.kv_stride;
-                cache[lane] = x0;
-                cache[lane + half] = x1;
-            }
-        }
-    }
+    prep_finish<HD>(a, pr, kvh, pos, a.fused && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
     __syncthreads();
     PHASE(2);
 
@@ -489,6 +525,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
         const int nk = min(kc, pos + 1 - t0);
         chunk_store_v4(ck, kt, kp, sk, t0, nk, skip, hd);
         __syncthreads();
+        if (t0 == 2 * kc) PHASE(6);  // third chunk staged
         const int tn = t0 + 2 * kc;  // the chunk two ahead reuses these registers
         if (tn <= pos) chunk_issue_t<HD>(ck, kbase, a.kv_stride, tn, min(kc, pos + 1 - tn), hd, kp, skip);
         if (tid < nk) {
@@ -497,6 +534,7 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
             scores[t0 + tid] = sc;
             lmax = fmaxf(lmax, sc);
         }
+        if (t0 == 2 * kc) PHASE_AFTER(7, lmax);  // third chunk's dots done
         __syncthreads();
     };
     for (int t0 = 0; t0 <= pos; t0 += 2 * kc) {
@@ -587,6 +625,186 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
     PHASE(5);
 }
 
+
+// ---------------------------------------------------------------------------
+// Split-key attention: two launches that spread one head over many CUs.
+//
+// attention_scores_split: workgroup (h, s) of kSplitWgs per head scores the
+// 64-key chunks s, s + kSplitWgs, ... of head h into the scores buffer; the
+// q / k prologue is recomputed by each (it is a few hundred cycles), and the
+// (first head, s = 0) workgroup appends the step's K and V rows.
+// attention_pv_split: workgroup (h, column block) runs the softmax over the
+// head's scores (max, exponentials, the ordered sum, x *= 1/sum) and the V sum
+// of its 32 output columns in key order, and quantises them for Wo.  Both
+// keep the single-kernel arithmetic and order exactly.
+static constexpr int kSplitWgs = 16;
+
+// Kernel variant: kAttnPathSplit, kAttnPathSingle (attention_decode_v4) or
+// kAttnPathGeneral; the first read takes MANTLE_HIP_ATTN ("split", "single",
+// "general") when set_attention_path has not been called.
+static std::atomic<int> g_attn_path{-1};
+
+int attention_path() {
+    int v = g_attn_path.load();
+    if (v >= 0) return v;
+    const char* e = getenv("MANTLE_HIP_ATTN");
+    v = kAttnPathSplit;
+    if (e && !strcmp(e, "single")) v = kAttnPathSingle;
+    if (e && !strcmp(e, "general")) v = kAttnPathGeneral;
+    int expect = -1;
+    g_attn_path.compare_exchange_strong(expect, v);
+    return g_attn_path.load();
+}
+
+bool set_attention_path(int path) {
+    if (path != kAttnPathSplit && path != kAttnPathSingle && path != kAttnPathGeneral) return false;
+    g_attn_path.store(path);
+    return true;
+}
+static constexpr int kSplitMaxCtx = 8192;  // the V-sum launch keeps the probabilities in LDS
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    float* sq = lds;
+    float* sk = lds + 128;
+    float* sv = lds + 256;
+    float* wbuf = lds + 384;
+    constexpr int kp = HD + 4;
+    constexpr int kc = kAttnKeys;
+    float* kt = lds + kAttnV4Hdr;
+    const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
+    const int S = gridDim.x / a.n_head;
+    const int tid = threadIdx.x;
+    const int kvh = h * a.kv_heads / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int nchunks = pos / kc + 1;
+    if (sidx >= nchunks) return;  // whole workgroup: no chunk of this context for it
+    const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
+    const int skip = a.fused ? pos : -1;
+    float* sg = a.scores + (size_t)h * a.max_ctx;
+    PHASE_SLOT();
+    PHASE(0);
+    const PrepRegs pr = prep_load<HD>(a, h, kvh, pos);
+    __builtin_amdgcn_sched_barrier(0);
+    ChunkRegs ck;
+    chunk_issue_t<HD>(ck, kbase, a.kv_stride, sidx * kc, min(kc, pos + 1 - sidx * kc), HD, kp, skip);
+    PHASE(1);
+    prep_finish<HD>(a, pr, kvh, pos, a.fused && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
+    __syncthreads();
+    PHASE(2);
+    for (int c = sidx; c < nchunks; c += S) {
+        const int t0 = c * kc;
+        const int nk = min(kc, pos + 1 - t0);
+        chunk_store_v4(ck, kt, kp, sk, t0, nk, skip, HD);
+        __syncthreads();
+        const int cn = c + S;
+        if (cn < nchunks) chunk_issue_t<HD>(ck, kbase, a.kv_stride, cn * kc, min(kc, pos + 1 - cn * kc), HD, kp, skip);
+        if (tid < nk)
+            sg[t0 + tid] = dot_v4_isa<HD>(reinterpret_cast<const float4*>(sq),
+                                          reinterpret_cast<const float4*>(kt + tid * kp), a.isa) * a.scale;
+        __syncthreads();
+    }
+    PHASE(3);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    constexpr int DB = 32;  // output columns per workgroup: one int8 block of the Wo activation
+    constexpr int VG = 32, NG = 5;
+    const int nd = HD / DB;
+    const int h = blockIdx.x / nd, db = blockIdx.x % nd;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = h * a.kv_heads / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int pcap = (a.max_ctx + 31) / 32 * 32;
+    float* p = lds;
+    float* red = lds + pcap;
+    const float* sg = a.scores + (size_t)h * a.max_ctx;
+    PHASE_SLOT();
+    PHASE(0);
+    // wave 0 (lanes 0-31 the columns; 32-63 shadow them) streams its V
+    // columns into a register ring from the start
+    const int d = db * DB + (lane & 31);
+    const float* vcol = a.cache_v + (size_t)kvh * a.head_stride + d;
+    const size_t vs = (size_t)a.kv_stride;
+    float vr[NG][VG];
+    auto vissue = [&](float (&r)[VG], int t0) {
+#pragma unroll
+        for (int k = 0; k < VG; k++) {
+            const int t = t0 + k <= pos ? t0 + k : pos;
+            r[k] = vcol[(size_t)t * vs];
+        }
+    };
+    if (wave == 0) {
+#pragma unroll
+        for (int g = 0; g < NG; g++)
+            if (g * VG <= pos) vissue(vr[g], g * VG);
+    }
+    // softmax (ops.go:83-106): max, exponentials, ordered sum, x *= 1/sum
+    float m = -INFINITY;
+    for (int t = tid; t <= pos; t += kThreads) {
+        const float v = sg[t];
+        p[t] = v;
+        m = fmaxf(m, v);
+    }
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_down(m, off, 64));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = tid; t <= pos; t += kThreads) p[t] = fast_exp_scalar(p[t] - mx);
+    __syncthreads();
+    if (tid == 0) red[4] = ordered_sum(p, 1, pos + 1);
+    __syncthreads();
+    const float sum = red[4];
+    if (sum != 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int t = tid; t <= pos; t += kThreads) p[t] = p[t] * inv;
+    }
+    __syncthreads();
+    PHASE(1);
+    if (wave != 0) return;
+    // out_d = sum_t p_t * v_t,d in t order (no FMA)
+    float acc = 0.0f;
+    for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            const int t0 = (g0 + gi) * VG;
+            if (t0 <= pos) {
+                float pg[VG];
+#pragma unroll
+                for (int i4 = 0; i4 < VG / 4; i4++) {
+                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
+                    pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                }
+                if (t0 + VG <= pos + 1) {
+#pragma unroll
+                    for (int k = 0; k < VG; k++) acc = acc + pg[k] * vr[gi][k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VG; k++) {
+                        const float nacc = acc + pg[k] * vr[gi][k];
+                        acc = t0 + k <= pos ? nacc : acc;
+                    }
+                }
+                if (t0 + NG * VG <= pos) vissue(vr[gi], t0 + NG * VG);
+            }
+        }
+    }
+    if (lane < 32) a.out[h * HD + d] = acc;
+    if (a.q_out) {  // lanes 0-31: exactly one int8 block of the Wo activation
+        float sc;
+        const int32_t qv = quant_lane32(acc, &sc);
+        const int gi = h * HD + d;
+        if (lane < 32) {
+            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
+            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+        }
+    }
+    PHASE(2);
+}
+
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
         a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || (a.head_stride & 3) || a.max_ctx <= 0)
@@ -603,11 +821,23 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (a.rope_cos && (!a.rope_sin || (a.head_dim & 1))) return hipErrorInvalidValue;
     const bool lds_scores = a.max_ctx <= kAttnLdsScores;
     if (!lds_scores && !a.scores) return hipErrorInvalidValue;
-    static const bool force_general = [] {
-        const char* e = getenv("MANTLE_HIP_ATTN_GENERAL");
-        return e && atoi(e) != 0;
-    }();
-    if ((a.head_dim == 128 || a.head_dim == 64) && !force_general) {
+    const int mode = attention_path();
+    const bool fast_hd = a.head_dim == 128 || a.head_dim == 64;
+    if (fast_hd && mode == kAttnPathSplit && a.scores && a.max_ctx <= kSplitMaxCtx) {
+        const int S = min(kSplitWgs, (a.max_ctx + kAttnKeys - 1) / kAttnKeys);
+        const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
+        const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
+        const int nd = a.head_dim / 32;
+        if (a.head_dim == 128) {
+            hipLaunchKernelGGL(attention_scores_split<128>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
+            hipLaunchKernelGGL(attention_pv_split<128>, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
+        } else {
+            hipLaunchKernelGGL(attention_scores_split<64>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
+            hipLaunchKernelGGL(attention_pv_split<64>, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
+        }
+        return hipGetLastError();
+    }
+    if (fast_hd && mode != kAttnPathGeneral) {
         const size_t smem = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4) +
                                              (lds_scores ? (a.max_ctx + 31) / 32 * 32 : 0));
         if (a.head_dim == 128)

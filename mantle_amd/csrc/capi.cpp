@@ -50,6 +50,10 @@ int mantleHipSetParityISA(int isa) {
 
 int mantleHipGetParityISA(void) { return g_isa.load(); }
 
+int mantleHipSetAttentionPath(int path) { return set_attention_path(path) ? hipSuccess : hipErrorInvalidValue; }
+
+int mantleHipGetAttentionPath(void) { return attention_path(); }
+
 int mantleHipQuantMatVecK4F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                               const float* x, float* y, int rows, int blocksPerRow, int cols,
                               mantleHipStream_t stream) {

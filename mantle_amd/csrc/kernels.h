@@ -95,6 +95,12 @@ struct AttnArgs {
     float* q_scale;        // ... and their scales, for the next W4A8 GEMV (head_dim % 32 == 0)
 };
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
+// Decode-attention kernel variant for head_dim 64 / 128 (other sizes always
+// take the general kernel).  A model's captured step keeps the variant it was
+// captured with.
+enum AttnPath : int { kAttnPathSplit = 0, kAttnPathSingle = 1, kAttnPathGeneral = 2 };
+int attention_path();
+bool set_attention_path(int path);
 
 hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
                         hipStream_t stream);

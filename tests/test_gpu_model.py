@@ -47,6 +47,28 @@ def test_greedy_logits_bitexact(hip, tiny_path, lane_path, shape, isa):
         om.close()
 
 
+@pytest.mark.parametrize("path", ["split", "single", "general"])
+def test_lane_long_context_attention_paths(hip, lane_path, path):
+    """140 fused steps (past two 64-key chunks, the step's own K/V row inside
+    a later chunk) on each attention variant: logits bit-identical to the oracle."""
+    import mantle_amd
+    from mantle_amd import _lib
+    _lib.call("mantleHipSetAttentionPath", {"split": 0, "single": 1, "general": 2}[path])
+    try:
+        rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=160)
+        om = models.oracle_model(lane_path, models.LANE, 160)
+        toks = models.prompt(140, models.LANE["vocab"], 5)
+        for step, tok in enumerate(toks):
+            logits = rt.forward_token(tok)
+            _, want = om.forward_greedy(tok, want_logits=True)
+            if step % 10 == 9 or step >= 128:
+                np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+        rt.close()
+        om.close()
+    finally:
+        _lib.call("mantleHipSetAttentionPath", 0)
+
+
 def test_tiny_generate_graph_matches_eager(hip, tiny_path):
     import mantle_amd
     p = models.prompt(9, models.TINY["vocab"], 1)

@@ -113,10 +113,16 @@ def _fill(n, scale):  # fillTestData (internal/backend/simd/attn_test.go:240-244
     return np.array([scale * np.float32((i % 29) - 14) for i in range(n)], dtype=np.float32)
 
 
+ATTN_PATHS = {"split": 0, "single": 1, "general": 2}
+
+
+@pytest.mark.parametrize("path", list(ATTN_PATHS))
 @pytest.mark.parametrize("isa", ISAS)
 @pytest.mark.parametrize("n_head,kv_heads,head_dim,pos", [(4, 2, 8, 5), (16, 8, 128, 0), (16, 8, 128, 130),
-                                                         (32, 8, 128, 1000)])
-def test_attention_bitexact(hip, oracle, isa, n_head, kv_heads, head_dim, pos):
+                                                         (32, 8, 128, 1000), (16, 8, 128, 1100), (8, 2, 64, 300)])
+def test_attention_bitexact(hip, oracle, path, isa, n_head, kv_heads, head_dim, pos):
+    """Every kernel variant bit-identical to the CPU order; 1100 keys give the
+    split variant more 64-key chunks than workgroups per head."""
     kv = kv_heads * head_dim
     if head_dim == 8:
         q, ck, cv = _fill(n_head * head_dim, 0.1), _fill((pos + 1) * kv, 0.2), _fill((pos + 1) * kv, 0.3)
@@ -127,9 +133,12 @@ def test_attention_bitexact(hip, oracle, isa, n_head, kv_heads, head_dim, pos):
         cv = rng.standard_normal((pos + 1) * kv).astype(np.float32)
     scale = np.float32(1.0 / np.sqrt(head_dim))
     g.call("mantleHipSetParityISA", isa)
+    g.call("mantleHipSetAttentionPath", ATTN_PATHS[path])
     out = g.empty(n_head * head_dim)
     scratch = g.empty(n_head * (pos + 1))
     g.call("mantleHipAttentionInnerF32Cache", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)), g.ptr(out),
            g.ptr(scratch), pos, 0, kv, head_dim, n_head, kv_heads, pos + 1, ctypes.c_float(scale), g.stream())
     want = oracle.attn_heads(isa, q, ck, cv, pos, kv, head_dim, n_head, kv_heads, float(scale))
-    g.assert_bitexact(g.host(out), want, "attention")
+    got = g.host(out)
+    g.call("mantleHipSetAttentionPath", 0)
+    g.assert_bitexact(got, want, "attention")
