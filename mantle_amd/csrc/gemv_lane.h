@@ -38,7 +38,7 @@ __device__ __forceinline__ float gather_add(float s, float t) {
     else return gather_add<LPR, JJ + 1>(s + from_lane<JJ, LPR>(t), t);
 }
 
-template <int EPI, int LPR, int BPL, int NB, int NW, int PRO>
+template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D>
 __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     static_assert(LPR == 8 || LPR == 16, "8 or 16 lanes per row");
     extern __shared__ __align__(16) unsigned char smem[];
@@ -165,7 +165,8 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     };
 
     const int G = (int)gridDim.x;
-    Unit A, Bq;
+    static_assert(D == 1 || D == 2, "one or two units in flight");
+    Unit A, Bq;  // D == 2: units blockIdx.x + (2k)G in A, + (2k+1)G in Bq
     PHASE_SLOT();
     PHASE(0);
     // Activation loads first: they must not queue behind the weight stream.
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight stream
     load_unit(A, blockIdx.x);
-    const bool two = (int)blockIdx.x + G < p.ntiles;
+    const bool two = D == 2 && (int)blockIdx.x + G < p.ntiles;
     if (two) load_unit(Bq, blockIdx.x + G);
     PHASE(1);
     if constexpr (PRO == kProQx) {
@@ -271,7 +272,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
             for (int bi = 0; bi < NB; bi++) res[k][bi] = row_sum(cur, k, bi);
         const int row = cur.row, ms = cur.ms, unit = cur.unit;
         const float resid = cur.resid;
-        const int ahead = cur.unit + 2 * G;
+        const int ahead = cur.unit + D * G;
         if (ahead < p.ntiles) load_unit(cur, ahead);  // refill while the results are written
         else cur.unit = -1;
         nstep++;
@@ -318,13 +319,18 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
             }
         }
     };
-    step(A);
-    if (two) {
-        while (true) {
-            step(Bq);
-            if (A.unit < 0) break;
-            step(A);
-            if (Bq.unit < 0) break;
+    if constexpr (D == 1) {
+        step(A);
+        while (A.unit >= 0) step(A);
+    } else {
+        step(A);
+        if (two) {
+            while (true) {
+                step(Bq);
+                if (A.unit < 0) break;
+                step(A);
+                if (Bq.unit < 0) break;
+            }
         }
     }
     PHASE(5);
@@ -339,14 +345,14 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         if (tid == 0) {
             unsigned long long m = red[0];
             for (int i = 1; i < NW; i++) m = red[i] > m ? red[i] : m;
-            atomicMax(p.key, m);
+            atomicMax(p.key + (blockIdx.x % kArgmaxSlots) * kArgmaxStride, m);
         }
     }
 }
 
-template <int EPI, int LPR, int BPL, int NB, int NW, int PRO>
+template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D = 2>
 static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
-    auto kern = k4_gemv_lane_kernel<EPI, LPR, BPL, NB, NW, PRO>;
+    auto kern = k4_gemv_lane_kernel<EPI, LPR, BPL, NB, NW, PRO, D>;
     constexpr int RPU = (64 / LPR) * NW;
     const size_t stage = PRO == kProNorm ? ((size_t)16 * rms_stage_pitch(p.bpr * 32) + 4) * 4 : 40 * 4;
     const size_t smem = (size_t)NB * p.bpr * 36 + stage;
@@ -364,7 +370,9 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     p.wg_begin[p.nmat] = units;
     p.ntiles = units;
     p.rpw = RPU;
-    int slots = resident_wgs(kern, smem);
+    // D == 1: one unit per workgroup (the dispatcher keeps the CUs full);
+    // D > 1: at most one resident wave of workgroups, units dealt out evenly
+    int slots = D == 1 ? units : resident_wgs(kern, smem);
     if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
     const int per = (units + slots - 1) / slots;
     const int grid = (units + per - 1) / per;
@@ -372,9 +380,13 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Large matrices (the logits): 8 lanes per row, four-wave workgroups streaming
-// many units.  Small ones are latency-bound, and what bounds them is the loads
-// each wave must issue before its data starts to arrive: 16 lanes per row and
+// Large matrices (the logits): 8 lanes per row, four-wave workgroups of one
+// 32-row unit each, as many as there are units.  Measured on the logits shape,
+// this beats a resident grid that streams several units per workgroup (ring
+// depth 1-4, 8 or 16 lanes per row, 2-8 waves): the dispatcher refills CUs as
+// workgroups finish, and the per-workgroup prologue overlaps other loads.
+// Small ones are latency-bound, and what bounds them is the loads each wave
+// must issue before its data starts to arrive: 16 lanes per row and
 // one-wave workgroups of 4 rows spread them over every CU.  The quantising
 // SiLU epilogue needs 32-row units: 16 lanes per row in eight-wave workgroups.
 template <int EPI, int BPR, int NB, int PRO>
@@ -382,7 +394,7 @@ static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
     int rows = 0;
     for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
     const bool q32 = EPI == kEpiSiluMul && p.q_out;
-    if (rows > lane_small_rows()) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO>(p, stream);
+    if (rows > lane_small_rows()) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 1>(p, stream);
     if (lane_small_lpr() == 8) {
         if (q32) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO>(p, stream);
         return launch_lane_gemv<EPI, 8, BPR / 8, NB, 1, PRO>(p, stream);

@@ -32,16 +32,24 @@ enum GemvEpi : int {
     kEpiArgmax = 3,   // y[r] = sum and a 64-bit (value, -index) atomicMax key
 };
 
+// The argmax epilogue spreads its atomicMax over kArgmaxSlots keys, one per
+// 128-byte line (workgroup w uses slot w % kArgmaxSlots): thousands of
+// workgroups on one address serialise at the memory-side atomic unit.
+constexpr int kArgmaxSlots = 64;
+constexpr int kArgmaxStride = 16;  // u64 per slot
+
 // Device-resident decode state (one per model).
 struct DecodeState {
     int pos;            // next position to run
     int next_tok;       // argmax of the last step
     int n_prompt;       // positions < n_prompt take their token from prompt[]
     int pad;
-    unsigned long long argmax_key;
+    alignas(128) unsigned long long argmax_keys[kArgmaxSlots * kArgmaxStride];
 };
 
 // y = W * x with x quantised per 32-block to int8 (Mantle's W4A8 CPU path).
+// kEpiArgmax: argmax_key points to kArgmaxSlots x kArgmaxStride keys, zeroed
+// by the caller; the argmax is the max over the slots (finish_step does it).
 // qx: [batch][blocks*32] in the even/odd permuted layout quantize_vec writes;
 // xs: [batch][blocks].  outs[i] receives matrix i's rows.
 hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, int cols,

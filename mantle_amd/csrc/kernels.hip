@@ -281,7 +281,7 @@ __global__ __launch_bounds__(kThreads) void k4_gemv_kernel(GemvParams p) {
         if (tid == 0) {
             unsigned long long m = red[0];
             for (int i = 1; i < kThreads / 64; i++) m = red[i] > m ? red[i] : m;
-            atomicMax(p.key, m);
+            atomicMax(p.key + (blockIdx.x % kArgmaxSlots) * kArgmaxStride, m);
         }
     }
 }
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(K4Mat emb, int cols, co
         const uint32_t word = reinterpret_cast<const uint32_t*>(emb.nib + blk * 16)[e >> 3];
         x[c] = sc == 0.0f ? 0.0f : (float)k4_nib(word, e & 7) * sc;
     }
-    if (threadIdx.x == 0) st->argmax_key = 0ull;
+    for (int i = threadIdx.x; i < kArgmaxSlots; i += kThreads) st->argmax_keys[i * kArgmaxStride] = 0ull;
 }
 
 hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
@@ -473,8 +473,15 @@ hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeSta
     return hipGetLastError();
 }
 
-__global__ void finish_step_kernel(DecodeState* st, int* out_tokens) {
-    const unsigned long long key = st->argmax_key;
+// One wave: the max over the argmax slots, then the step bookkeeping.
+__global__ __launch_bounds__(64) void finish_step_kernel(DecodeState* st, int* out_tokens) {
+    const int lane = threadIdx.x;
+    unsigned long long key = lane < kArgmaxSlots ? st->argmax_keys[lane * kArgmaxStride] : 0ull;
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_down(key, off, 64);
+        key = o > key ? o : key;
+    }
+    if (lane != 0) return;
     const int idx = key == 0ull ? 0 : (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
     st->next_tok = idx;
     out_tokens[st->pos] = idx;
@@ -483,7 +490,7 @@ __global__ void finish_step_kernel(DecodeState* st, int* out_tokens) {
 
 hipError_t launch_finish_step(DecodeState* st, int* out_tokens, hipStream_t stream) {
     if (!st || !out_tokens) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(finish_step_kernel, dim3(1), dim3(1), 0, stream, st, out_tokens);
+    hipLaunchKernelGGL(finish_step_kernel, dim3(1), dim3(64), 0, stream, st, out_tokens);
     return hipGetLastError();
 }
 

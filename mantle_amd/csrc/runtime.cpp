@@ -124,7 +124,7 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
     // runtime_greedy.go:53-67: final RMSNorm, lm_head, argmax (first max wins)
     float* lo[1] = {m->logits};
     TRY(launch_k4_gemv_w4a8_fused(&m->lm_head, lo, 1, d, m->x, m->final_norm, c.eps, m->isa, 1, kEpiArgmax,
-                                  &m->state->argmax_key, s));
+                                  m->state->argmax_keys, s));
     TRY(launch_finish_step(m->state, m->out_tokens, s));
 #undef TRY
     return hipSuccess;
