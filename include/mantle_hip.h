@@ -98,6 +98,20 @@ int mantleHipStoreKVF32Row(float* cache, const float* src, int cachePos, int kvS
 int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const float* cacheV, float* out,
                                     float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
                                     int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
+/* Causal GQA attention over a whole prompt, bf16 inputs, on MFMA (head_dim 128).  Mantle
+ * prefills k4 models position by position, RunAttnHeads over keys 0..t after RoPE
+ * (internal/backend/simd/runtime_prefill.go:11-30, attnpool.go:77-153); its
+ * FlashAttention fast path (internal/backend/simd/attn.go:33-35, flash_attn.go:17)
+ * is the non-causal, one-KV-head-per-head form.  This computes every position at
+ * once: q bf16 [seqLen][nHead][128], k / v bf16 [seqLen][kvHeads][128] (as the
+ * cache rows), optional RoPE tables ropeCos / ropeSin [seqLen][64] (both or
+ * neither) applied to q and k, out fp32 [seqLen][nHead][128].  fp16 MFMA operands
+ * (the RoPE'd q / k, V, the probabilities), fp32 accumulation and softmax: within
+ * max-abs 1e-3 + rel 1e-2 of the CPU path, not bit-exact.
+ * All pointers 16-byte aligned. */
+int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ropeCos,
+                                  const float* ropeSin, float* out, int seqLen, int nHead, int kvHeads, int headDim,
+                                  float scale, mantleHipStream_t stream);
 /* Replaces mantleCudaSoftmaxRowsF32 (softmax.h:13), with Mantle's CPU fastExp / ordered sum. */
 int mantleHipSoftmaxRowsF32(float* data, int rows, int cols, mantleHipStream_t stream);
 /* Replaces mantleCudaSiluMulF32 (softmax.h:59-64), CPU fastSiluVec arithmetic. */

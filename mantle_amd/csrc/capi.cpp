@@ -152,6 +152,13 @@ int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const f
     return launch_attention_decode(a, S(stream));
 }
 
+int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ropeCos,
+                                  const float* ropeSin, float* out, int seqLen, int nHead, int kvHeads, int headDim,
+                                  float scale, mantleHipStream_t stream) {
+    return launch_attention_prefill_bf16(q, k, v, ropeCos, ropeSin, out, seqLen, nHead, kvHeads, headDim, scale,
+                                         S(stream));
+}
+
 int mantleHipSoftmaxRowsF32(float* data, int rows, int cols, mantleHipStream_t stream) {
     return launch_softmax_rows(data, rows, cols, S(stream));
 }

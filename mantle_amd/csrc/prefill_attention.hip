@@ -1,0 +1,309 @@
+// prefill_attention.hip -- causal GQA attention over a whole prompt (bf16
+// inputs) on MFMA, gfx950 v_mfma_f32_32x32x16_f16: the one dense contraction
+// of the path.
+//
+// Mantle prefills k4 models token by token: each position runs RunAttnHeads
+// over the keys 0..t of the cache (internal/backend/simd/runtime_prefill.go:11-30,
+// attnpool.go:77-153), after RoPE on q and k (ops_avx512.go:132-191).  This
+// kernel produces the same outputs for every position at once: out[t] =
+// softmax(q_t . K[0..t] * scale) V[0..t] per query head, K/V of its KV group.
+// Inputs are bf16.  The MFMA operands are fp16 (same rate as bf16): q and k
+// after RoPE, V (bf16 values are exact in fp16) and the probabilities.  With
+// bf16 operands the rounding of the RoPE'd q / k alone put 0.2% of outputs
+// past max-abs 1e-3 + rel 1e-2 of the CPU result (5e-3 worst); fp16 keeps them
+// under 6e-4.  Accumulation and the softmax are fp32: the result matches the
+// CPU path within that tolerance, not bit for bit.
+//
+// Layout (queries are MFMA columns throughout):
+//  * S^T = K . Q^T per 32-key tile: A = K rows from LDS (RoPE applied while
+//    staging), B = this wave's 32 queries, RoPE'd once into registers.  Lane l
+//    then holds query l % 32 and 16 of the tile's keys, so each query's max and
+//    sum are one lane's 16 values plus one exchange with lane l ^ 32.
+//  * O^T += V^T . P^T: B = P straight from the S^T registers (fp16), A = V^T
+//    from LDS, its keys taken in the order the P registers hold them (the sum
+//    over keys does not depend on that order).  O^T keeps the query in the
+//    column too, so the online-softmax rescale is one factor per lane.
+//  * A workgroup is four waves: two query heads of one KV group x 64 queries
+//    (or, without GQA, one head x 128 queries); K/V tiles are staged once for
+//    all four and double-buffered, the next tile's global loads in flight
+//    while the current one is used.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "kernels.h"
+#include "phase_trace.h"
+
+namespace mantle {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+
+static constexpr int kPfHd = 128;             // head_dim
+static constexpr int kPfKeys = 32;            // keys per tile
+static constexpr int kPfKPitch = kPfHd + 8;   // fp16 per staged K row (16-byte rows, 4-bank skew)
+static constexpr int kPfVPitch = kPfKeys + 4; // fp16 per staged V^T row (conflict-free 8-byte reads)
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ uint32_t f16_bits(float x) {  // round to nearest even
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) { return f16_bits(lo) | (f16_bits(hi) << 16); }
+
+// RoPE of the pairs (x0[j], x1[j]) = elements (i + j, i + 64 + j):
+// y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c) (ops_avx512.go:162-190).
+__device__ __forceinline__ void rope8(float (&x0)[8], float (&x1)[8], const float* cs, const float* sn) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float y0 = x0[j] * cs[j] - x1[j] * sn[j];
+        const float y1 = __builtin_fmaf(x0[j], sn[j], x1[j] * cs[j]);
+        x0[j] = y0;
+        x1[j] = y1;
+    }
+}
+
+__device__ __forceinline__ void unpack8(const u32x4v w, float (&x)[8]) {
+    x[0] = bf_lo(w.x); x[1] = bf_hi(w.x); x[2] = bf_lo(w.y); x[3] = bf_hi(w.y);
+    x[4] = bf_lo(w.z); x[5] = bf_hi(w.z); x[6] = bf_lo(w.w); x[7] = bf_hi(w.w);
+}
+
+struct PrefillArgs {
+    const uint16_t* q;  // bf16 [seq][n_head][128]
+    const uint16_t* k;  // bf16 [seq][kv_heads][128]
+    const uint16_t* v;
+    const float* rope_cos;  // [seq][64] or null (no RoPE)
+    const float* rope_sin;
+    float* out;  // fp32 [seq][n_head][128]
+    int seq, n_head, kv_heads;
+    int heads_per_wg;  // 2 (GQA groups of an even size) or 1
+    int q_block;       // queries per workgroup and head
+    int n_qblocks;
+    float scale;
+};
+
+// The staging registers of one K/V tile (this thread's share).
+struct TileRegs {
+    u32x4v k0, k1;       // K row key_k: hd [8c, 8c+8) and [64+8c, 64+8c+8)
+    f32x4v c0, c1, s0, s1;  // RoPE cos / sin for those 8 pairs
+    u32x4v v0, v1;       // V rows 2p and 2p+1: hd [8cv, 8cv+8)
+};
+
+__global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
+    __shared__ __align__(16) uint16_t kt[2][kPfKeys * kPfKPitch];
+    __shared__ __align__(16) uint16_t vt[2][kPfHd * kPfVPitch];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h2 = lane >> 5, l32 = lane & 31;
+    const int wph = 4 / a.heads_per_wg;  // waves per head
+    const int groups = a.n_head / a.heads_per_wg;
+    // the longest query blocks (most keys) are dispatched first
+    const int qb = a.n_qblocks - 1 - (int)blockIdx.x / groups;
+    const int hg = (int)blockIdx.x % groups;
+    const int head = hg * a.heads_per_wg + wave / wph;
+    const int kvh = head * a.kv_heads / a.n_head;
+    const int q0 = qb * a.q_block;
+    const int qw = q0 + (wave % wph) * 32;  // this wave's first query
+    const int myq = qw + l32;               // this lane's query
+    const int qc = myq < a.seq ? myq : a.seq - 1;
+    const int kv_row = a.kv_heads * kPfHd;  // elements per position of K / V
+    const bool rope = a.rope_cos != nullptr;
+
+    // ---- this wave's queries, RoPE'd, as MFMA B operands: qb_op[s] holds
+    // hd 16s + 8*h2 + j (j < 8) of query myq
+    f16x8 qop[8];
+    {
+        const uint16_t* qrow = a.q + ((size_t)qc * a.n_head + head) * kPfHd;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int d = 16 * s + 8 * h2;
+            float x0[8], x1[8];
+            unpack8(*reinterpret_cast<const u32x4v*>(qrow + d), x0);
+            unpack8(*reinterpret_cast<const u32x4v*>(qrow + 64 + d), x1);
+            if (rope) {
+                float cs[8], sn[8];
+                const float* cr = a.rope_cos + (size_t)qc * 64 + d;
+                const float* sr = a.rope_sin + (size_t)qc * 64 + d;
+#pragma unroll
+                for (int j = 0; j < 8; j++) { cs[j] = cr[j]; sn[j] = sr[j]; }
+                rope8(x0, x1, cs, sn);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                qop[s][j] = (_Float16)x0[j];
+                qop[s + 4][j] = (_Float16)x1[j];
+            }
+        }
+    }
+
+    // ---- tile staging: thread -> K (key tid/8, pair chunk tid%8), V (keys 2p, 2p+1, chunk tid/16)
+    const int kk = tid >> 3, kc = tid & 7;
+    const int vp = tid & 15, vc = tid >> 4;
+    auto load_tile = [&](TileRegs& r, int t0) {
+        const int tk = min(t0 + kk, a.seq - 1);
+        const uint16_t* krow = a.k + (size_t)tk * kv_row + kvh * kPfHd;
+        r.k0 = *reinterpret_cast<const u32x4v*>(krow + 8 * kc);
+        r.k1 = *reinterpret_cast<const u32x4v*>(krow + 64 + 8 * kc);
+        if (rope) {
+            const float* cr = a.rope_cos + (size_t)tk * 64 + 8 * kc;
+            const float* sr = a.rope_sin + (size_t)tk * 64 + 8 * kc;
+            r.c0 = *reinterpret_cast<const f32x4v*>(cr);
+            r.c1 = *reinterpret_cast<const f32x4v*>(cr + 4);
+            r.s0 = *reinterpret_cast<const f32x4v*>(sr);
+            r.s1 = *reinterpret_cast<const f32x4v*>(sr + 4);
+        }
+        const int tv0 = min(t0 + 2 * vp, a.seq - 1), tv1 = min(t0 + 2 * vp + 1, a.seq - 1);
+        r.v0 = *reinterpret_cast<const u32x4v*>(a.v + (size_t)tv0 * kv_row + kvh * kPfHd + 8 * vc);
+        r.v1 = *reinterpret_cast<const u32x4v*>(a.v + (size_t)tv1 * kv_row + kvh * kPfHd + 8 * vc);
+    };
+    auto store_tile = [&](const TileRegs& r, int buf) {
+        float x0[8], x1[8];
+        unpack8(r.k0, x0);
+        unpack8(r.k1, x1);
+        if (rope) {
+            const float cs[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+            const float sn[8] = {r.s0.x, r.s0.y, r.s0.z, r.s0.w, r.s1.x, r.s1.y, r.s1.z, r.s1.w};
+            rope8(x0, x1, cs, sn);
+        }
+        u32x4v w0, w1;
+        w0.x = pack_f16(x0[0], x0[1]); w0.y = pack_f16(x0[2], x0[3]);
+        w0.z = pack_f16(x0[4], x0[5]); w0.w = pack_f16(x0[6], x0[7]);
+        w1.x = pack_f16(x1[0], x1[1]); w1.y = pack_f16(x1[2], x1[3]);
+        w1.z = pack_f16(x1[4], x1[5]); w1.w = pack_f16(x1[6], x1[7]);
+        *reinterpret_cast<u32x4v*>(&kt[buf][kk * kPfKPitch + 8 * kc]) = w0;
+        *reinterpret_cast<u32x4v*>(&kt[buf][kk * kPfKPitch + 64 + 8 * kc]) = w1;
+        // V^T in fp16: element (hd 8vc + j, keys 2vp, 2vp+1) as one 32-bit word
+        float e0[8], e1[8];
+        unpack8(r.v0, e0);
+        unpack8(r.v1, e1);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            *reinterpret_cast<uint32_t*>(&vt[buf][(8 * vc + j) * kPfVPitch + 2 * vp]) = pack_f16(e0[j], e1[j]);
+    };
+
+    // ---- online softmax state of this lane's query, O^T accumulators
+    f32x16 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[t][i] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+
+    const int kend = min(q0 + a.q_block, a.seq);  // keys this workgroup needs
+    const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
+    TileRegs tr;
+    load_tile(tr, 0);
+    store_tile(tr, 0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; it++) {
+        const int buf = it & 1;
+        const int t0 = it * kPfKeys;
+        if (it + 1 < ntiles) load_tile(tr, t0 + kPfKeys);
+        if (t0 <= qw + 31) {  // some key of the tile is visible to some query of this wave
+            // S^T = K . Q^T
+            f32x16 sacc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) sacc[i] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const f16x8 ka = *reinterpret_cast<const f16x8*>(&kt[buf][l32 * kPfKPitch + 16 * s + 8 * h2]);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qop[s], sacc, 0, 0, 0);
+            }
+            // element i: key t0 + (i/4)*8 + 4*h2 + i%4 of query myq; causal mask
+            float x[16];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int key = t0 + (i >> 2) * 8 + 4 * h2 + (i & 3);
+                x[i] = key <= myq && key < a.seq ? sacc[i] * sl2 : -INFINITY;
+                mt = fmaxf(mt, x[i]);
+            }
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = exp2f(m_run - m_new);
+            float ls = 0.0f;
+            f16x8 pb[2];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float pv = exp2f(x[i] - m_new);
+                ls += pv;
+                pb[i >> 3][i & 7] = (_Float16)pv;
+            }
+            ls += __shfl_xor(ls, 32, 64);
+            l_run = l_run * alpha + ls;
+            m_run = m_new;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) o[t][i] *= alpha;
+            // O^T += V^T . P^T: k index 8*h2 + j of step s2 is key 16*s2 + (j/4)*8 + 4*h2 + j%4
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) {
+                    const uint16_t* vr = &vt[buf][(32 * t + l32) * kPfVPitch + 16 * s2 + 4 * h2];
+                    const u32x2v lo = *reinterpret_cast<const u32x2v*>(vr);
+                    const u32x2v hi = *reinterpret_cast<const u32x2v*>(vr + 8);
+                    u32x4v w;
+                    w.x = lo.x; w.y = lo.y; w.z = hi.x; w.w = hi.y;
+                    const f16x8 va = __builtin_bit_cast(f16x8, w);
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s2], o[t], 0, 0, 0);
+                }
+            }
+        }
+        // the other buffer's last readers finished before the previous barrier
+        if (it + 1 < ntiles) store_tile(tr, buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- out[myq][head][hd] = O^T[hd][myq] / l
+    if (myq < a.seq) {
+        const float inv = 1.0f / l_run;
+        float* orow = a.out + ((size_t)myq * a.n_head + head) * kPfHd;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                f32x4v r;
+                r.x = o[t][4 * g] * inv;
+                r.y = o[t][4 * g + 1] * inv;
+                r.z = o[t][4 * g + 2] * inv;
+                r.w = o[t][4 * g + 3] * inv;
+                *reinterpret_cast<f32x4v*>(orow + 32 * t + 8 * g + 4 * h2) = r;
+            }
+    }
+}
+
+hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                         const float* rope_cos, const float* rope_sin, float* out, int seq,
+                                         int n_head, int kv_heads, int head_dim, float scale, hipStream_t stream) {
+    if (!q || !k || !v || !out || seq <= 0 || n_head <= 0 || kv_heads <= 0 || head_dim != kPfHd ||
+        n_head % kv_heads != 0 || (!rope_cos) != (!rope_sin))
+        return hipErrorInvalidValue;
+    if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) ||
+        (rope_cos && (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15)))
+        return hipErrorInvalidValue;
+    PrefillArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.out = out;
+    a.seq = seq;
+    a.n_head = n_head;
+    a.kv_heads = kv_heads;
+    a.heads_per_wg = (n_head / kv_heads) % 2 == 0 ? 2 : 1;
+    a.q_block = 32 * (4 / a.heads_per_wg);
+    a.n_qblocks = (seq + a.q_block - 1) / a.q_block;
+    a.scale = scale;
+    const long long grid = (long long)a.n_qblocks * (n_head / a.heads_per_wg);
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attention_prefill_bf16, dim3((unsigned)grid), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace mantle
