@@ -27,6 +27,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 PROMPT_LEN = 31
 CPU_BASELINE_README_TOKS = 3.20  # Qwen3-0.6B k4, Mantle CPU, README.md:43-60
 
@@ -112,6 +113,68 @@ def copy_calibration(nbytes=256 << 20, reps=5):
     log(f"copy calibration: {reps} x {nbytes} B device-to-device copies")
 
 
+def prefill_microbench(seqs=(512, 2048, 8192), nh=16, kvh=8, hd=128, reps=20):
+    """Config 3: causal GQA attention prefill (bf16 q / k / v N(0,1), seed 3, RoPE base 1e6) on MFMA,
+    and the pre-attention RMSNorm over seq x 2048 rows (unit-mean gains); HIP events on the launch stream."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from mantle_amd import _lib
+
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator("cuda:0").manual_seed(3)
+    out = []
+    for S in seqs:
+        q = torch.randn(S * nh * hd, device="cuda:0", generator=gen).to(torch.bfloat16)
+        k = torch.randn(S * kvh * hd, device="cuda:0", generator=gen).to(torch.bfloat16)
+        v = torch.randn(S * kvh * hd, device="cuda:0", generator=gen).to(torch.bfloat16)
+        inv = 1.0 / (1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd))  # loader.go:1604-1612
+        ang = np.arange(S, dtype=np.float64)[:, None] * inv[None, :]
+        cos = torch.from_numpy(np.cos(ang).astype(np.float32)).to("cuda:0")
+        sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to("cuda:0")
+        o = torch.empty(S * nh * hd, device="cuda:0")
+        scale = ctypes.c_float(1.0 / np.sqrt(hd))
+
+        def attn():
+            _lib.call("mantleHipAttentionPrefillBF16", q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(),
+                      sin.data_ptr(), o.data_ptr(), S, nh, kvh, hd, scale, stream.cuda_stream)
+
+        x = torch.randn(S * 2048, device="cuda:0", generator=gen)
+        w = 1.0 + 0.1 * torch.randn(2048, device="cuda:0", generator=gen)  # unit-mean gains
+        y = torch.empty_like(x)
+
+        def norm():
+            _lib.call("mantleHipRMSNormBatchedF32", y.data_ptr(), x.data_ptr(), w.data_ptr(), ctypes.c_float(1e-6),
+                      2048, S, stream.cuda_stream)
+
+        def timed(fn):
+            for _ in range(3):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / reps
+
+        t_attn, t_norm = timed(attn), timed(norm)
+        flops = 4 * hd * nh * S * (S + 1) / 2
+        tf = flops / (t_attn * 1e-6) / 1e12
+        nbytes = S * 2048 * 8 + 2048 * 4
+        gbs = nbytes / (t_norm * 1e-6) / 1e9
+        out.append(dict(seq=S, attention_us=round(t_attn, 2), algo_flops=flops, tflops=round(tf, 1),
+                        mfma_frac=round(tf / PEAK_MFMA_F16_TFLOPS, 4),
+                        rmsnorm_us=round(t_norm, 2), rmsnorm_bytes=nbytes, rmsnorm_gbs=round(gbs, 1),
+                        rmsnorm_frac=round(gbs / PEAK_HBM_GBS, 4)))
+        log(f"prefill attention S={S}: {t_attn:.1f} us, {tf:.1f} TFLOP/s ({tf / PEAK_MFMA_F16_TFLOPS:.1%} of "
+            f"{PEAK_MFMA_F16_TFLOPS:.0f}); rmsnorm {S}x2048: {t_norm:.2f} us, {gbs:.0f} GB/s")
+        del q, k, v, o, x, y
+    return out
+
+
 def traffic_from_profile():
     """HBM bytes per launch of the roofline kernel, as measured by the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/), or None."""
@@ -160,6 +223,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV microbench")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill attention microbench")
+    ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill microbench (for rocprofv3)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the lm_head GEMV microbench and a copy calibration (for rocprofv3 --pmc runs)")
     ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
@@ -174,6 +239,10 @@ def main():
     import mantle_amd
     from mantle_amd import mcf
     from mantle_amd.mcf import QWEN3_0_6B
+
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_microbench()}), flush=True)
+        return
 
     if args.gemv_only:
         g = gemv_microbench([(151936, 1024)], [1], iters=50)[0]
@@ -213,6 +282,7 @@ def main():
     gemv = []
     if not args.no_gemv:
         gemv = gemv_microbench([(151936, 1024), (3072, 1024), (1024, 3072), (2048, 1024)], [1, 8])
+    prefill = [] if args.no_prefill else prefill_microbench()
     head = next((g for g in gemv if g["rows"] == 151936 and g["batch"] == 1), None)
     roofline = None
     if head:
@@ -248,6 +318,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in g.items()} for g in gemv],
+        "prefill_attention": prefill,
     }
     print(json.dumps(line), flush=True)
 
