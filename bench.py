@@ -136,10 +136,14 @@ def prefill_microbench(seqs=(512, 2048, 8192), nh=16, kvh=8, hd=128, reps=20):
         sin = torch.from_numpy(np.sin(ang).astype(np.float32)).to("cuda:0")
         o = torch.empty(S * nh * hd, device="cuda:0")
         scale = ctypes.c_float(1.0 / np.sqrt(hd))
+        nws = ctypes.c_size_t()
+        _lib.call("mantleHipAttentionPrefillWorkspaceSize", S, kvh, hd, ctypes.byref(nws))
+        ws = torch.empty(nws.value, dtype=torch.uint8, device="cuda:0")
 
         def attn():
             _lib.call("mantleHipAttentionPrefillBF16", q.data_ptr(), k.data_ptr(), v.data_ptr(), cos.data_ptr(),
-                      sin.data_ptr(), o.data_ptr(), S, nh, kvh, hd, scale, stream.cuda_stream)
+                      sin.data_ptr(), o.data_ptr(), S, nh, kvh, hd, scale, ws.data_ptr(), nws.value,
+                      stream.cuda_stream)
 
         x = torch.randn(S * 2048, device="cuda:0", generator=gen)
         w = 1.0 + 0.1 * torch.randn(2048, device="cuda:0", generator=gen)  # unit-mean gains
@@ -171,7 +175,7 @@ def prefill_microbench(seqs=(512, 2048, 8192), nh=16, kvh=8, hd=128, reps=20):
                         rmsnorm_frac=round(gbs / PEAK_HBM_GBS, 4)))
         log(f"prefill attention S={S}: {t_attn:.1f} us, {tf:.1f} TFLOP/s ({tf / PEAK_MFMA_F16_TFLOPS:.1%} of "
             f"{PEAK_MFMA_F16_TFLOPS:.0f}); rmsnorm {S}x2048: {t_norm:.2f} us, {gbs:.0f} GB/s")
-        del q, k, v, o, x, y
+        del q, k, v, o, x, y, ws
     return out
 
 

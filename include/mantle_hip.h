@@ -107,11 +107,13 @@ int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const f
  * cache rows), optional RoPE tables ropeCos / ropeSin [seqLen][64] (both or
  * neither) applied to q and k, out fp32 [seqLen][nHead][128].  fp16 MFMA operands
  * (the RoPE'd q / k, V, the probabilities), fp32 accumulation and softmax: within
- * max-abs 1e-3 + rel 1e-2 of the CPU path, not bit-exact.
- * All pointers 16-byte aligned. */
+ * max-abs 1e-3 + rel 1e-2 of the CPU path, not bit-exact.  workspace: caller-owned
+ * device scratch of mantleHipAttentionPrefillWorkspaceSize bytes (the RoPE'd K
+ * and transposed V in fp16, written once per call).  All pointers 16-byte aligned. */
 int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ropeCos,
                                   const float* ropeSin, float* out, int seqLen, int nHead, int kvHeads, int headDim,
-                                  float scale, mantleHipStream_t stream);
+                                  float scale, void* workspace, size_t workspaceBytes, mantleHipStream_t stream);
+int mantleHipAttentionPrefillWorkspaceSize(int seqLen, int kvHeads, int headDim, size_t* bytes);
 /* Replaces mantleCudaSoftmaxRowsF32 (softmax.h:13), with Mantle's CPU fastExp / ordered sum. */
 int mantleHipSoftmaxRowsF32(float* data, int rows, int cols, mantleHipStream_t stream);
 /* Replaces mantleCudaSiluMulF32 (softmax.h:59-64), CPU fastSiluVec arithmetic. */

@@ -154,9 +154,15 @@ int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const f
 
 int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ropeCos,
                                   const float* ropeSin, float* out, int seqLen, int nHead, int kvHeads, int headDim,
-                                  float scale, mantleHipStream_t stream) {
+                                  float scale, void* workspace, size_t workspaceBytes, mantleHipStream_t stream) {
     return launch_attention_prefill_bf16(q, k, v, ropeCos, ropeSin, out, seqLen, nHead, kvHeads, headDim, scale,
-                                         S(stream));
+                                         workspace, workspaceBytes, S(stream));
+}
+
+int mantleHipAttentionPrefillWorkspaceSize(int seqLen, int kvHeads, int headDim, size_t* bytes) {
+    if (!bytes || seqLen <= 0 || kvHeads <= 0 || headDim != 128) return hipErrorInvalidValue;
+    *bytes = attention_prefill_workspace(seqLen, kvHeads);
+    return hipSuccess;
 }
 
 int mantleHipSoftmaxRowsF32(float* data, int rows, int cols, mantleHipStream_t stream) {

@@ -27,6 +27,9 @@
 //    (or, without GQA, one head x 128 queries); K/V tiles are staged once for
 //    all four and double-buffered, the next tile's global loads in flight
 //    while the current one is used.
+//  * A pre-pass (prefill_prep_kv) writes K RoPE'd in fp16 [kv][seq][128] and
+//    V in fp16 transposed [kv][128][seq] into the caller's workspace once, so
+//    the attention workgroups (seq/64 of them per KV group) stage plain copies.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -78,19 +81,76 @@ struct PrefillArgs {
     const float* rope_cos;  // [seq][64] or null (no RoPE)
     const float* rope_sin;
     float* out;  // fp32 [seq][n_head][128]
-    int seq, n_head, kv_heads;
+    uint16_t* kr;  // workspace: fp16 RoPE'd K [kv_heads][seq_pad][128]
+    uint16_t* vtr;  // workspace: fp16 V^T [kv_heads][128][seq_pad]
+    int seq, seq_pad, n_head, kv_heads;
     int heads_per_wg;  // 2 (GQA groups of an even size) or 1
     int q_block;       // queries per workgroup and head
     int n_qblocks;
     float scale;
 };
 
-// The staging registers of one K/V tile (this thread's share).
+// The staging registers of one K/V tile (this thread's share: 32 bytes of each).
 struct TileRegs {
-    u32x4v k0, k1;       // K row key_k: hd [8c, 8c+8) and [64+8c, 64+8c+8)
-    f32x4v c0, c1, s0, s1;  // RoPE cos / sin for those 8 pairs
-    u32x4v v0, v1;       // V rows 2p and 2p+1: hd [8cv, 8cv+8)
+    u32x4v k0, k1;  // K row tid/8, hd 16*(tid%8) .. +16
+    u32x4v v0, v1;  // V^T row tid/2, keys 16*(tid%2) .. +16
 };
+
+// Pre-pass: workgroup (kv head g, keys t0..t0+31) writes K RoPE'd in fp16 and
+// V transposed in fp16 (through LDS), zeros for keys past seq.
+__global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
+    __shared__ __align__(16) uint16_t vs[kPfHd * 40];
+    const int tid = threadIdx.x;
+    const int nkb = a.seq_pad / kPfKeys;
+    const int g = (int)blockIdx.x / nkb, t0 = ((int)blockIdx.x % nkb) * kPfKeys;
+    const int kv_row = a.kv_heads * kPfHd;
+    {  // K: key tid/8, pairs hd [8c, 8c+8) + 64
+        const int kk = tid >> 3, kc = tid & 7;
+        const int t = t0 + kk;
+        u32x4v w0 = {0, 0, 0, 0}, w1 = {0, 0, 0, 0};
+        if (t < a.seq) {
+            const uint16_t* krow = a.k + (size_t)t * kv_row + g * kPfHd;
+            float x0[8], x1[8];
+            unpack8(*reinterpret_cast<const u32x4v*>(krow + 8 * kc), x0);
+            unpack8(*reinterpret_cast<const u32x4v*>(krow + 64 + 8 * kc), x1);
+            if (a.rope_cos) {
+                float cs[8], sn[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    cs[j] = a.rope_cos[(size_t)t * 64 + 8 * kc + j];
+                    sn[j] = a.rope_sin[(size_t)t * 64 + 8 * kc + j];
+                }
+                rope8(x0, x1, cs, sn);
+            }
+            w0.x = pack_f16(x0[0], x0[1]); w0.y = pack_f16(x0[2], x0[3]);
+            w0.z = pack_f16(x0[4], x0[5]); w0.w = pack_f16(x0[6], x0[7]);
+            w1.x = pack_f16(x1[0], x1[1]); w1.y = pack_f16(x1[2], x1[3]);
+            w1.z = pack_f16(x1[4], x1[5]); w1.w = pack_f16(x1[6], x1[7]);
+        }
+        uint16_t* dst = a.kr + ((size_t)g * a.seq_pad + t) * kPfHd;
+        *reinterpret_cast<u32x4v*>(dst + 8 * kc) = w0;
+        *reinterpret_cast<u32x4v*>(dst + 64 + 8 * kc) = w1;
+    }
+    {  // V: keys 2p, 2p+1, hd [8c, 8c+8) -> LDS [hd][key]
+        const int vp = tid & 15, vc = tid >> 4;
+        float e0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, e1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        const int ta = t0 + 2 * vp, tb = ta + 1;
+        if (ta < a.seq) unpack8(*reinterpret_cast<const u32x4v*>(a.v + (size_t)ta * kv_row + g * kPfHd + 8 * vc), e0);
+        if (tb < a.seq) unpack8(*reinterpret_cast<const u32x4v*>(a.v + (size_t)tb * kv_row + g * kPfHd + 8 * vc), e1);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            *reinterpret_cast<uint32_t*>(&vs[(8 * vc + j) * 40 + 2 * vp]) = pack_f16(e0[j], e1[j]);
+    }
+    __syncthreads();
+    {  // V^T row hd = tid/2, keys 16*(tid%2) .. +16
+        const int hd = tid >> 1, hf = tid & 1;
+        const u32x4v r0 = *reinterpret_cast<const u32x4v*>(&vs[hd * 40 + 16 * hf]);
+        const u32x4v r1 = *reinterpret_cast<const u32x4v*>(&vs[hd * 40 + 16 * hf + 8]);
+        uint16_t* dst = a.vtr + ((size_t)g * kPfHd + hd) * a.seq_pad + t0 + 16 * hf;
+        *reinterpret_cast<u32x4v*>(dst) = r0;
+        *reinterpret_cast<u32x4v*>(dst + 8) = r1;
+    }
+}
 
 __global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
     __shared__ __align__(16) uint16_t kt[2][kPfKeys * kPfKPitch];
@@ -108,7 +168,6 @@ __global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
     const int qw = q0 + (wave % wph) * 32;  // this wave's first query
     const int myq = qw + l32;               // this lane's query
     const int qc = myq < a.seq ? myq : a.seq - 1;
-    const int kv_row = a.kv_heads * kPfHd;  // elements per position of K / V
     const bool rope = a.rope_cos != nullptr;
 
     // ---- this wave's queries, RoPE'd, as MFMA B operands: qb_op[s] holds
@@ -138,49 +197,27 @@ __global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
         }
     }
 
-    // ---- tile staging: thread -> K (key tid/8, pair chunk tid%8), V (keys 2p, 2p+1, chunk tid/16)
-    const int kk = tid >> 3, kc = tid & 7;
-    const int vp = tid & 15, vc = tid >> 4;
+    // ---- tile staging (plain copies of the pre-pass output)
+    const int krw = tid >> 3, kcol = 16 * (tid & 7);  // K tile: row, first fp16
+    const int vrw = tid >> 1, vcol = 16 * (tid & 1);  // V^T tile: hd row, first key
+    const uint16_t* kbase = a.kr + (size_t)kvh * a.seq_pad * kPfHd;
+    const uint16_t* vbase = a.vtr + ((size_t)kvh * kPfHd + vrw) * a.seq_pad + vcol;
     auto load_tile = [&](TileRegs& r, int t0) {
-        const int tk = min(t0 + kk, a.seq - 1);
-        const uint16_t* krow = a.k + (size_t)tk * kv_row + kvh * kPfHd;
-        r.k0 = *reinterpret_cast<const u32x4v*>(krow + 8 * kc);
-        r.k1 = *reinterpret_cast<const u32x4v*>(krow + 64 + 8 * kc);
-        if (rope) {
-            const float* cr = a.rope_cos + (size_t)tk * 64 + 8 * kc;
-            const float* sr = a.rope_sin + (size_t)tk * 64 + 8 * kc;
-            r.c0 = *reinterpret_cast<const f32x4v*>(cr);
-            r.c1 = *reinterpret_cast<const f32x4v*>(cr + 4);
-            r.s0 = *reinterpret_cast<const f32x4v*>(sr);
-            r.s1 = *reinterpret_cast<const f32x4v*>(sr + 4);
-        }
-        const int tv0 = min(t0 + 2 * vp, a.seq - 1), tv1 = min(t0 + 2 * vp + 1, a.seq - 1);
-        r.v0 = *reinterpret_cast<const u32x4v*>(a.v + (size_t)tv0 * kv_row + kvh * kPfHd + 8 * vc);
-        r.v1 = *reinterpret_cast<const u32x4v*>(a.v + (size_t)tv1 * kv_row + kvh * kPfHd + 8 * vc);
+        const uint16_t* kp = kbase + (size_t)(t0 + krw) * kPfHd + kcol;
+        r.k0 = *reinterpret_cast<const u32x4v*>(kp);
+        r.k1 = *reinterpret_cast<const u32x4v*>(kp + 8);
+        r.v0 = *reinterpret_cast<const u32x4v*>(vbase + t0);
+        r.v1 = *reinterpret_cast<const u32x4v*>(vbase + t0 + 8);
     };
     auto store_tile = [&](const TileRegs& r, int buf) {
-        float x0[8], x1[8];
-        unpack8(r.k0, x0);
-        unpack8(r.k1, x1);
-        if (rope) {
-            const float cs[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
-            const float sn[8] = {r.s0.x, r.s0.y, r.s0.z, r.s0.w, r.s1.x, r.s1.y, r.s1.z, r.s1.w};
-            rope8(x0, x1, cs, sn);
-        }
-        u32x4v w0, w1;
-        w0.x = pack_f16(x0[0], x0[1]); w0.y = pack_f16(x0[2], x0[3]);
-        w0.z = pack_f16(x0[4], x0[5]); w0.w = pack_f16(x0[6], x0[7]);
-        w1.x = pack_f16(x1[0], x1[1]); w1.y = pack_f16(x1[2], x1[3]);
-        w1.z = pack_f16(x1[4], x1[5]); w1.w = pack_f16(x1[6], x1[7]);
-        *reinterpret_cast<u32x4v*>(&kt[buf][kk * kPfKPitch + 8 * kc]) = w0;
-        *reinterpret_cast<u32x4v*>(&kt[buf][kk * kPfKPitch + 64 + 8 * kc]) = w1;
-        // V^T in fp16: element (hd 8vc + j, keys 2vp, 2vp+1) as one 32-bit word
-        float e0[8], e1[8];
-        unpack8(r.v0, e0);
-        unpack8(r.v1, e1);
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            *reinterpret_cast<uint32_t*>(&vt[buf][(8 * vc + j) * kPfVPitch + 2 * vp]) = pack_f16(e0[j], e1[j]);
+        *reinterpret_cast<u32x4v*>(&kt[buf][krw * kPfKPitch + kcol]) = r.k0;
+        *reinterpret_cast<u32x4v*>(&kt[buf][krw * kPfKPitch + kcol + 8]) = r.k1;
+        // V^T rows are 72 bytes (8-byte aligned): four 8-byte stores
+        u32x2v* vd = reinterpret_cast<u32x2v*>(&vt[buf][vrw * kPfVPitch + vcol]);
+        vd[0] = u32x2v{r.v0.x, r.v0.y};
+        vd[1] = u32x2v{r.v0.z, r.v0.w};
+        vd[2] = u32x2v{r.v1.x, r.v1.y};
+        vd[3] = u32x2v{r.v1.z, r.v1.w};
     };
 
     // ---- online softmax state of this lane's query, O^T accumulators
@@ -212,23 +249,32 @@ __global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
                 const f16x8 ka = *reinterpret_cast<const f16x8*>(&kt[buf][l32 * kPfKPitch + 16 * s + 8 * h2]);
                 sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qop[s], sacc, 0, 0, 0);
             }
-            // element i: key t0 + (i/4)*8 + 4*h2 + i%4 of query myq; causal mask
+            // element i: key t0 + (i/4)*8 + 4*h2 + i%4 of query myq; the causal
+            // mask only on tiles that reach past the wave's first query
             float x[16];
             float mt = -INFINITY;
+            if (t0 + kPfKeys - 1 <= qw && t0 + kPfKeys <= a.seq) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int key = t0 + (i >> 2) * 8 + 4 * h2 + (i & 3);
-                x[i] = key <= myq && key < a.seq ? sacc[i] * sl2 : -INFINITY;
-                mt = fmaxf(mt, x[i]);
+                for (int i = 0; i < 16; i++) {
+                    x[i] = sacc[i] * sl2;
+                    mt = fmaxf(mt, x[i]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int key = t0 + (i >> 2) * 8 + 4 * h2 + (i & 3);
+                    x[i] = key <= myq && key < a.seq ? sacc[i] * sl2 : -INFINITY;
+                    mt = fmaxf(mt, x[i]);
+                }
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
             const float m_new = fmaxf(m_run, mt);
-            const float alpha = exp2f(m_run - m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             float ls = 0.0f;
             f16x8 pb[2];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float pv = exp2f(x[i] - m_new);
+                const float pv = __builtin_amdgcn_exp2f(x[i] - m_new);
                 ls += pv;
                 pb[i >> 3][i & 7] = (_Float16)pv;
             }
@@ -277,15 +323,22 @@ __global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
     }
 }
 
+size_t attention_prefill_workspace(int seq, int kv_heads) {
+    const size_t seq_pad = (size_t)(seq + kPfKeys - 1) / kPfKeys * kPfKeys;
+    return (size_t)kv_heads * seq_pad * kPfHd * 2 * sizeof(uint16_t);
+}
+
 hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                          const float* rope_cos, const float* rope_sin, float* out, int seq,
-                                         int n_head, int kv_heads, int head_dim, float scale, hipStream_t stream) {
-    if (!q || !k || !v || !out || seq <= 0 || n_head <= 0 || kv_heads <= 0 || head_dim != kPfHd ||
+                                         int n_head, int kv_heads, int head_dim, float scale, void* workspace,
+                                         size_t workspace_bytes, hipStream_t stream) {
+    if (!q || !k || !v || !out || !workspace || seq <= 0 || n_head <= 0 || kv_heads <= 0 || head_dim != kPfHd ||
         n_head % kv_heads != 0 || (!rope_cos) != (!rope_sin))
         return hipErrorInvalidValue;
-    if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) ||
+    if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)workspace) & 15) ||
         (rope_cos && (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15)))
         return hipErrorInvalidValue;
+    if (workspace_bytes < attention_prefill_workspace(seq, kv_heads)) return hipErrorInvalidValue;
     PrefillArgs a;
     a.q = q;
     a.k = k;
@@ -294,6 +347,9 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     a.rope_sin = rope_sin;
     a.out = out;
     a.seq = seq;
+    a.seq_pad = (seq + kPfKeys - 1) / kPfKeys * kPfKeys;
+    a.kr = static_cast<uint16_t*>(workspace);
+    a.vtr = a.kr + (size_t)kv_heads * a.seq_pad * kPfHd;
     a.n_head = n_head;
     a.kv_heads = kv_heads;
     a.heads_per_wg = (n_head / kv_heads) % 2 == 0 ? 2 : 1;
@@ -301,7 +357,9 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     a.n_qblocks = (seq + a.q_block - 1) / a.q_block;
     a.scale = scale;
     const long long grid = (long long)a.n_qblocks * (n_head / a.heads_per_wg);
-    if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const long long prep = (long long)kv_heads * (a.seq_pad / kPfKeys);
+    if (grid > 0x7FFFFFFF || prep > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prefill_prep_kv, dim3((unsigned)prep), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(attention_prefill_bf16, dim3((unsigned)grid), dim3(256), 0, stream, a);
     return hipGetLastError();
 }

@@ -42,13 +42,20 @@ def rope_tables(oracle, seq):
     return (np.stack([c for c, _ in cs]).astype(np.float32), np.stack([s for _, s in cs]).astype(np.float32))
 
 
+def workspace(seq, kvh):
+    n = ctypes.c_size_t()
+    g.call("mantleHipAttentionPrefillWorkspaceSize", seq, kvh, HD, ctypes.byref(n))
+    return g.empty(n.value, dtype=torch.uint8), n.value
+
+
 def run_gpu(bits, cos, sin, seq, nh, kvh, scale):
     qb, kb, vb = (g.keep(b) for b in bits)
     out = g.empty(seq * nh * HD)
     cp = g.ptr(g.keep(cos)) if cos is not None else None
     sp = g.ptr(g.keep(sin)) if sin is not None else None
+    ws, nws = workspace(seq, kvh)
     g.call("mantleHipAttentionPrefillBF16", g.ptr(qb), g.ptr(kb), g.ptr(vb), cp, sp, g.ptr(out), seq, nh, kvh, HD,
-           ctypes.c_float(scale), g.stream())
+           ctypes.c_float(scale), g.ptr(ws), nws, g.stream())
     return g.host(out).reshape(seq, nh * HD)
 
 
@@ -121,7 +128,10 @@ def test_prefill_rejects_bad_shapes(hip):
     f = ctypes.c_float(1.0)
     from mantle_amd import _lib
     L = _lib.lib()
-    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 8, 64, f, None) != 0  # head_dim 64
-    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 6, 128, f, None) != 0  # 16 % 6
-    assert L.mantleHipAttentionPrefillBF16(p, p, p, p, None, p, 4, 16, 8, 128, f, None) != 0  # cos without sin
-    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 0, 16, 8, 128, f, None) != 0  # empty
+    big = 1 << 30
+    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 8, 64, f, p, big, None) != 0  # head_dim 64
+    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 6, 128, f, p, big, None) != 0  # 16 % 6
+    assert L.mantleHipAttentionPrefillBF16(p, p, p, p, None, p, 4, 16, 8, 128, f, p, big, None) != 0  # cos, no sin
+    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 0, 16, 8, 128, f, p, big, None) != 0  # empty
+    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 8, 128, f, p, 16, None) != 0  # workspace
+    assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 8, 128, f, None, big, None) != 0
