@@ -38,6 +38,17 @@ __device__ __forceinline__ float gather_add(float s, float t) {
     else return gather_add<LPR, JJ + 1>(s + from_lane<JJ, LPR>(t), t);
 }
 
+// gather_add for NB independent sums at once: the chains interleave, so each
+// DPP add's latency is hidden behind the other columns' adds.
+template <int LPR, int NB, int JJ = 0>
+__device__ __forceinline__ void gather_add_n(float (&s)[NB], const float (&t)[NB]) {
+    if constexpr (JJ < LPR) {
+#pragma unroll
+        for (int bi = 0; bi < NB; bi++) s[bi] = s[bi] + from_lane<JJ, LPR>(t[bi]);
+        gather_add_n<LPR, NB, JJ + 1>(s, t);
+    }
+}
+
 template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D>
 __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     static_assert(LPR == 8 || LPR == 16, "8 or 16 lanes per row");
@@ -141,12 +152,17 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         }
     };
     // Ordered row sum of matrix k, batch column bi; valid in lane j == LPR-1.
-    auto row_sum = [&](const Unit& R, int k, int bi) -> float {
+    // The weight block scales of matrix k (shared by every batch column).
+    auto block_scales = [&](const Unit& R, int k, float (&sw)[BPL]) {
+#pragma unroll
+        for (int q = 0; q < BPL; q++) sw[q] = k4_scale(super_half(R, k, q), (uint8_t)sub_byte(R, k, q));
+    };
+    auto row_sum = [&](const Unit& R, int k, int bi, const float (&swk)[BPL]) -> float {
         float t[BPL];
 #pragma unroll
         for (int q = 0; q < BPL; q++) {
             const int b = j + LPR * q;
-            const float sw = k4_scale(super_half(R, k, q), (uint8_t)sub_byte(R, k, q));
+            const float sw = swk[q];
             const float xsv = sxs[bi * bpr + b];
             float term = 0.0f;
             if (sw != 0.0f && xsv != 0.0f) {
@@ -162,6 +178,31 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
 #pragma unroll
         for (int q = 0; q < BPL; q++) s = gather_add<LPR>(s, t[q]);
         return s;
+    };
+    // All NB batch columns of matrix k: per block the terms of every column,
+    // then the ordered sums of the columns interleaved (same order per column).
+    auto row_sums = [&](const Unit& R, int k, const float (&swk)[BPL], float (&res)[NB]) {
+        float t[BPL][NB];
+#pragma unroll
+        for (int q = 0; q < BPL; q++) {
+            const int b = j + LPR * q;
+#pragma unroll
+            for (int bi = 0; bi < NB; bi++) {
+                const float xsv = sxs[bi * bpr + b];
+                float term = 0.0f;
+                if (swk[q] != 0.0f && xsv != 0.0f) {
+                    const int8_t* xb = sq + (bi * bpr + b) * 32;
+                    const uint4 xe = *reinterpret_cast<const uint4*>(xb);
+                    const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
+                    term = (float)k4_block_dot(R.w[k][q], xe, xo) * (swk[q] * xsv);
+                }
+                t[q][bi] = term;
+            }
+        }
+#pragma unroll
+        for (int bi = 0; bi < NB; bi++) res[bi] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < BPL; q++) gather_add_n<LPR, NB>(res, t[q]);
     };
 
     const int G = (int)gridDim.x;
@@ -267,9 +308,12 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     auto step = [&](Unit& cur) {
         float res[NSUB][NB];
 #pragma unroll
-        for (int k = 0; k < NSUB; k++)
-#pragma unroll
-            for (int bi = 0; bi < NB; bi++) res[k][bi] = row_sum(cur, k, bi);
+        for (int k = 0; k < NSUB; k++) {
+            float swk[BPL];
+            block_scales(cur, k, swk);
+            if constexpr (NB == 1) res[k][0] = row_sum(cur, k, 0, swk);
+            else row_sums(cur, k, swk, res[k]);
+        }
         const int row = cur.row, ms = cur.ms, unit = cur.unit;
         const float resid = cur.resid;
         const int ahead = cur.unit + D * G;

@@ -11,7 +11,7 @@ static hipError_t launch_lane_gemv_b8(GemvParams& p, hipStream_t stream) {
     int rows = 0;
     for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
     if (rows <= lane_small_rows()) return launch_lane_gemv<kEpiStore, 8, 4, 8, 1, PRO>(p, stream);
-    return launch_lane_gemv<kEpiStore, 8, 4, 8, 4, PRO>(p, stream);
+    return launch_lane_gemv<kEpiStore, 8, 4, 8, 4, PRO, 1>(p, stream);  // one unit per workgroup, as at batch 1
 }
 
 hipError_t lane_gemv_batch8(GemvParams& p, int pro, hipStream_t stream, bool* used) {
