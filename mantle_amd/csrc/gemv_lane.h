@@ -40,6 +40,10 @@ __device__ __forceinline__ float gather_add(float s, float t) {
 
 // gather_add for NB independent sums at once: the chains interleave, so each
 // DPP add's latency is hidden behind the other columns' adds.
+#ifndef MANTLE_BATCH_GROUP
+#define MANTLE_BATCH_GROUP 4
+#endif
+static constexpr int kBatchGroup = MANTLE_BATCH_GROUP;  // batch columns summed together
 template <int LPR, int NB, int JJ = 0>
 __device__ __forceinline__ void gather_add_n(float (&s)[NB], const float (&t)[NB]) {
     if constexpr (JJ < LPR) {
@@ -177,32 +181,48 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         float s = 0.0f;
 #pragma unroll
         for (int q = 0; q < BPL; q++) s = gather_add<LPR>(s, t[q]);
+        // materialise the sum here: left alone, the adds sink into the store
+        // branch of the last lane and keep every DPP move's result live until then
+        asm volatile("" : "+v"(s));
         return s;
     };
     // All NB batch columns of matrix k: per block the terms of every column,
     // then the ordered sums of the columns interleaved (same order per column).
     auto row_sums = [&](const Unit& R, int k, const float (&swk)[BPL], float (&res)[NB]) {
-        float t[BPL][NB];
+        // columns in groups of CG: a group's terms, then its CG ordered sums
+        // interleaved; one group at a time bounds the live DPP results
+        constexpr int CG = NB % kBatchGroup == 0 ? kBatchGroup : 1;
 #pragma unroll
-        for (int q = 0; q < BPL; q++) {
-            const int b = j + LPR * q;
+        for (int b0 = 0; b0 < NB; b0 += CG) {
+            float t[BPL][CG];
 #pragma unroll
-            for (int bi = 0; bi < NB; bi++) {
-                const float xsv = sxs[bi * bpr + b];
-                float term = 0.0f;
-                if (swk[q] != 0.0f && xsv != 0.0f) {
-                    const int8_t* xb = sq + (bi * bpr + b) * 32;
-                    const uint4 xe = *reinterpret_cast<const uint4*>(xb);
-                    const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
-                    term = (float)k4_block_dot(R.w[k][q], xe, xo) * (swk[q] * xsv);
+            for (int q = 0; q < BPL; q++) {
+                const int b = j + LPR * q;
+#pragma unroll
+                for (int c = 0; c < CG; c++) {
+                    const int bi = b0 + c;
+                    const float xsv = sxs[bi * bpr + b];
+                    float term = 0.0f;
+                    if (swk[q] != 0.0f && xsv != 0.0f) {
+                        const int8_t* xb = sq + (bi * bpr + b) * 32;
+                        const uint4 xe = *reinterpret_cast<const uint4*>(xb);
+                        const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
+                        term = (float)k4_block_dot(R.w[k][q], xe, xo) * (swk[q] * xsv);
+                    }
+                    t[q][c] = term;
                 }
-                t[q][bi] = term;
+            }
+            float acc[CG];
+#pragma unroll
+            for (int c = 0; c < CG; c++) acc[c] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < BPL; q++) gather_add_n<LPR, CG>(acc, t[q]);
+#pragma unroll
+            for (int c = 0; c < CG; c++) {
+                asm volatile("" : "+v"(acc[c]));  // see row_sum
+                res[b0 + c] = acc[c];
             }
         }
-#pragma unroll
-        for (int bi = 0; bi < NB; bi++) res[bi] = 0.0f;
-#pragma unroll
-        for (int q = 0; q < BPL; q++) gather_add_n<LPR, NB>(res, t[q]);
     };
 
     const int G = (int)gridDim.x;
