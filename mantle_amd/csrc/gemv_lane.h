@@ -181,9 +181,6 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         float s = 0.0f;
 #pragma unroll
         for (int q = 0; q < BPL; q++) s = gather_add<LPR>(s, t[q]);
-        // materialise the sum here: left alone, the adds sink into the store
-        // branch of the last lane and keep every DPP move's result live until then
-        asm volatile("" : "+v"(s));
         return s;
     };
     // All NB batch columns of matrix k: per block the terms of every column,
@@ -219,7 +216,9 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
             for (int q = 0; q < BPL; q++) gather_add_n<LPR, CG>(acc, t[q]);
 #pragma unroll
             for (int c = 0; c < CG; c++) {
-                asm volatile("" : "+v"(acc[c]));  // see row_sum
+                // materialise the sum here: left alone, the adds sink into the
+                // last lane's store branch and keep every DPP result live until then
+                asm volatile("" : "+v"(acc[c]));
                 res[b0 + c] = acc[c];
             }
         }
