@@ -152,7 +152,10 @@ __global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
     }
 }
 
-__global__ __launch_bounds__(256) void attention_prefill_bf16(PrefillArgs a) {
+// Three waves per SIMD (three workgroups per CU, 108 KB of LDS): the
+// register file then holds 165 VGPRs per lane, enough without spills, and one
+// wave's softmax overlaps another's MFMAs.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_prefill_bf16(PrefillArgs a) {
     __shared__ __align__(16) uint16_t kt[2][kPfKeys * kPfKPitch];
     __shared__ __align__(16) uint16_t vt[2][kPfHd * kPfVPitch];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
