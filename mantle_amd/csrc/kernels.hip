@@ -60,9 +60,57 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float* __restrict__ o
     for (int i = threadIdx.x; i < n; i += kThreads) out[i] = (x[i] * scale) * weight[i];
 }
 
+// Rows of a multiple of 64 values, up to 16 per thread (n <= 4096): the row is
+// loaded once as float4 by every thread, staged transposed in LDS for the
+// parity lanes (float4 runs), and scaled from registers.
+static constexpr int kRowsMaxPer = 4;  // float4 per thread
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                                const float* __restrict__ weight, float eps, int n,
+                                                                int isa) {
+    extern __shared__ __align__(16) float tv[];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)row * n);
+    const float4* w4 = reinterpret_cast<const float4*>(weight);
+    float4* o4 = reinterpret_cast<float4*>(out + (size_t)row * n);
+    const int n4 = n >> 2, P = rms_stage_pitch(n);
+    float4 v[kRowsMaxPer], g[kRowsMaxPer];
+#pragma unroll
+    for (int r = 0; r < kRowsMaxPer; r++) {
+        const int c = tid + r * kThreads;
+        const int cc = c < n4 ? c : 0;  // unconditional loads; the surplus is not used
+        v[r] = x4[cc];
+        g[r] = w4[cc];
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsMaxPer; r++) {
+        const int c = tid + r * kThreads;
+        if (c < n4) {  // value i = 4c + e goes to staged row i % 16, column i / 16
+            const int i = 4 * c;
+            tv[((i + 0) & 15) * P + ((i + 0) >> 4)] = v[r].x;
+            tv[((i + 1) & 15) * P + ((i + 1) >> 4)] = v[r].y;
+            tv[((i + 2) & 15) * P + ((i + 2) >> 4)] = v[r].z;
+            tv[((i + 3) & 15) * P + ((i + 3) >> 4)] = v[r].w;
+        }
+    }
+    __syncthreads();
+    const float scale = wg_rms_scale_rt(tv, n, eps, isa, tv + 16 * P);
+#pragma unroll
+    for (int r = 0; r < kRowsMaxPer; r++) {
+        const int c = tid + r * kThreads;
+        if (c < n4)
+            o4[c] = make_float4((v[r].x * scale) * g[r].x, (v[r].y * scale) * g[r].y, (v[r].z * scale) * g[r].z,
+                                (v[r].w * scale) * g[r].w);
+    }
+}
+
 hipError_t launch_rmsnorm(float* out, const float* x, const float* weight, float eps, int n, int rows, int isa,
                           hipStream_t stream) {
     if (!out || !x || !weight || n <= 0 || rows <= 0) return hipErrorInvalidValue;
+    if (n % 64 == 0 && n <= kRowsMaxPer * 4 * kThreads && !(((uintptr_t)out | (uintptr_t)x | (uintptr_t)weight) & 15)) {
+        const size_t smem = sizeof(float) * (16 * (size_t)rms_stage_pitch(n) + 4);
+        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kThreads), smem, stream, out, x, weight, eps, n, isa);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, stream, out, x, weight, eps, n, isa);
     return hipGetLastError();
 }

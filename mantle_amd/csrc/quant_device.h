@@ -428,6 +428,68 @@ __device__ __forceinline__ float wg_rms_scale_t(const float* tv, float eps, int 
     return scale;
 }
 
+// wg_rms_scale_t for a run-time row length n (a multiple of 64, staged with
+// rms_stage_pitch(n)); the same orders, the wave-0 result returned to every
+// thread through red[0].
+__device__ __forceinline__ float wg_rms_scale_rt(const float* tv, int n, float eps, int isa, float* red) {
+    const int P = rms_stage_pitch(n);
+    const int m4 = n / 64;
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        float sum = 0.0f;
+        if (isa == kIsaAvx512) {
+            float acc = 0.0f;
+            if (tid < 16) {
+                const float4* r = reinterpret_cast<const float4*>(tv + tid * P);
+                for (int c = 0; c < m4; c++) {
+                    const float4 a = r[c];
+                    acc = __builtin_fmaf(a.x, a.x, acc);
+                    acc = __builtin_fmaf(a.y, a.y, acc);
+                    acc = __builtin_fmaf(a.z, a.z, acc);
+                    acc = __builtin_fmaf(a.w, a.w, acc);
+                }
+            }
+            float part[16];
+#pragma unroll
+            for (int l = 0; l < 16; l++) part[l] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), l));
+            sum = part[0];
+#pragma unroll
+            for (int l = 1; l < 16; l++) sum += part[l];
+        } else if (isa == kIsaAvx2) {
+            float acc = 0.0f;
+            if (tid < 8) {
+                const float4* ra = reinterpret_cast<const float4*>(tv + tid * P);
+                const float4* rb = reinterpret_cast<const float4*>(tv + (tid + 8) * P);
+                for (int c = 0; c < m4; c++) {
+                    const float4 a = ra[c], b = rb[c];
+                    acc = __builtin_fmaf(a.x, a.x, acc);
+                    acc = __builtin_fmaf(b.x, b.x, acc);
+                    acc = __builtin_fmaf(a.y, a.y, acc);
+                    acc = __builtin_fmaf(b.y, b.y, acc);
+                    acc = __builtin_fmaf(a.z, a.z, acc);
+                    acc = __builtin_fmaf(b.z, b.z, acc);
+                    acc = __builtin_fmaf(a.w, a.w, acc);
+                    acc = __builtin_fmaf(b.w, b.w, acc);
+                }
+            }
+            float part[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++) part[l] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), l));
+            sum = part[0];
+#pragma unroll
+            for (int l = 1; l < 8; l++) sum += part[l];
+        } else {
+            for (int i = 0; i < n; i++) {
+                const float v = tv[(i & 15) * P + (i >> 4)];
+                sum += v * v;
+            }
+        }
+        if (tid == 0) red[0] = rms_scale(sum, n, eps);
+    }
+    __syncthreads();
+    return red[0];
+}
+
 template <int NT = kThreads>
 __device__ void wg_quantize_vec_pre(const float* __restrict__ x, const float* __restrict__ weight, float eps, int n,
                                     int isa, float* vals, float* red, int8_t* q_out, float* s_out, float* norm_out,

@@ -21,7 +21,7 @@ def _reset_isa(hip):
 
 
 @pytest.mark.parametrize("isa", ISAS)
-@pytest.mark.parametrize("n", [7, 128, 1000, 1024, 2048])
+@pytest.mark.parametrize("n", [7, 128, 1000, 1024, 2048, 3072, 4096])
 def test_rmsnorm_bitexact(hip, oracle, isa, n):
     rng = np.random.default_rng(n + isa)
     x = (rng.standard_normal(n) * 3).astype(np.float32)
