@@ -87,15 +87,6 @@ static inline int lane_small_rows() {
     return v;
 }
 
-// Lanes per row of the lane GEMV on small matrices (8 or 16).
-static inline int lane_small_lpr() {
-    static int v = [] {
-        const char* e = getenv("MANTLE_HIP_GEMV_SMALL_LPR");
-        return e && atoi(e) == 8 ? 8 : 16;
-    }();
-    return v;
-}
-
 static inline int gemv_max_wgs() {
     static int v = [] {
         const char* e = getenv("MANTLE_HIP_GEMV_MAX_WGS");

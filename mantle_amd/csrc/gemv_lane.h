@@ -53,20 +53,32 @@ __device__ __forceinline__ void gather_add_n(float (&s)[NB], const float (&t)[NB
     }
 }
 
-template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D>
+// Rows wider than a lane's registers hold (BPLT > BPL blocks per lane) are
+// processed in NCHK pieces of BPL blocks per lane, in block order: piece c
+// covers blocks LPR*BPL*c .. LPR*BPL*(c+1)-1, so the last lane's running sum
+// continues the CPU's ordered sum from one piece to the next.  Blocks past the
+// row in the last piece re-read the row's last block and add exactly 0.
+template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D, int BPLT_ = 0>
 __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     static_assert(LPR == 8 || LPR == 16, "8 or 16 lanes per row");
+    constexpr int BPLT = BPLT_ ? BPLT_ : BPL;              // blocks per lane over the whole row
+    constexpr int NCHK = (BPLT + BPL - 1) / BPL;           // pieces per row
+    constexpr bool CHUNKED = NCHK > 1;
+    static_assert(!CHUNKED || NB == 1, "pieced rows at batch 1 only");
+    static_assert(!CHUNKED || D == 2, "pieces of a row are double-buffered");
+    // 8-lane whole rows take their u6 bytes and supers as u32 words
+    constexpr bool WORDS = LPR == 8 && !CHUNKED;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NT = NW * 64;
     constexpr int NSUB = EPI == kEpiSiluMul ? 2 : 1;
     constexpr int RPW = 64 / LPR;   // rows per wave
     constexpr int RPU = RPW * NW;   // rows per unit
-    constexpr int BPR = LPR * BPL;  // blocks per row
-    // LPR 8: the u6 bytes of a row arrive as u32 words (lane j: bytes j*BPL ..
-    // j*BPL+BPL-1) and the f16 supers as words; LPR 16: one byte / half each.
-    constexpr int NQ = LPR == 8 ? BPL / 4 : BPL;
-    constexpr int NS = LPR == 8 ? BPL / 2 : BPL;
-    static_assert(LPR == 16 || BPL % 4 == 0, "8-lane rows take 4k blocks per lane");
+    constexpr int BPR = LPR * BPLT;  // blocks per row
+    // WORDS: the u6 bytes of a row arrive as u32 words (lane j: bytes j*BPL ..
+    // j*BPL+BPL-1) and the f16 supers as words; otherwise one byte / half each.
+    constexpr int NQ = WORDS ? BPL / 4 : BPL;
+    constexpr int NS = WORDS ? BPL / 2 : BPL;
+    static_assert(!WORDS || BPL % 4 == 0, "8-lane rows take 4k blocks per lane");
     const int bpr = BPR;
     int8_t* sq = reinterpret_cast<int8_t*>(smem);
     float* sxs = reinterpret_cast<float*>(smem + NB * bpr * 32);
@@ -81,10 +93,17 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         uint4 w[NSUB][BPL];  // nibbles of blocks j, j+LPR, ...
         uint32_t sub[NSUB][NQ];
         uint32_t sup[NSUB][NS];
-        int unit, ms, row;
+        int unit, ms, row, piece, chunk;
         float resid;
     };
-    auto load_unit = [&](Unit& R, int unit) {
+    const int G = (int)gridDim.x;
+    // Piece i of this workgroup: unit blockIdx.x + (i / NCHK) * G, chunk i % NCHK.
+    auto unit_of = [&](int i) { return (int)blockIdx.x + (NCHK == 1 ? i : i / NCHK) * G; };
+    auto load_unit = [&](Unit& R, int piece) {
+        const int unit = unit_of(piece);
+        const int chunk = NCHK == 1 ? 0 : piece % NCHK;
+        R.piece = piece;
+        R.chunk = chunk;
         R.unit = unit;
         int ms = 0, first = 0;
         if (EPI != kEpiSiluMul) {
@@ -101,13 +120,26 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         for (int k = 0; k < NSUB; k++) {
             const K4Mat M = pick_mat(p, NSUB == 2 ? k : ms);
             const uint32_t rc = (uint32_t)(row < M.rows ? row : M.rows - 1);
+            if constexpr (CHUNKED) {
+                const unsigned char* nb = reinterpret_cast<const unsigned char*>(M.nib);
+#pragma unroll
+                for (int q = 0; q < BPL; q++) {
+                    const int qg = chunk * BPL + q;
+                    const uint32_t b = (uint32_t)(j + LPR * (qg < BPLT ? qg : BPLT - 1));
+                    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nb + (rc * BPR + b) * 16u));
+                    R.w[k][q] = make_uint4(v.x, v.y, v.z, v.w);
+                    R.sub[k][q] = M.sub[rc * BPR + b];
+                    R.sup[k][q] = M.sup[rc * (BPR / 8) + (b >> 3)];
+                }
+                continue;
+            }
             const unsigned char* nb = reinterpret_cast<const unsigned char*>(M.nib) + (rc * BPR + j) * 16u;
 #pragma unroll
             for (int q = 0; q < BPL; q++) {
                 const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(nb + q * LPR * 16));
                 R.w[k][q] = make_uint4(v.x, v.y, v.z, v.w);
             }
-            if constexpr (LPR == 8) {
+            if constexpr (WORDS) {
                 const uint32_t* sw = reinterpret_cast<const uint32_t*>(M.sub + rc * BPR + j * BPL);
                 const uint32_t* su = reinterpret_cast<const uint32_t*>(M.sup + rc * BPL);
 #pragma unroll
@@ -132,7 +164,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     };
     // LPR 8: u6 byte of block b = j + 8q is held by lane b / BPL of the group, word (b % BPL) / 4.
     auto sub_byte = [&](const Unit& R, int k, int q) -> uint32_t {
-        if constexpr (LPR == 16) {
+        if constexpr (!WORDS) {
             return R.sub[k][q];
         } else {
             const int b = j + 8 * q;
@@ -148,7 +180,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         }
     };
     auto super_half = [&](const Unit& R, int k, int q) -> uint16_t {
-        if constexpr (LPR == 16) {
+        if constexpr (!WORDS) {
             return (uint16_t)R.sup[k][q];
         } else {
             const uint32_t supw = R.sup[k][q >> 1];
@@ -161,15 +193,18 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
 #pragma unroll
         for (int q = 0; q < BPL; q++) sw[q] = k4_scale(super_half(R, k, q), (uint8_t)sub_byte(R, k, q));
     };
-    auto row_sum = [&](const Unit& R, int k, int bi, const float (&swk)[BPL]) -> float {
+    // s0: the running sum of the row's earlier pieces (0 for the first).
+    auto row_sum = [&](const Unit& R, int k, int bi, const float (&swk)[BPL], float s0) -> float {
         float t[BPL];
 #pragma unroll
         for (int q = 0; q < BPL; q++) {
-            const int b = j + LPR * q;
+            const int qg = R.chunk * BPL + q;
+            const bool live = !CHUNKED || BPLT % BPL == 0 || qg < BPLT;
+            const int b = j + LPR * (live ? qg : BPLT - 1);
             const float sw = swk[q];
             const float xsv = sxs[bi * bpr + b];
             float term = 0.0f;
-            if (sw != 0.0f && xsv != 0.0f) {
+            if (live && sw != 0.0f && xsv != 0.0f) {
                 const int8_t* xb = sq + (bi * bpr + b) * 32;
                 const uint4 xe = *reinterpret_cast<const uint4*>(xb);
                 const uint4 xo = *reinterpret_cast<const uint4*>(xb + 16);
@@ -178,7 +213,7 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
             t[q] = term;
         }
         // Block b = jj + LPR*q lives in lane jj: the last lane adds them in block order.
-        float s = 0.0f;
+        float s = s0;
 #pragma unroll
         for (int q = 0; q < BPL; q++) s = gather_add<LPR>(s, t[q]);
         return s;
@@ -224,9 +259,8 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         }
     };
 
-    const int G = (int)gridDim.x;
     static_assert(D == 1 || D == 2, "one or two units in flight");
-    Unit A, Bq;  // D == 2: units blockIdx.x + (2k)G in A, + (2k+1)G in Bq
+    Unit A, Bq;  // D == 2: the workgroup's even pieces in A, odd ones in Bq
     PHASE_SLOT();
     PHASE(0);
     // Activation loads first: they must not queue behind the weight stream.
@@ -274,9 +308,9 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight stream
-    load_unit(A, blockIdx.x);
-    const bool two = D == 2 && (int)blockIdx.x + G < p.ntiles;
-    if (two) load_unit(Bq, blockIdx.x + G);
+    load_unit(A, 0);
+    const bool two = D == 2 && unit_of(1) < p.ntiles;
+    if (two) load_unit(Bq, 1);
     PHASE(1);
     if constexpr (PRO == kProQx) {
         PHASE_AFTER(2, qpre[0].x);
@@ -324,20 +358,27 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     PHASE(3);
     unsigned long long best = 0;
     int nstep = 0;
+    float carry[NSUB] = {};  // running sums of the current row's earlier pieces
     auto step = [&](Unit& cur) {
         float res[NSUB][NB];
 #pragma unroll
         for (int k = 0; k < NSUB; k++) {
             float swk[BPL];
             block_scales(cur, k, swk);
-            if constexpr (NB == 1) res[k][0] = row_sum(cur, k, 0, swk);
+            if constexpr (NB == 1) res[k][0] = row_sum(cur, k, 0, swk, CHUNKED ? carry[k] : 0.0f);
             else row_sums(cur, k, swk, res[k]);
         }
         const int row = cur.row, ms = cur.ms, unit = cur.unit;
+        const bool last = !CHUNKED || cur.chunk == NCHK - 1;
         const float resid = cur.resid;
-        const int ahead = cur.unit + D * G;
-        if (ahead < p.ntiles) load_unit(cur, ahead);  // refill while the results are written
+        const int ahead = cur.piece + D;
+        if (unit_of(ahead) < p.ntiles) load_unit(cur, ahead);  // refill while the results are written
         else cur.unit = -1;
+        if constexpr (CHUNKED) {
+#pragma unroll
+            for (int k = 0; k < NSUB; k++) carry[k] = last ? 0.0f : res[k][0];
+            if (!last) return;
+        }
         nstep++;
         if (nstep == 1) PHASE(4);
         if constexpr (EPI == kEpiSiluMul) {
@@ -413,13 +454,14 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     }
 }
 
-template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D = 2>
+template <int EPI, int LPR, int BPL, int NB, int NW, int PRO, int D = 2, int BPLT = 0>
 static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
-    auto kern = k4_gemv_lane_kernel<EPI, LPR, BPL, NB, NW, PRO, D>;
+    auto kern = k4_gemv_lane_kernel<EPI, LPR, BPL, NB, NW, PRO, D, BPLT>;
     constexpr int RPU = (64 / LPR) * NW;
     const size_t stage = PRO == kProNorm ? ((size_t)16 * rms_stage_pitch(p.bpr * 32) + 4) * 4 : 40 * 4;
     const size_t smem = (size_t)NB * p.bpr * 36 + stage;
     if (smem > 64 * 1024) return hipErrorInvalidValue;
+    if (EPI == kEpiSiluMul && p.q_out && RPU != 32) return hipErrorInvalidValue;  // quantises 32-row units
     int units = 0;
     if (EPI == kEpiSiluMul) {
         p.wg_begin[0] = 0;
@@ -435,7 +477,8 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     p.rpw = RPU;
     // D == 1: one unit per workgroup (the dispatcher keeps the CUs full);
     // D > 1: at most one resident wave of workgroups, units dealt out evenly
-    int slots = D == 1 ? units : resident_wgs(kern, smem);
+    // (pieced rows: one unit per workgroup, its pieces double-buffered)
+    int slots = D == 1 || BPLT > BPL ? units : resident_wgs(kern, smem);
     if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
     const int per = (units + slots - 1) / slots;
     const int grid = (units + per - 1) / per;
@@ -443,36 +486,63 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Large matrices (the logits): 8 lanes per row, four-wave workgroups of one
-// 32-row unit each, as many as there are units.  Measured on the logits shape,
-// this beats a resident grid that streams several units per workgroup (ring
-// depth 1-4, 8 or 16 lanes per row, 2-8 waves): the dispatcher refills CUs as
-// workgroups finish, and the per-workgroup prologue overlaps other loads.
+// Blocks per lane of one piece of a row that spans BPLT blocks per lane: whole
+// rows up to MAXC blocks per lane, else the fewest pieces of at most MAXC.
+template <int BPLT, int MAXC>
+constexpr int piece_bpl() {
+    constexpr int n = (BPLT + MAXC - 1) / MAXC;
+    return (BPLT + n - 1) / n;
+}
+
+// Large matrices (the logits): four-wave workgroups of one 32-row unit each,
+// as many as there are units; 8 lanes per row where the row fits 8 lanes'
+// registers.  Measured on the logits shape, this beats a resident grid that
+// streams several units per workgroup (ring depth 1-4, 8 or 16 lanes per row,
+// 2-8 waves): the dispatcher refills CUs as workgroups finish, and the
+// per-workgroup prologue overlaps other loads.
 // Small ones are latency-bound, and what bounds them is the loads each wave
 // must issue before its data starts to arrive: 16 lanes per row and
 // one-wave workgroups of 4 rows spread them over every CU.  The quantising
 // SiLU epilogue needs 32-row units: 16 lanes per row in eight-wave workgroups.
+// Rows of more than 6 blocks per lane (4 for gate and up) go in double-buffered pieces.
 template <int EPI, int BPR, int NB, int PRO>
 static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
+    static_assert(BPR % 16 == 0, "16-lane rows need a multiple of 16 blocks");
+    constexpr int T16 = BPR / 16;             // blocks per lane at 16 lanes per row
+    // two matrices' blocks per lane (gate and up) with the SiLU epilogue: at most 4
+    constexpr int C16 = piece_bpl<T16, EPI == kEpiSiluMul ? 4 : 6>();
+    constexpr bool L8 = BPR % 32 == 0 && BPR / 8 <= 8;  // whole 8-lane rows (u6 words: 4k blocks per lane)
     int rows = 0;
     for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
     const bool q32 = EPI == kEpiSiluMul && p.q_out;
-    if (rows > lane_small_rows()) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 1>(p, stream);
-    if (lane_small_lpr() == 8) {
-        if (q32) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO>(p, stream);
-        return launch_lane_gemv<EPI, 8, BPR / 8, NB, 1, PRO>(p, stream);
+    // (16-lane rows make 16-row units at four waves: the quantising SiLU
+    // epilogue takes the eight-wave instance below)
+    if (rows > lane_small_rows() && (L8 || !q32)) {
+        if constexpr (L8) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 1>(p, stream);
+        else if constexpr (C16 == T16) return launch_lane_gemv<EPI, 16, T16, NB, 4, PRO, 1>(p, stream);
+        else return launch_lane_gemv<EPI, 16, C16, NB, 4, PRO, 2, T16>(p, stream);
     }
-    if (q32) return launch_lane_gemv<EPI, 16, BPR / 16, NB, 8, PRO>(p, stream);
-    return launch_lane_gemv<EPI, 16, BPR / 16, NB, 1, PRO>(p, stream);
+    if constexpr (C16 == T16) {
+        if (q32) return launch_lane_gemv<EPI, 16, T16, NB, 8, PRO>(p, stream);
+        return launch_lane_gemv<EPI, 16, T16, NB, 1, PRO>(p, stream);
+    } else {
+        if (q32) return launch_lane_gemv<EPI, 16, C16, NB, 8, PRO, 2, T16>(p, stream);
+        return launch_lane_gemv<EPI, 16, C16, NB, 1, PRO, 2, T16>(p, stream);
+    }
 }
 
 template <int EPI, int NB, int PRO>
 static hipError_t try_lane_gemv(GemvParams& p, hipStream_t stream, bool* used) {
     *used = true;
     switch (p.bpr) {
+        // Qwen3 0.6B (1024 / 2048 / 3072 columns), 4B (2560 / 4096 / 9728), 8B (4096 / 12288)
         case 32: return launch_lane_gemv_sized<EPI, 32, NB, PRO>(p, stream);
         case 64: return launch_lane_gemv_sized<EPI, 64, NB, PRO>(p, stream);
+        case 80: return launch_lane_gemv_sized<EPI, 80, NB, PRO>(p, stream);
         case 96: return launch_lane_gemv_sized<EPI, 96, NB, PRO>(p, stream);
+        case 128: return launch_lane_gemv_sized<EPI, 128, NB, PRO>(p, stream);
+        case 304: return launch_lane_gemv_sized<EPI, 304, NB, PRO>(p, stream);
+        case 384: return launch_lane_gemv_sized<EPI, 384, NB, PRO>(p, stream);
         default: *used = false; return hipSuccess;
     }
 }

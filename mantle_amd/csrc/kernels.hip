@@ -415,6 +415,19 @@ static hipError_t launch_gemv(GemvParams& p, GemvEpi epi, hipStream_t stream) {
     }
 }
 
+// Largest batch whose int8 activations, scales and one row's partial sums
+// fit the tile kernel's 64 KiB of LDS; wider batches run as several launches
+// over consecutive activation rows (the columns of a batch are independent).
+static int tile_batch_fit(int bpr, size_t stage) {
+    int b = 8;
+    while (b > 1) {
+        const size_t work = (size_t)(b | 1) * bpr * 4;
+        if ((size_t)b * bpr * 36 + (work > stage ? work : stage) <= 64 * 1024) break;
+        b--;
+    }
+    return b;
+}
+
 hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, int cols, const int8_t* qx,
                                const float* xs, int batch, GemvEpi epi, unsigned long long* argmax_key,
                                hipStream_t stream) {
@@ -440,6 +453,18 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
     bool used = false;
     hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
     if (used) return e;
+    const int fit = tile_batch_fit(p.bpr, 17 * 4);
+    if (batch > fit) {  // store epilogue only (batch > 1)
+        for (int b0 = 0; b0 < batch; b0 += fit) {
+            float* o[3];
+            for (int i = 0; i < nmat; i++) o[i] = outs[i] + (size_t)b0 * mats[i].rows;
+            const int nb = batch - b0 < fit ? batch - b0 : fit;
+            e = launch_k4_gemv_w4a8(mats, o, nmat, cols, qx + (size_t)b0 * p.bpr * 32, xs + (size_t)b0 * p.bpr, nb,
+                                    epi, argmax_key, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     return launch_gemv<kModeW4A8>(p, epi, stream);
 }
 
@@ -474,6 +499,18 @@ hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int 
     bool used = false;
     hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
     if (used) return e;
+    const int fit = tile_batch_fit(p.bpr, norm_w ? ((size_t)p.bpr * 32 + 17) * 4 : 17 * 4);
+    if (batch > fit) {  // store epilogue only (batch > 1)
+        for (int b0 = 0; b0 < batch; b0 += fit) {
+            float* o[3];
+            for (int i = 0; i < nmat; i++) o[i] = outs[i] + (size_t)b0 * mats[i].rows;
+            const int nb = batch - b0 < fit ? batch - b0 : fit;
+            e = launch_k4_gemv_w4a8_fused(mats, o, nmat, cols, x + (size_t)b0 * cols, norm_w, eps, isa, nb, epi,
+                                          argmax_key, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     e = launch_gemv<kModeW4A8Fused>(p, epi, stream);
     if (e != hipSuccess || !q_out) return e;
     // the tile kernel has no quantising epilogue: a separate quantiser launch

@@ -13,6 +13,14 @@ TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=128, ffn=
 LANE = dict(n_layers=2, d_model=1024, n_heads=16, n_kv_heads=8, head_dim=128, ffn=3072, vocab=2048,
             rope_base=1e6, eps=1e-6, tie_embeddings=1)
 
+# Two blocks at Qwen3-4B's and Qwen3-8B's row widths (2560 / 4096 / 9728 and
+# 4096 / 12288 columns): 80-, 128-, 304- and 384-block rows, the wide ones in
+# pieces; 20000 logits rows take the large-matrix launch.
+WIDE4B = dict(n_layers=2, d_model=2560, n_heads=32, n_kv_heads=8, head_dim=128, ffn=9728, vocab=20000,
+              rope_base=1e6, eps=1e-6, tie_embeddings=1)
+WIDE8B = dict(n_layers=2, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=12288, vocab=20000,
+              rope_base=1e6, eps=1e-6, tie_embeddings=0)
+
 
 def pack(path: str, seed: int, cfg: dict) -> str:
     from mantle_amd import mcf

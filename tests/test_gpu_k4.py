@@ -9,7 +9,9 @@ torch = pytest.importorskip("torch")
 
 from tests import gpu_util as g  # noqa: E402
 
-SHAPES = [(2, 96), (37, 100), (64, 1000), (3072, 1024), (1024, 3072), (2048, 1024), (151936, 1024)]
+SHAPES = [(2, 96), (37, 100), (64, 1000), (3072, 1024), (1024, 3072), (2048, 1024), (151936, 1024),
+          # Qwen3-4B / 8B row widths: 80, 128, 304 (pieced) and 384 (pieced) blocks; 20000 rows: large launch
+          (6144, 2560), (2560, 4096), (2560, 9728), (20000, 2560), (4096, 12288), (20000, 4096)]
 
 
 def _weights(rows, cols, seed):

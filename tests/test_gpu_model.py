@@ -47,6 +47,29 @@ def test_greedy_logits_bitexact(hip, tiny_path, lane_path, shape, isa):
         om.close()
 
 
+@pytest.mark.parametrize("shape", ["wide4b", "wide8b"])
+def test_wide_rows_logits_bitexact(hip, tmp_models, shape):
+    """Qwen3-4B / 8B row widths: 80/128-block rows whole, 304/384-block rows
+    (the down projections) in double-buffered pieces, 20000 logits rows on the
+    large-matrix launch -- logits and residual stream bit-identical per step."""
+    import mantle_amd
+    cfg = models.WIDE4B if shape == "wide4b" else models.WIDE8B
+    path = models.pack(str(tmp_models / f"{shape}.mcf"), 7, cfg)
+    rt = mantle_amd.new_backend("hip").load_model(path, max_context=32)
+    om = models.oracle_model(path, cfg, 32)
+    try:
+        tok = 5
+        for step in range(6):
+            logits = rt.forward_token(tok)
+            nxt, want = om.forward_greedy(tok, want_logits=True)
+            np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+            np.testing.assert_array_equal(rt.hidden().view(np.uint32), om.hidden().view(np.uint32))
+            tok = nxt
+    finally:
+        rt.close()
+        om.close()
+
+
 @pytest.mark.parametrize("path", ["split", "single", "general"])
 def test_lane_long_context_attention_paths(hip, lane_path, path):
     """140 fused steps (past two 64-key chunks, the step's own K/V row inside
