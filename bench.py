@@ -220,6 +220,82 @@ def cpu_baseline(path, cfg, prompt, budget_s=15.0, max_tokens=24):
                        f"of Mantle's archsimd path (AVX-512 reduction order)")
 
 
+def weight_bytes_per_token(cfg):
+    """k4 weight bytes one decode token streams: every block matrix plus the lm_head
+    (the tied embedding when tie_embeddings), norms as fp32."""
+    from mantle_amd.mcf import payload_size
+    d, f, hd = cfg["d_model"], cfg["ffn"], cfg["head_dim"]
+    qd, kvd = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    layer = (payload_size(qd, d) + 2 * payload_size(kvd, d) + payload_size(d, qd) + 2 * payload_size(f, d)
+             + payload_size(d, f) + 4 * (2 * d + 2 * hd))
+    return cfg["n_layers"] * layer + payload_size(cfg["vocab"], d) + 4 * d
+
+
+def decode_run(rt, prompt, warmup, steps):
+    """Token-by-token prefill of `prompt` (as Mantle runs k4 prefill; the first
+    token also captures the step graph), then `warmup` untimed and `steps` timed
+    greedy decode steps.  Returns (decode seconds, prefill tok/s)."""
+    import torch
+    rt.prefill_tokens(prompt[:1])
+    rt.synchronize()
+    t0 = time.perf_counter()
+    for i in range(1, len(prompt), 1024):  # progress on long prompts
+        rt.prefill_tokens(prompt[i:i + 1024])
+        rt.synchronize()
+        if len(prompt) > 4096:
+            log(f"prefill {min(i + 1024, len(prompt))}/{len(prompt)} tokens, {time.perf_counter() - t0:.1f} s")
+    prefill_tps = (len(prompt) - 1) / (time.perf_counter() - t0)
+    if warmup:
+        rt.decode_steps(warmup)
+    rt.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rt.decode_steps(steps)
+    rt.synchronize()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, prefill_tps
+
+
+# Configs 4 and 5 (reported, not the headline): larger decoders after a long prompt.
+LARGE_MODELS = {"qwen3-4b": ("QWEN3_4B", 4, 2048), "qwen3-8b": ("QWEN3_8B", 5, 16384)}
+
+
+def large_model_run(args):
+    import mantle_amd
+    from mantle_amd import mcf
+    name, seed, plen = LARGE_MODELS[args.model]
+    cfg = getattr(mcf, name)
+    plen = args.prompt or plen
+    os.makedirs(args.model_dir, exist_ok=True)
+    path = os.path.join(args.model_dir, f"{args.model}_k4_seed{seed}.mcf")
+    t0 = time.perf_counter()
+    mcf.pack_cached(path, seed, cfg)
+    log(f"model ready in {time.perf_counter() - t0:.1f} s: {path}")
+    prompt = mcf.uniform_tokens(plen, cfg["vocab"], 1)
+    rt = mantle_amd.new_backend("hip").load_model(path, max_context=plen + args.warmup + args.steps + 8)
+    try:
+        dt, prefill_tps = decode_run(rt, prompt, args.warmup, args.steps)
+    finally:
+        rt.close()
+    tps = args.steps / dt
+    wb = weight_bytes_per_token(cfg)
+    kv_mid = 2 * cfg["n_layers"] * cfg["n_kv_heads"] * cfg["head_dim"] * 4 * (plen + args.warmup + args.steps // 2)
+    log(f"{args.model}: decode {tps:.1f} tok/s, prefill {prefill_tps:.1f} tok/s")
+    print(json.dumps({
+        "metric": f"decode tok/s @batch1, {args.model} k4 after a {plen}-token prompt",
+        "value": round(tps, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "k4 weights x int8 activations, int32 block dots, fp32 accumulation",
+        "data": f"synthetic: random-init N(0,0.02) weights seed {seed} packed to MCF k4, {plen} uniform token ids seed 1",
+        "config": {"workload": f"{args.model}-shape k4 greedy decode, batch 1 (BASELINE config {seed})",
+                   "prompt_tokens": plen, "parallelism": "none (1 GPU)"},
+        "prefill_tok_s": round(prefill_tps, 2),
+        "weight_bytes_per_token": wb,
+        "kv_bytes_per_token_mid": kv_mid,
+        "effective_gbs": round((wb + kv_mid) * tps / 1e9, 1),
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -231,6 +307,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill microbench (for rocprofv3)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the lm_head GEMV microbench and a copy calibration (for rocprofv3 --pmc runs)")
+    ap.add_argument("--model", default="qwen3-0.6b", choices=["qwen3-0.6b", *LARGE_MODELS],
+                    help="qwen3-4b / qwen3-8b: configs 4 / 5, a decode line of their own (not the headline)")
+    ap.add_argument("--prompt", type=int, default=0, help="prompt length for --model qwen3-4b / qwen3-8b")
     ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
     args = ap.parse_args()
     if args.gpus != 1:
@@ -243,6 +322,10 @@ def main():
     import mantle_amd
     from mantle_amd import mcf
     from mantle_amd.mcf import QWEN3_0_6B
+
+    if args.model != "qwen3-0.6b":
+        large_model_run(args)
+        return
 
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_microbench()}), flush=True)
@@ -263,21 +346,7 @@ def main():
     max_ctx = PROMPT_LEN + args.warmup + args.steps + 8
     rt = mantle_amd.new_backend("hip").load_model(path, max_context=max_ctx)
     try:
-        # prefill (token-by-token, as Mantle runs k4 prefill), includes graph capture on first use
-        rt.prefill_tokens(prompt[:1])
-        rt.synchronize()
-        t0 = time.perf_counter()
-        rt.prefill_tokens(prompt[1:])
-        prefill_tps = (PROMPT_LEN - 1) / (time.perf_counter() - t0)
-        if args.warmup:
-            rt.decode_steps(args.warmup)
-        rt.synchronize()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        rt.decode_steps(args.steps)
-        rt.synchronize()
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
+        dt, prefill_tps = decode_run(rt, prompt, args.warmup, args.steps)
     finally:
         rt.close()
     tps = args.steps / dt
@@ -301,7 +370,7 @@ def main():
             log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline failed: {e!r}")
-    bytes_per_token = 321_272_832
+    bytes_per_token = weight_bytes_per_token(QWEN3_0_6B)
     line = {
         "metric": "decode tok/s @batch1 + k4 GEMV HBM GB/s (% of peak), Qwen3-0.6B-shape k4",
         "value": round(tps, 2),

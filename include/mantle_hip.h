@@ -40,12 +40,15 @@ int mantleHipSetParityISA(int isa);
 int mantleHipGetParityISA(void);
 /* Decode-attention kernel variant for head_dim 64 / 128: no counterpart in
  * the reference (its CUDA backend has one attention kernel).  All variants are
- * bit-identical; the split one spreads a head over several CUs (two launches),
- * "single" keeps one workgroup per head, "general" is the any-head_dim kernel.
+ * bit-identical; the split ones spread a head over several CUs ("split", the
+ * default: two launches up to 8192 keys, "fused" beyond; "fused": one launch
+ * whose last workgroup per head does the softmax and V sum), "single" keeps
+ * one workgroup per head, "general" is the any-head_dim kernel.
  * A loaded model's captured step keeps the variant it was captured with. */
 #define MANTLE_HIP_ATTN_SPLIT 0
 #define MANTLE_HIP_ATTN_SINGLE 1
 #define MANTLE_HIP_ATTN_GENERAL 2
+#define MANTLE_HIP_ATTN_FUSED 3
 int mantleHipSetAttentionPath(int path);
 int mantleHipGetAttentionPath(void);
 

@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -639,9 +640,17 @@ __global__ __launch_bounds__(kThreads) void attention_decode_v4(AttnArgs a) {
 // keep the single-kernel arithmetic and order exactly.
 static constexpr int kSplitWgs = 16;
 
-// Kernel variant: kAttnPathSplit, kAttnPathSingle (attention_decode_v4) or
-// kAttnPathGeneral; the first read takes MANTLE_HIP_ATTN ("split", "single",
-// "general") when set_attention_path has not been called.
+// Kernel variant: kAttnPathSplit (two launches up to kSplitMaxCtx keys, the
+// one-launch attention_split_fused beyond), kAttnPathFused (always one
+// launch), kAttnPathSingle (attention_decode_v4) or kAttnPathGeneral; the
+// first read takes MANTLE_HIP_ATTN ("fused", "single", "general"; anything
+// else: split) when set_attention_path has not been called.
+//
+// Measured on MI355X, the one-launch form is the slower one where both apply
+// (Qwen3-0.6B decode 1135 -> 986 tok/s; Qwen3-8B after 16k tokens, 29 tok/s
+// against XXX for the split form): its V sum runs in one workgroup per
+// head, whose CU's memory pipeline then bounds the head's V stream, while the
+// second launch of the split form spreads it over head_dim / 32 workgroups.
 static std::atomic<int> g_attn_path{-1};
 
 int attention_path() {
@@ -649,6 +658,7 @@ int attention_path() {
     if (v >= 0) return v;
     const char* e = getenv("MANTLE_HIP_ATTN");
     v = kAttnPathSplit;
+    if (e && !strcmp(e, "fused")) v = kAttnPathFused;
     if (e && !strcmp(e, "single")) v = kAttnPathSingle;
     if (e && !strcmp(e, "general")) v = kAttnPathGeneral;
     int expect = -1;
@@ -657,15 +667,26 @@ int attention_path() {
 }
 
 bool set_attention_path(int path) {
-    if (path != kAttnPathSplit && path != kAttnPathSingle && path != kAttnPathGeneral) return false;
+    if (path != kAttnPathSplit && path != kAttnPathSingle && path != kAttnPathGeneral && path != kAttnPathFused)
+        return false;
     g_attn_path.store(path);
     return true;
 }
-static constexpr int kSplitMaxCtx = 8192;  // the V-sum launch keeps the probabilities in LDS
+// The V-sum launch keeps the probabilities in LDS: up to 128 KiB of the 160
+// KiB a gfx950 workgroup may hold.
+static constexpr int kSplitMaxCtx = 32768;
 
+// Dynamic LDS above 64 KiB is allowed per kernel before its launch.
+static hipError_t allow_lds(void (*kern)(AttnArgs), size_t bytes) {
+    if (bytes <= 64 * 1024) return hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)bytes);
+}
+
+// Scores of head h, chunks sidx, sidx + S, ... into the scores buffer (the
+// body of attention_scores_split; attention_split_fused runs it first).
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
-    extern __shared__ __align__(16) float lds[];
+__device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* lds, int h, int sidx, int S, int pos) {
     float* sq = lds;
     float* sk = lds + 128;
     float* sv = lds + 256;
@@ -673,18 +694,12 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     constexpr int kp = HD + 4;
     constexpr int kc = kAttnKeys;
     float* kt = lds + kAttnV4Hdr;
-    const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
-    const int S = gridDim.x / a.n_head;
     const int tid = threadIdx.x;
     const int kvh = h * a.kv_heads / a.n_head;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     const int nchunks = pos / kc + 1;
-    if (sidx >= nchunks) return;  // whole workgroup: no chunk of this context for it
     const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
     const int skip = a.fused ? pos : -1;
     float* sg = a.scores + (size_t)h * a.max_ctx;
-    PHASE_SLOT();
-    PHASE(0);
     const PrepRegs pr = prep_load<HD>(a, h, kvh, pos);
     __builtin_amdgcn_sched_barrier(0);
     ChunkRegs ck;
@@ -706,6 +721,144 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
         __syncthreads();
     }
     PHASE(3);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
+    const int S = gridDim.x / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    if (sidx >= pos / kAttnKeys + 1) return;  // whole workgroup: no chunk of this context for it
+    PHASE_SLOT();
+    PHASE(0);
+    scores_split_chunks<HD>(a, lds, h, sidx, S, pos);
+}
+
+// Softmax of head h's scores and the V sum of all its columns, by the last of
+// the head's S score workgroups to finish (attention_split_fused): Mantle's
+// softmax (ops.go:83-106: max, exponentials, ordered sum, x *= 1/sum) with the
+// probabilities in LDS (PG false) or in place in the scores buffer (PG true,
+// contexts too long for LDS), then out_d = sum_t p_t * v_t,d in key order, no
+// FMA, one column per lane of waves 0 .. HD/64-1.  The step's own V row
+// (fused) is read from the v input: the workgroup that appends it to the
+// cache may belong to another head and still be running.
+template <int HD, bool PG>
+__device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, int h, int pos) {
+    constexpr int VG = 32, NG = 5;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = h * a.kv_heads / a.n_head;
+    float* sg = a.scores + (size_t)h * a.max_ctx;
+    float* p = PG ? sg : lds;
+    float* red = PG ? lds : lds + (a.max_ctx + 31) / 32 * 32;
+    const bool pv_wave = wave < HD / 64;
+    const int d = wave * 64 + lane;
+    const float* vcol = a.cache_v + (size_t)kvh * a.head_stride + (pv_wave ? d : 0);
+    const float* vown = a.fused ? a.v + kvh * HD + (pv_wave ? d : 0) : vcol;
+    const int skip = a.fused ? pos : -1;
+    const size_t vs = (size_t)a.kv_stride;
+    float vr[NG][VG];
+    auto vissue = [&](float (&r)[VG], int t0) {
+#pragma unroll
+        for (int k = 0; k < VG; k++) {
+            const int t = t0 + k <= pos ? t0 + k : pos;
+            r[k] = *(t == skip ? vown : vcol + (size_t)t * vs);
+        }
+    };
+    if (pv_wave) {  // the V ring fills while the softmax runs
+#pragma unroll
+        for (int g = 0; g < NG; g++)
+            if (g * VG <= pos) vissue(vr[g], g * VG);
+    }
+    float m = -INFINITY;
+    for (int t = tid; t <= pos; t += kThreads) {
+        const float v = sg[t];
+        if (!PG) p[t] = v;
+        m = fmaxf(m, v);
+    }
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_down(m, off, 64));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int t = tid; t <= pos; t += kThreads) p[t] = fast_exp_scalar(p[t] - mx);
+    if (PG) __threadfence_block();
+    __syncthreads();
+    if (tid == 0) red[4] = ordered_sum(p, 1, pos + 1);
+    __syncthreads();
+    const float sum = red[4];
+    if (sum != 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int t = tid; t <= pos; t += kThreads) p[t] = p[t] * inv;
+    }
+    if (PG) __threadfence_block();
+    __syncthreads();
+    PHASE(5);
+    if (!pv_wave) return;
+    float acc = 0.0f;
+    for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            const int t0 = (g0 + gi) * VG;
+            if (t0 <= pos) {
+                float pg[VG];
+#pragma unroll
+                for (int i4 = 0; i4 < VG / 4; i4++) {
+                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
+                    pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                }
+                if (t0 + VG <= pos + 1) {
+#pragma unroll
+                    for (int k = 0; k < VG; k++) acc = acc + pg[k] * vr[gi][k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VG; k++) {
+                        const float nacc = acc + pg[k] * vr[gi][k];
+                        acc = t0 + k <= pos ? nacc : acc;
+                    }
+                }
+                if (t0 + NG * VG <= pos) vissue(vr[gi], t0 + NG * VG);
+            }
+        }
+    }
+    const int gi = h * HD + d;
+    a.out[gi] = acc;
+    if (a.q_out) {  // lanes 0-31 and 32-63: two whole int8 blocks of the Wo activation
+        float sc;
+        const int32_t qv = quant_lane32(acc, &sc);
+        a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
+        if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+    }
+}
+
+// One launch for the split-key attention: workgroup (h, s) scores its chunks
+// like attention_scores_split, then counts itself done on the head's counter;
+// the last of the head's S workgroups (the others have published their scores
+// with a device-scope fence before counting) resets the counter and runs
+// softmax_pv_head.  Every workgroup counts, with or without a chunk, so the
+// last one always arrives and every wave exits.
+template <int HD, bool PG>
+__global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
+    const int S = gridDim.x / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    PHASE_SLOT();
+    PHASE(0);
+    if (sidx < pos / kAttnKeys + 1) scores_split_chunks<HD>(a, lds, h, sidx, S, pos);
+    __threadfence();  // this workgroup's scores (and cache rows) before its arrival
+    __syncthreads();
+    __shared__ int is_last;  // outside the dynamic LDS that the softmax overwrites
+    if (threadIdx.x == 0) {
+        const unsigned old = atomicAdd(a.counters + h, 1u);
+        const int last = old == (unsigned)(S - 1);
+        if (last) atomicExch(a.counters + h, 0u);  // ready for the next launch
+        is_last = last;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();  // the other workgroups' scores, seen after their arrivals
+    PHASE(4);
+    softmax_pv_head<HD, PG>(a, lds, h, pos);
 }
 
 template <int HD>
@@ -805,6 +958,27 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     PHASE(2);
 }
 
+// The library's zeroed arrival counters (one set per device, allocated on first
+// use, never freed), for callers that pass none.  Each launch leaves them at
+// zero again, so launches stream-ordered after one another may share them;
+// launches that may overlap need counters of their own.
+static constexpr int kLibCounters = 4096;
+static unsigned* library_counters(int n_head) {
+    static std::mutex mu;
+    static unsigned* per_dev[64] = {};
+    if (n_head > kLibCounters) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!per_dev[dev]) {
+        unsigned* p = nullptr;
+        if (hipMalloc((void**)&p, sizeof(unsigned) * kLibCounters) != hipSuccess) return nullptr;
+        if (hipMemset(p, 0, sizeof(unsigned) * kLibCounters) != hipSuccess) { (void)hipFree(p); return nullptr; }
+        per_dev[dev] = p;
+    }
+    return per_dev[dev];
+}
+
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
         a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || (a.head_stride & 3) || a.max_ctx <= 0)
@@ -823,11 +997,32 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!lds_scores && !a.scores) return hipErrorInvalidValue;
     const int mode = attention_path();
     const bool fast_hd = a.head_dim == 128 || a.head_dim == 64;
+    if (fast_hd && (mode == kAttnPathFused || (mode == kAttnPathSplit && a.max_ctx > kSplitMaxCtx)) && a.scores) {
+        AttnArgs f = a;
+        if (!f.counters) f.counters = library_counters(a.n_head);
+        if (!f.counters) return hipErrorInvalidValue;
+        const int S = min(kSplitWgs, (a.max_ctx + kAttnKeys - 1) / kAttnKeys);
+        const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
+        const size_t smem_p = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
+        const bool pg = smem_p > 64 * 1024;  // probabilities in place in the scores buffer
+        const size_t smem = pg || smem_p < smem_a ? smem_a : smem_p;
+        const dim3 grid(a.n_head * S);
+        if (a.head_dim == 128) {
+            if (pg) hipLaunchKernelGGL((attention_split_fused<128, true>), grid, dim3(kThreads), smem, stream, f);
+            else hipLaunchKernelGGL((attention_split_fused<128, false>), grid, dim3(kThreads), smem, stream, f);
+        } else {
+            if (pg) hipLaunchKernelGGL((attention_split_fused<64, true>), grid, dim3(kThreads), smem, stream, f);
+            else hipLaunchKernelGGL((attention_split_fused<64, false>), grid, dim3(kThreads), smem, stream, f);
+        }
+        return hipGetLastError();
+    }
     if (fast_hd && mode == kAttnPathSplit && a.scores && a.max_ctx <= kSplitMaxCtx) {
         const int S = min(kSplitWgs, (a.max_ctx + kAttnKeys - 1) / kAttnKeys);
         const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
         const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
         const int nd = a.head_dim / 32;
+        const hipError_t e = allow_lds(a.head_dim == 128 ? attention_pv_split<128> : attention_pv_split<64>, smem_b);
+        if (e != hipSuccess) return e;
         if (a.head_dim == 128) {
             hipLaunchKernelGGL(attention_scores_split<128>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
             hipLaunchKernelGGL(attention_pv_split<128>, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);

@@ -101,12 +101,16 @@ struct AttnArgs {
     int isa;
     int8_t* q_out;         // optional: out also as Mantle's int8 blocks (permuted layout) ...
     float* q_scale;        // ... and their scales, for the next W4A8 GEMV (head_dim % 32 == 0)
+    unsigned* counters;    // [n_head] zeroed arrival counters of the one-launch split path (null: the
+                           // library's own, for callers that serialise their launches on one stream)
 };
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 // Decode-attention kernel variant for head_dim 64 / 128 (other sizes always
 // take the general kernel).  A model's captured step keeps the variant it was
 // captured with.
-enum AttnPath : int { kAttnPathSplit = 0, kAttnPathSingle = 1, kAttnPathGeneral = 2 };
+// kAttnPathFused is the split-key path in one launch (kAttnPathSplit takes it
+// past 8192 keys).
+enum AttnPath : int { kAttnPathSplit = 0, kAttnPathSingle = 1, kAttnPathGeneral = 2, kAttnPathFused = 3 };
 int attention_path();
 bool set_attention_path(int path);
 

@@ -46,6 +46,7 @@ struct mantleHipModel {
     std::vector<Layer> layers;
     // activations / scratch
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *scores = nullptr;
+    unsigned* attn_counters = nullptr;  // [n_heads] arrival counters of the one-launch split attention
     int8_t* qx = nullptr;
     float* xs = nullptr;
     float *cache_k = nullptr, *cache_v = nullptr;
@@ -104,6 +105,7 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         const bool qattn = (c.head_dim & 31) == 0;  // whole int8 blocks per head
         a.q_out = qattn ? m->qx : nullptr;
         a.q_scale = qattn ? m->xs : nullptr;
+        a.counters = m->attn_counters;
         TRY(launch_attention_decode(a, s));
         // attn.go:417 Wo on the re-quantised attention output (quantised by the
         // attention kernel), residual folded in
@@ -181,7 +183,7 @@ static bool json_number(const std::string& js, const char* key, double* out) {
 static void free_model(mantleHipModel* m) {
     if (!m) return;
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
-    void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->qx, m->xs, m->cache_k,
+    void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->attn_counters, m->qx, m->xs, m->cache_k,
                     m->cache_v, m->rope_cos, m->rope_sin, m->state, m->prompt, m->out_tokens};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -359,6 +361,8 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     CHECK(hipMalloc((void**)&m->act, sizeof(float) * c.ffn));
     CHECK(hipMalloc((void**)&m->logits, sizeof(float) * c.vocab));
     CHECK(hipMalloc((void**)&m->scores, sizeof(float) * (size_t)c.n_heads * max_ctx));
+    CHECK(hipMalloc((void**)&m->attn_counters, sizeof(unsigned) * c.n_heads));
+    CHECK(hipMemset(m->attn_counters, 0, sizeof(unsigned) * c.n_heads));
     CHECK(hipMalloc((void**)&m->qx, (size_t)big_blocks * 32));
     CHECK(hipMalloc((void**)&m->xs, sizeof(float) * big_blocks));
     const size_t kv_elems = (size_t)c.n_layers * max_ctx * m->kv_dim;

@@ -70,13 +70,13 @@ def test_wide_rows_logits_bitexact(hip, tmp_models, shape):
         om.close()
 
 
-@pytest.mark.parametrize("path", ["split", "single", "general"])
+@pytest.mark.parametrize("path", ["fused", "split", "single", "general"])
 def test_lane_long_context_attention_paths(hip, lane_path, path):
     """140 fused steps (past two 64-key chunks, the step's own K/V row inside
     a later chunk) on each attention variant: logits bit-identical to the oracle."""
     import mantle_amd
     from mantle_amd import _lib
-    _lib.call("mantleHipSetAttentionPath", {"split": 0, "single": 1, "general": 2}[path])
+    _lib.call("mantleHipSetAttentionPath", {"split": 0, "single": 1, "general": 2, "fused": 3}[path])
     try:
         rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=160)
         om = models.oracle_model(lane_path, models.LANE, 160)

@@ -113,7 +113,7 @@ def _fill(n, scale):  # fillTestData (internal/backend/simd/attn_test.go:240-244
     return np.array([scale * np.float32((i % 29) - 14) for i in range(n)], dtype=np.float32)
 
 
-ATTN_PATHS = {"split": 0, "single": 1, "general": 2}
+ATTN_PATHS = {"fused": 3, "split": 0, "single": 1, "general": 2}
 
 
 @pytest.mark.parametrize("path", list(ATTN_PATHS))
@@ -142,3 +142,29 @@ def test_attention_bitexact(hip, oracle, path, isa, n_head, kv_heads, head_dim, 
     got = g.host(out)
     g.call("mantleHipSetAttentionPath", 0)
     g.assert_bitexact(got, want, "attention")
+
+
+@pytest.mark.parametrize("path", ["split", "fused", "single"])
+def test_attention_long_context_bitexact(hip, oracle, path):
+    """16500 keys (Qwen3-8B's 16k-token prompt): the split path's V-sum launch
+    holds 66 KB of probabilities in LDS, the one-launch path keeps them in the
+    scores buffer (past its 64 KiB), the single-head kernel streams scores
+    through global memory."""
+    n_head, kv_heads, head_dim, pos = 32, 8, 128, 16499
+    kv = kv_heads * head_dim
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal(n_head * head_dim).astype(np.float32)
+    ck = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+    cv = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(head_dim))
+    g.call("mantleHipSetParityISA", 2)
+    g.call("mantleHipSetAttentionPath", ATTN_PATHS[path])
+    try:
+        out = g.empty(n_head * head_dim)
+        scratch = g.empty(n_head * (pos + 1))
+        g.call("mantleHipAttentionInnerF32Cache", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)), g.ptr(out),
+               g.ptr(scratch), pos, 0, kv, head_dim, n_head, kv_heads, pos + 1, ctypes.c_float(scale), g.stream())
+        want = oracle.attn_heads(2, q, ck, cv, pos, kv, head_dim, n_head, kv_heads, float(scale))
+        g.assert_bitexact(g.host(out), want, "attention")
+    finally:
+        g.call("mantleHipSetAttentionPath", 0)
