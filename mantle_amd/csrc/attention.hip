@@ -442,9 +442,15 @@ __device__ __forceinline__ void prep_finish(const AttnArgs& a, PrepRegs r, int k
         dst[lane] = x0;
         dst[lane + half] = x1;
         if (a.fused && wave > 0 && append) {
-            float* cache = (wave == 1 ? a.cache_k : a.cache_v) + (size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride;
-            cache[lane] = x0;
-            cache[lane + half] = x1;
+            if (wave == 2 && a.vt_stride > 0) {  // transposed V: one column per row of the cache
+                float* col = a.cache_v + (size_t)(kvh * HD + lane) * a.vt_stride + pos;
+                col[0] = x0;
+                col[(size_t)half * a.vt_stride] = x1;
+            } else {
+                float* cache = (wave == 1 ? a.cache_k : a.cache_v) + (size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride;
+                cache[lane] = x0;
+                cache[lane + half] = x1;
+            }
         }
     }
 }
@@ -735,41 +741,100 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     scores_split_chunks<HD>(a, lds, h, sidx, S, pos);
 }
 
-// Softmax of head h's scores and the V sum of all its columns, by the last of
-// the head's S score workgroups to finish (attention_split_fused): Mantle's
-// softmax (ops.go:83-106: max, exponentials, ordered sum, x *= 1/sum) with the
-// probabilities in LDS (PG false) or in place in the scores buffer (PG true,
-// contexts too long for LDS), then out_d = sum_t p_t * v_t,d in key order, no
-// FMA, one column per lane of waves 0 .. HD/64-1.  The step's own V row
-// (fused) is read from the v input: the workgroup that appends it to the
-// cache may belong to another head and still be running.
-template <int HD, bool PG>
-__device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, int h, int pos) {
-    constexpr int VG = 32, NG = 5;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int kvh = h * a.kv_heads / a.n_head;
-    float* sg = a.scores + (size_t)h * a.max_ctx;
-    float* p = PG ? sg : lds;
-    float* red = PG ? lds : lds + (a.max_ctx + 31) / 32 * 32;
-    const bool pv_wave = wave < HD / 64;
-    const int d = wave * 64 + lane;
-    const float* vcol = a.cache_v + (size_t)kvh * a.head_stride + (pv_wave ? d : 0);
-    const float* vown = a.fused ? a.v + kvh * HD + (pv_wave ? d : 0) : vcol;
-    const int skip = a.fused ? pos : -1;
-    const size_t vs = (size_t)a.kv_stride;
-    float vr[NG][VG];
-    auto vissue = [&](float (&r)[VG], int t0) {
-#pragma unroll
-        for (int k = 0; k < VG; k++) {
-            const int t = t0 + k <= pos ? t0 + k : pos;
-            r[k] = *(t == skip ? vown : vcol + (size_t)t * vs);
+// V column d of one head for the V sum out_d = sum_t p_t * v_t,d (key order,
+// no FMA), streamed into a register ring of NG groups of VG keys that is
+// filled ahead of its use.  VT (transposed cache): the column's keys are
+// contiguous and one 16-byte load brings four of them; otherwise one 4-byte
+// load per key (rows kv_stride apart).  `own` (the fused step's V row, a
+// workgroup of this launch may still be appending it) replaces key `skip`.
+template <bool VT>
+struct VColumn {
+    static constexpr int VG = 32, NG = 5;
+    f32x4 r[NG][VG / 4];
+    const float* col;
+    size_t step;
+    float own;
+    int skip, pos;
+
+    __device__ __forceinline__ void init(const AttnArgs& a, int kvh, int hd, int d, int pos_) {
+        pos = pos_;
+        skip = a.fused ? pos : -1;
+        if (VT) {
+            col = a.cache_v + (size_t)(kvh * hd + d) * a.vt_stride;
+            step = 1;
+        } else {
+            col = a.cache_v + (size_t)kvh * a.head_stride + d;
+            step = (size_t)a.kv_stride;
         }
-    };
-    if (pv_wave) {  // the V ring fills while the softmax runs
+        own = a.fused ? a.v[kvh * hd + d] : 0.0f;
+    }
+    __device__ __forceinline__ void issue(int g, int t0) {
+        if (VT) {
+#pragma unroll
+            for (int k4 = 0; k4 < VG / 4; k4++) {
+                const int t = t0 + 4 * k4 <= pos ? t0 + 4 * k4 : (pos & ~3);
+                f32x4 v = *reinterpret_cast<const f32x4*>(col + t);  // keys past pos are read, never added
+                if (skip >= 0) {
+                    v.x = t == skip ? own : v.x;
+                    v.y = t + 1 == skip ? own : v.y;
+                    v.z = t + 2 == skip ? own : v.z;
+                    v.w = t + 3 == skip ? own : v.w;
+                }
+                r[g][k4] = v;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < VG; k++) {
+                const int t = t0 + k <= pos ? t0 + k : pos;
+                const float v = col[(size_t)t * step];
+                r[g][k >> 2][k & 3] = t == skip ? own : v;
+            }
+        }
+    }
+    // Fill the ring (before the probabilities are ready).
+    __device__ __forceinline__ void prime() {
 #pragma unroll
         for (int g = 0; g < NG; g++)
-            if (g * VG <= pos) vissue(vr[g], g * VG);
+            if (g * VG <= pos) issue(g, g * VG);
     }
+    // The ordered sum over keys 0 .. pos with probabilities p[0 .. pos].
+    __device__ __forceinline__ float sum(const float* p) {
+        float acc = 0.0f;
+        for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const int t0 = (g0 + gi) * VG;
+                if (t0 <= pos) {
+                    float pg[VG];
+#pragma unroll
+                    for (int i4 = 0; i4 < VG / 4; i4++) {
+                        const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
+                        pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                    }
+                    if (t0 + VG <= pos + 1) {
+#pragma unroll
+                        for (int k = 0; k < VG; k++) acc = acc + pg[k] * r[gi][k >> 2][k & 3];
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < VG; k++) {
+                            const float nacc = acc + pg[k] * r[gi][k >> 2][k & 3];
+                            acc = t0 + k <= pos ? nacc : acc;
+                        }
+                    }
+                    if (t0 + NG * VG <= pos) issue(gi, t0 + NG * VG);
+                }
+            }
+        }
+        return acc;
+    }
+};
+
+// Softmax of head h's scores (ops.go:83-106: max, exponentials, the ordered
+// sum, x *= 1/sum) into p (LDS or, PG, in place in the scores buffer); red:
+// 5 floats of LDS.  Whole workgroup.
+template <bool PG>
+__device__ __forceinline__ void head_softmax(const float* sg, float* p, float* red, int pos) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     float m = -INFINITY;
     for (int t = tid; t <= pos; t += kThreads) {
         const float v = sg[t];
@@ -792,42 +857,41 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
     }
     if (PG) __threadfence_block();
     __syncthreads();
-    PHASE(5);
-    if (!pv_wave) return;
-    float acc = 0.0f;
-    for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) {
-            const int t0 = (g0 + gi) * VG;
-            if (t0 <= pos) {
-                float pg[VG];
-#pragma unroll
-                for (int i4 = 0; i4 < VG / 4; i4++) {
-                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
-                    pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
-                }
-                if (t0 + VG <= pos + 1) {
-#pragma unroll
-                    for (int k = 0; k < VG; k++) acc = acc + pg[k] * vr[gi][k];
-                } else {
-#pragma unroll
-                    for (int k = 0; k < VG; k++) {
-                        const float nacc = acc + pg[k] * vr[gi][k];
-                        acc = t0 + k <= pos ? nacc : acc;
-                    }
-                }
-                if (t0 + NG * VG <= pos) vissue(vr[gi], t0 + NG * VG);
-            }
-        }
-    }
-    const int gi = h * HD + d;
-    a.out[gi] = acc;
-    if (a.q_out) {  // lanes 0-31 and 32-63: two whole int8 blocks of the Wo activation
+}
+
+// The output value of column gi (= h*HD + d) and, with q_out, its int8 block
+// of the Wo activation (32 consecutive lanes hold one whole block).
+__device__ __forceinline__ void store_attn_out(const AttnArgs& a, int gi, float acc, bool live) {
+    if (live) a.out[gi] = acc;
+    if (a.q_out) {
         float sc;
         const int32_t qv = quant_lane32(acc, &sc);
-        a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
-        if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+        if (live) {
+            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
+            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
+        }
     }
+}
+
+// Softmax and the V sum of all of head h's columns, by the last of the head's
+// S score workgroups to finish (attention_split_fused), one column per lane of
+// waves 0 .. HD/64-1.
+template <int HD, bool PG, bool VT>
+__device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, int h, int pos) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = h * a.kv_heads / a.n_head;
+    float* sg = a.scores + (size_t)h * a.max_ctx;
+    float* p = PG ? sg : lds;
+    float* red = PG ? lds : lds + (a.max_ctx + 31) / 32 * 32;
+    const bool pv_wave = wave < HD / 64;
+    const int d = wave * 64 + lane;
+    VColumn<VT> vc;
+    vc.init(a, kvh, HD, pv_wave ? d : 0, pos);
+    if (pv_wave) vc.prime();  // the ring fills while the softmax runs
+    head_softmax<PG>(sg, p, red, pos);
+    PHASE(5);
+    if (!pv_wave) return;
+    store_attn_out(a, h * HD + d, vc.sum(p), true);
 }
 
 // One launch for the split-key attention: workgroup (h, s) scores its chunks
@@ -836,7 +900,7 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
 // with a device-scope fence before counting) resets the counter and runs
 // softmax_pv_head.  Every workgroup counts, with or without a chunk, so the
 // last one always arrives and every wave exits.
-template <int HD, bool PG>
+template <int HD, bool PG, bool VT>
 __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
@@ -858,103 +922,33 @@ __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     if (!is_last) return;
     __threadfence();  // the other workgroups' scores, seen after their arrivals
     PHASE(4);
-    softmax_pv_head<HD, PG>(a, lds, h, pos);
+    softmax_pv_head<HD, PG, VT>(a, lds, h, pos);
 }
 
-template <int HD>
+template <int HD, bool VT>
 __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     constexpr int DB = 32;  // output columns per workgroup: one int8 block of the Wo activation
-    constexpr int VG = 32, NG = 5;
     const int nd = HD / DB;
     const int h = blockIdx.x / nd, db = blockIdx.x % nd;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvh = h * a.kv_heads / a.n_head;
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     const int pcap = (a.max_ctx + 31) / 32 * 32;
-    float* p = lds;
-    float* red = lds + pcap;
     const float* sg = a.scores + (size_t)h * a.max_ctx;
     PHASE_SLOT();
     PHASE(0);
     // wave 0 (lanes 0-31 the columns; 32-63 shadow them) streams its V
     // columns into a register ring from the start
     const int d = db * DB + (lane & 31);
-    const float* vcol = a.cache_v + (size_t)kvh * a.head_stride + d;
-    const size_t vs = (size_t)a.kv_stride;
-    float vr[NG][VG];
-    auto vissue = [&](float (&r)[VG], int t0) {
-#pragma unroll
-        for (int k = 0; k < VG; k++) {
-            const int t = t0 + k <= pos ? t0 + k : pos;
-            r[k] = vcol[(size_t)t * vs];
-        }
-    };
-    if (wave == 0) {
-#pragma unroll
-        for (int g = 0; g < NG; g++)
-            if (g * VG <= pos) vissue(vr[g], g * VG);
-    }
-    // softmax (ops.go:83-106): max, exponentials, ordered sum, x *= 1/sum
-    float m = -INFINITY;
-    for (int t = tid; t <= pos; t += kThreads) {
-        const float v = sg[t];
-        p[t] = v;
-        m = fmaxf(m, v);
-    }
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_down(m, off, 64));
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int t = tid; t <= pos; t += kThreads) p[t] = fast_exp_scalar(p[t] - mx);
-    __syncthreads();
-    if (tid == 0) red[4] = ordered_sum(p, 1, pos + 1);
-    __syncthreads();
-    const float sum = red[4];
-    if (sum != 0.0f) {
-        const float inv = 1.0f / sum;
-        for (int t = tid; t <= pos; t += kThreads) p[t] = p[t] * inv;
-    }
-    __syncthreads();
+    VColumn<VT> vc;
+    vc.init(a, kvh, HD, d, pos);
+    vc.skip = -1;  // the previous launch appended the step's row
+    if (wave == 0) vc.prime();
+    head_softmax<false>(sg, lds, lds + pcap, pos);
     PHASE(1);
     if (wave != 0) return;
-    // out_d = sum_t p_t * v_t,d in t order (no FMA)
-    float acc = 0.0f;
-    for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) {
-            const int t0 = (g0 + gi) * VG;
-            if (t0 <= pos) {
-                float pg[VG];
-#pragma unroll
-                for (int i4 = 0; i4 < VG / 4; i4++) {
-                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
-                    pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
-                }
-                if (t0 + VG <= pos + 1) {
-#pragma unroll
-                    for (int k = 0; k < VG; k++) acc = acc + pg[k] * vr[gi][k];
-                } else {
-#pragma unroll
-                    for (int k = 0; k < VG; k++) {
-                        const float nacc = acc + pg[k] * vr[gi][k];
-                        acc = t0 + k <= pos ? nacc : acc;
-                    }
-                }
-                if (t0 + NG * VG <= pos) vissue(vr[gi], t0 + NG * VG);
-            }
-        }
-    }
-    if (lane < 32) a.out[h * HD + d] = acc;
-    if (a.q_out) {  // lanes 0-31: exactly one int8 block of the Wo activation
-        float sc;
-        const int32_t qv = quant_lane32(acc, &sc);
-        const int gi = h * HD + d;
-        if (lane < 32) {
-            a.q_out[(gi >> 5) * 32 + qx_perm(gi & 31)] = (int8_t)qv;
-            if ((gi & 31) == 0) a.q_scale[gi >> 5] = sc;
-        }
-    }
+    store_attn_out(a, h * HD + d, vc.sum(lds), lane < 32);
     PHASE(2);
 }
 
@@ -997,7 +991,11 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!lds_scores && !a.scores) return hipErrorInvalidValue;
     const int mode = attention_path();
     const bool fast_hd = a.head_dim == 128 || a.head_dim == 64;
-    if (fast_hd && (mode == kAttnPathFused || (mode == kAttnPathSplit && a.max_ctx > kSplitMaxCtx)) && a.scores) {
+    const bool vt = a.vt_stride > 0;
+    const bool split_ok = fast_hd && a.scores && (mode == kAttnPathSplit || mode == kAttnPathFused);
+    if (vt && (!split_ok || (a.vt_stride & 3) || a.vt_stride < (a.max_ctx + 3) / 4 * 4))
+        return hipErrorInvalidValue;  // the transposed V cache is read by the split kernels only
+    if (split_ok && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
         AttnArgs f = a;
         if (!f.counters) f.counters = library_counters(a.n_head);
         if (!f.counters) return hipErrorInvalidValue;
@@ -1007,29 +1005,30 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         const bool pg = smem_p > 64 * 1024;  // probabilities in place in the scores buffer
         const size_t smem = pg || smem_p < smem_a ? smem_a : smem_p;
         const dim3 grid(a.n_head * S);
-        if (a.head_dim == 128) {
-            if (pg) hipLaunchKernelGGL((attention_split_fused<128, true>), grid, dim3(kThreads), smem, stream, f);
-            else hipLaunchKernelGGL((attention_split_fused<128, false>), grid, dim3(kThreads), smem, stream, f);
-        } else {
-            if (pg) hipLaunchKernelGGL((attention_split_fused<64, true>), grid, dim3(kThreads), smem, stream, f);
-            else hipLaunchKernelGGL((attention_split_fused<64, false>), grid, dim3(kThreads), smem, stream, f);
-        }
+        // kernel[hd 128][pg][vt]
+        void (*const kerns[2][2][2])(AttnArgs) = {
+            {{attention_split_fused<64, false, false>, attention_split_fused<64, false, true>},
+             {attention_split_fused<64, true, false>, attention_split_fused<64, true, true>}},
+            {{attention_split_fused<128, false, false>, attention_split_fused<128, false, true>},
+             {attention_split_fused<128, true, false>, attention_split_fused<128, true, true>}}};
+        hipLaunchKernelGGL(kerns[a.head_dim == 128][pg][vt], grid, dim3(kThreads), smem, stream, f);
         return hipGetLastError();
     }
-    if (fast_hd && mode == kAttnPathSplit && a.scores && a.max_ctx <= kSplitMaxCtx) {
+    if (split_ok) {
         const int S = min(kSplitWgs, (a.max_ctx + kAttnKeys - 1) / kAttnKeys);
         const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
         const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
         const int nd = a.head_dim / 32;
-        const hipError_t e = allow_lds(a.head_dim == 128 ? attention_pv_split<128> : attention_pv_split<64>, smem_b);
+        void (*const pv[2][2])(AttnArgs) = {{attention_pv_split<64, false>, attention_pv_split<64, true>},
+                                            {attention_pv_split<128, false>, attention_pv_split<128, true>}};
+        auto pvk = pv[a.head_dim == 128][vt];
+        const hipError_t e = allow_lds(pvk, smem_b);
         if (e != hipSuccess) return e;
-        if (a.head_dim == 128) {
+        if (a.head_dim == 128)
             hipLaunchKernelGGL(attention_scores_split<128>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
-            hipLaunchKernelGGL(attention_pv_split<128>, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
-        } else {
+        else
             hipLaunchKernelGGL(attention_scores_split<64>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
-            hipLaunchKernelGGL(attention_pv_split<64>, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
-        }
+        hipLaunchKernelGGL(pvk, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
         return hipGetLastError();
     }
     if (fast_hd && mode != kAttnPathGeneral) {

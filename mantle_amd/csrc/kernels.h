@@ -101,6 +101,8 @@ struct AttnArgs {
     int isa;
     int8_t* q_out;         // optional: out also as Mantle's int8 blocks (permuted layout) ...
     float* q_scale;        // ... and their scales, for the next W4A8 GEMV (head_dim % 32 == 0)
+    int vt_stride;         // > 0: V is stored transposed, element (t, d) of kv head g at
+                           // cache_v + (g*head_dim + d)*vt_stride + t (split paths only)
     unsigned* counters;    // [n_head] zeroed arrival counters of the one-launch split path (null: the
                            // library's own, for callers that serialise their launches on one stream)
 };

@@ -11,8 +11,9 @@
 //     device memory, so one decode step is a fixed sequence of kernel
 //     launches that never reads the host: it is captured once as a HIP
 //     graph and replayed per position;
-//   * the f32 KV cache is head-major, [layer][kv_head][max_ctx][head_dim]: the
-//     keys a decode step reads for one kv head are one contiguous run.
+//   * the f32 K cache is head-major, [layer][kv_head][max_ctx][head_dim]: the
+//     keys a decode step reads for one kv head are one contiguous run; the V
+//     cache is transposed for the split attention kernels (see vt_stride).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -50,6 +51,11 @@ struct mantleHipModel {
     int8_t* qx = nullptr;
     float* xs = nullptr;
     float *cache_k = nullptr, *cache_v = nullptr;
+    // V cache: head-major like K, or (vt_stride > 0, the split attention
+    // kernels) transposed, [layer][kv_head][head_dim][vt_stride]: a column's
+    // keys contiguous, so the V sum loads four keys per 16 bytes.
+    int vt_stride = 0;
+    int v_rows = 0;  // per layer and kv column: max_ctx or vt_stride
     float *rope_cos = nullptr, *rope_sin = nullptr;
     DecodeState* state = nullptr;
     int* prompt = nullptr;
@@ -90,7 +96,8 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.rope_sin = m->rope_sin;
         a.pos_dev = &m->state->pos;
         a.cache_k = m->cache_k + (size_t)l * m->max_ctx * m->kv_dim;
-        a.cache_v = m->cache_v + (size_t)l * m->max_ctx * m->kv_dim;
+        a.cache_v = m->cache_v + (size_t)l * m->v_rows * m->kv_dim;
+        a.vt_stride = m->vt_stride;
         a.scores = m->scores;
         a.out = m->attn;
         a.n_head = c.n_heads;
@@ -366,8 +373,13 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     CHECK(hipMalloc((void**)&m->qx, (size_t)big_blocks * 32));
     CHECK(hipMalloc((void**)&m->xs, sizeof(float) * big_blocks));
     const size_t kv_elems = (size_t)c.n_layers * max_ctx * m->kv_dim;
+    const int apath = attention_path();
+    const bool split = (c.head_dim == 64 || c.head_dim == 128) && (apath == kAttnPathSplit || apath == kAttnPathFused);
+    m->vt_stride = split ? (max_ctx + 3) / 4 * 4 : 0;
+    m->v_rows = split ? m->vt_stride : max_ctx;
+    const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
     CHECK(hipMalloc((void**)&m->cache_k, sizeof(float) * kv_elems));
-    CHECK(hipMalloc((void**)&m->cache_v, sizeof(float) * kv_elems));
+    CHECK(hipMalloc((void**)&m->cache_v, sizeof(float) * v_elems));
     CHECK(hipMalloc((void**)&m->state, sizeof(DecodeState)));
     CHECK(hipMalloc((void**)&m->prompt, sizeof(int) * max_ctx));
     CHECK(hipMalloc((void**)&m->out_tokens, sizeof(int) * max_ctx));
@@ -390,7 +402,7 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     CHECK(hipMemset(m->prompt, 0, sizeof(int) * max_ctx));
     CHECK(hipMemset(m->out_tokens, 0, sizeof(int) * max_ctx));
     CHECK(hipMemset(m->cache_k, 0, sizeof(float) * kv_elems));
-    CHECK(hipMemset(m->cache_v, 0, sizeof(float) * kv_elems));
+    CHECK(hipMemset(m->cache_v, 0, sizeof(float) * v_elems));
     CHECK(hipDeviceSynchronize());
 #undef CHECK
     *out = m;
