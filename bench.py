@@ -221,11 +221,14 @@ def cpu_baseline(path, cfg, prompt, budget_s=15.0, max_tokens=24):
 
 
 def weight_bytes_per_token(cfg):
-    """k4 weight bytes one decode token streams: every block matrix plus the lm_head
-    (the tied embedding when tie_embeddings), norms as fp32."""
+    """Weight bytes one decode token streams: every block matrix plus the lm_head
+    (the tied embedding when tie_embeddings), norms as fp32; k4 payloads, or 2
+    bytes per weight with cfg["weights"] == "bf16"."""
     from mantle_amd.mcf import payload_size
     d, f, hd = cfg["d_model"], cfg["ffn"], cfg["head_dim"]
     qd, kvd = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    if cfg.get("weights") == "bf16":
+        payload_size = lambda r, c: 2 * r * c  # noqa: E731
     layer = (payload_size(qd, d) + 2 * payload_size(kvd, d) + payload_size(d, qd) + 2 * payload_size(f, d)
              + payload_size(d, f) + 4 * (2 * d + 2 * hd))
     return cfg["n_layers"] * layer + payload_size(cfg["vocab"], d) + 4 * d
@@ -264,10 +267,10 @@ def large_model_run(args):
     import mantle_amd
     from mantle_amd import mcf
     name, seed, plen = LARGE_MODELS[args.model]
-    cfg = getattr(mcf, name)
+    cfg = dict(getattr(mcf, name), weights=args.weights)
     plen = args.prompt or plen
     os.makedirs(args.model_dir, exist_ok=True)
-    path = os.path.join(args.model_dir, f"{args.model}_k4_seed{seed}.mcf")
+    path = os.path.join(args.model_dir, f"{args.model}_{args.weights}_seed{seed}.mcf")
     t0 = time.perf_counter()
     mcf.pack_cached(path, seed, cfg)
     log(f"model ready in {time.perf_counter() - t0:.1f} s: {path}")
@@ -280,14 +283,17 @@ def large_model_run(args):
     tps = args.steps / dt
     wb = weight_bytes_per_token(cfg)
     kv_mid = 2 * cfg["n_layers"] * cfg["n_kv_heads"] * cfg["head_dim"] * 4 * (plen + args.warmup + args.steps // 2)
-    log(f"{args.model}: decode {tps:.1f} tok/s, prefill {prefill_tps:.1f} tok/s")
+    log(f"{args.model} {args.weights}: decode {tps:.1f} tok/s, prefill {prefill_tps:.1f} tok/s")
     print(json.dumps({
-        "metric": f"decode tok/s @batch1, {args.model} k4 after a {plen}-token prompt",
+        "metric": f"decode tok/s @batch1, {args.model} {args.weights} after a {plen}-token prompt",
         "value": round(tps, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "k4 weights x int8 activations, int32 block dots, fp32 accumulation",
-        "data": f"synthetic: random-init N(0,0.02) weights seed {seed} packed to MCF k4, {plen} uniform token ids seed 1",
-        "config": {"workload": f"{args.model}-shape k4 greedy decode, batch 1 (BASELINE config {seed})",
+        "vs_baseline": None,
+        "dtype": ("bf16 weights x fp32 activations, fp32 accumulation" if args.weights == "bf16"
+                  else "k4 weights x int8 activations, int32 block dots, fp32 accumulation"),
+        "data": f"synthetic: random-init N(0,0.02) weights seed {seed} packed to MCF {args.weights}, {plen} uniform "
+                f"token ids seed 1",
+        "config": {"workload": f"{args.model}-shape {args.weights} greedy decode, batch 1 (BASELINE config {seed})",
                    "prompt_tokens": plen, "parallelism": "none (1 GPU)"},
         "prefill_tok_s": round(prefill_tps, 2),
         "weight_bytes_per_token": wb,
@@ -310,6 +316,8 @@ def main():
     ap.add_argument("--model", default="qwen3-0.6b", choices=["qwen3-0.6b", *LARGE_MODELS],
                     help="qwen3-4b / qwen3-8b: configs 4 / 5, a decode line of their own (not the headline)")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length for --model qwen3-4b / qwen3-8b")
+    ap.add_argument("--weights", default="k4", choices=["k4", "bf16"],
+                    help="weight format for --model qwen3-4b / qwen3-8b (config 5 runs both)")
     ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
     args = ap.parse_args()
     if args.gpus != 1:

@@ -52,6 +52,15 @@ int mantleHipGetParityISA(void);
 int mantleHipSetAttentionPath(int path);
 int mantleHipGetAttentionPath(void);
 
+/* ---------------- bf16 dense GEMV ---------------- */
+/* y[rows] = W x with raw bf16 W [rows][cols] (16-byte aligned, cols a multiple
+ * of 8, at most 32768) and fp32 x (16-byte aligned), bit-exact to Mantle's CPU
+ * matVecRangeBF16 in the parity ISA's order (internal/backend/simd/matvec.go:406-979).
+ * Replaces the BF16 weight branch of the CUDA backend's DeviceMatVec
+ * (internal/backend/cuda/ops.go:1814-1824, cuBLAS on bf16-converted x), whose
+ * arithmetic is not the CPU path's. */
+int mantleHipMatVecBF16F32(const uint16_t* w, const float* x, float* y, int rows, int cols, mantleHipStream_t stream);
+
 /* ---------------- k4 kernels ---------------- */
 /* W4A32 k4 GEMV; replaces mantleCudaQuantMatVecK4F32
  * (internal/backend/cuda/native/softmax.h:32-41).  y[rows] = W x, fp32 x. */
@@ -137,11 +146,16 @@ typedef struct {
     double rope_base;
     float eps;
     int tie_embeddings;
+    int weight_dtype; /* rank-2 tensors: 0 or MANTLE_HIP_DTYPE_K4 (k4), MANTLE_HIP_DTYPE_BF16 (raw bf16) */
 } mantleHipQwen3Config;
+#define MANTLE_HIP_DTYPE_BF16 3
+#define MANTLE_HIP_DTYPE_K4 0x31
 
 /* Write a random-init (N(0,0.02), unit norm gains) Qwen3-shaped model as an MCF
  * file with k4 weights: the equivalent of `mantle pack` + `mantle quantize
- * --method k4` (pkg/mcf/pack.go:68, cmd/mantle/quantize.go:174-350). */
+ * --method k4` (pkg/mcf/pack.go:68, cmd/mantle/quantize.go:174-350); with
+ * cfg->weight_dtype == MANTLE_HIP_DTYPE_BF16, `mantle pack --cast bf16`
+ * (pkg/mcf/pack.go:291-294, round to nearest even, :789-793) instead. */
 int mantleHipPackSyntheticQwen3(const char* path, const mantleHipQwen3Config* cfg, uint64_t seed, int threads);
 /* Deterministic N(0, std) generator used by the packer (splitmix64 + Box-Muller). */
 int mantleHipFillNormal(float* dst, int64_t n, uint64_t seed, float std);

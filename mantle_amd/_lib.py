@@ -22,7 +22,7 @@ D = C.c_double
 class Qwen3Config(C.Structure):
     _fields_ = [
         ("n_layers", I), ("d_model", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I),
-        ("ffn", I), ("vocab", I), ("rope_base", D), ("eps", F), ("tie_embeddings", I),
+        ("ffn", I), ("vocab", I), ("rope_base", D), ("eps", F), ("tie_embeddings", I), ("weight_dtype", I),
     ]
 
     def as_dict(self) -> dict:
@@ -37,6 +37,7 @@ _SIGS = {
     "mantleHipSetAttentionPath": (I, [I]),
     "mantleHipGetAttentionPath": (I, []),
     "mantleHipGetParityISA": (I, []),
+    "mantleHipMatVecBF16F32": (I, [P, P, P, I, I, P]),
     "mantleHipQuantMatVecK4F32": (I, [P, P, P, P, P, I, I, I, P]),
     "mantleHipQuantMatVecK4W4A8F32": (I, [P, P, P, P, P, I, I, I, I, P, P, P]),
     "mantleHipQuantMatVecK4W4A8QF32": (I, [P, P, P, P, P, P, I, I, I, I, P]),

@@ -54,6 +54,13 @@ int mantleHipSetAttentionPath(int path) { return set_attention_path(path) ? hipS
 
 int mantleHipGetAttentionPath(void) { return attention_path(); }
 
+int mantleHipMatVecBF16F32(const uint16_t* w, const float* x, float* y, int rows, int cols, mantleHipStream_t stream) {
+    if (!w || !x || !y || rows <= 0 || cols <= 0) return hipErrorInvalidValue;
+    const int r[1] = {rows};
+    float* o[1] = {y};
+    return launch_bf16_gemv(&w, o, r, 1, cols, x, kEpiStore, nullptr, g_isa.load(), S(stream));
+}
+
 int mantleHipQuantMatVecK4F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                               const float* x, float* y, int rows, int blocksPerRow, int cols,
                               mantleHipStream_t stream) {
@@ -200,6 +207,7 @@ int mantleHipPackSyntheticQwen3(const char* path, const mantleHipQwen3Config* c,
         c->head_dim <= 0 || c->ffn <= 0 || c->vocab <= 0)
         return hipErrorInvalidValue;
     if (threads < 1) threads = 1;
+    if (c->weight_dtype != 0 && c->weight_dtype != kDTypeK4 && c->weight_dtype != kDTypeBF16) return hipErrorInvalidValue;
     McfWriter w;
     std::string err;
     if (!w.open(path, &err)) return hipErrorInvalidValue;
@@ -249,6 +257,18 @@ int mantleHipPackSyntheticQwen3(const char* path, const mantleHipQwen3Config* c,
         }
         buf.resize((size_t)(t.rows * t.cols));
         fill_normal(buf.data(), t.rows * t.cols, splitmix64(seed ^ fnv1a64(t.name)), 0.02f, threads);
+        if (c->weight_dtype == kDTypeBF16) {  // pkg/mcf/pack.go:789-793 bf16FromF32Bits
+            std::vector<uint16_t> b16(buf.size());
+            for (size_t i = 0; i < buf.size(); i++) {
+                uint32_t u;
+                memcpy(&u, &buf[i], 4);
+                b16[i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+            }
+            if (!w.add_tensor(t.name, kDTypeBF16, {(uint64_t)t.rows, (uint64_t)t.cols}, b16.data(), 2 * b16.size(),
+                              false, 0, 0))
+                return hipErrorInvalidValue;
+            continue;
+        }
         payload.resize((size_t)k4_payload_bytes(t.rows, t.cols));
         float mn = 0, mx = 0;
         if (quantize_k4(buf.data(), t.rows, t.cols, payload.data(), &mn, &mx, threads) != 0) return hipErrorInvalidValue;

@@ -68,6 +68,16 @@ hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int 
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch,
                                 hipStream_t stream);
 
+// Dense bf16 GEMV with fp32 x (raw-bf16 MCF weights, matvec.go:406-979), bit-exact
+// to Mantle's `isa` order: y_i = W_i x for up to three matrices W_i [rows_i][cols]
+// (bf16, 16-byte aligned) sharing x.  kEpiResAdd adds into y; kEpiArgmax
+// (one matrix) also folds each row into argmax_key's kArgmaxSlots keys.
+// cols: a multiple of 8, at most kBf16MaxCols (x is staged in LDS).
+constexpr int kBf16MaxCols = 32768;
+hipError_t launch_bf16_gemv(const uint16_t* const* w, float* const* y, const int* rows, int nmat, int cols,
+                            const float* x, GemvEpi epi, unsigned long long* argmax_key, int isa,
+                            hipStream_t stream);
+
 // Activation quantiser (internal/backend/simd/matvec_quant.go:746-797), optionally
 // preceded by Mantle's RMSNorm (weight != nullptr).  norm_out (nullable) receives
 // the normalised fp32 vector.  batch rows of length n, one workgroup per row.
@@ -128,6 +138,8 @@ size_t attention_prefill_workspace(int seq, int kv_heads);
 
 hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
                         hipStream_t stream);
+hipError_t launch_embed_bf16(const uint16_t* emb, int vocab, int cols, const int* prompt, DecodeState* st, float* x,
+                             hipStream_t stream);
 hipError_t launch_finish_step(DecodeState* st, int* out_tokens, hipStream_t stream);
 
 // Small standalone ops behind the mantleHip* C ABI.

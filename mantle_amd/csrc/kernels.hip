@@ -551,6 +551,25 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(K4Mat emb, int cols, co
     for (int i = threadIdx.x; i < kArgmaxSlots; i += kThreads) st->argmax_keys[i * kArgmaxStride] = 0ull;
 }
 
+// Embedding row of a raw-bf16 table (bf16 -> f32 is exact: bits << 16).
+__global__ __launch_bounds__(kThreads) void embed_bf16_kernel(const uint16_t* __restrict__ emb, int vocab, int cols,
+                                                              const int* __restrict__ prompt, DecodeState* st,
+                                                              float* __restrict__ x) {
+    const int pos = st->pos;
+    int tok = pos < st->n_prompt ? prompt[pos] : st->next_tok;
+    if (tok < 0 || tok >= vocab) tok = 0;
+    const uint16_t* row = emb + (size_t)tok * cols;
+    for (int c = threadIdx.x; c < cols; c += kThreads) x[c] = __uint_as_float((uint32_t)row[c] << 16);
+    for (int i = threadIdx.x; i < kArgmaxSlots; i += kThreads) st->argmax_keys[i * kArgmaxStride] = 0ull;
+}
+
+hipError_t launch_embed_bf16(const uint16_t* emb, int vocab, int cols, const int* prompt, DecodeState* st, float* x,
+                             hipStream_t stream) {
+    if (!emb || !prompt || !st || !x || cols <= 0 || vocab <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_bf16_kernel, dim3(1), dim3(kThreads), 0, stream, emb, vocab, cols, prompt, st, x);
+    return hipGetLastError();
+}
+
 hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
                         hipStream_t stream) {
     if (!emb.nib || !prompt || !st || !x || cols <= 0) return hipErrorInvalidValue;

@@ -40,13 +40,19 @@ struct mantleHipModel {
     size_t arena_bytes = 0;
     K4Mat embed{}, lm_head{};
     const float* final_norm = nullptr;
+    // raw-bf16 weights (cfg.weight_dtype == kDTypeBF16): the b* pointers below
+    // instead of the K4Mat ones
+    bool bf16 = false;
+    const uint16_t *bembed = nullptr, *blm_head = nullptr;
     struct Layer {
         const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
         K4Mat wq, wk, wv, wo, gate, up, down;
+        const uint16_t *bq, *bk, *bv, *bo, *bgate, *bup, *bdown;
     };
     std::vector<Layer> layers;
     // activations / scratch
     float *x = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr, *scores = nullptr;
+    float *xn = nullptr, *up = nullptr;  // bf16 path: normalised x, the up projection
     unsigned* attn_counters = nullptr;  // [n_heads] arrival counters of the one-launch split attention
     int8_t* qx = nullptr;
     float* xs = nullptr;
@@ -65,7 +71,78 @@ struct mantleHipModel {
     hipGraphExec_t graph = nullptr;
 };
 
+// One decode step with raw-bf16 weights: Mantle's same layer loop
+// (runtime_decode.go:81-203) with every GEMV the plain bf16 one on fp32 x
+// (matvec.go:154-172 quantises activations only for quantised weights).
+static hipError_t enqueue_step_bf16(mantleHipModel* m, hipStream_t s) {
+    const mantleHipQwen3Config& c = m->cfg;
+    hipError_t e;
+#define TRY(x)                         \
+    do {                               \
+        if ((e = (x)) != hipSuccess) { \
+            return e;                  \
+        }                              \
+    } while (0)
+    const int d = c.d_model;
+    TRY(launch_embed_bf16(m->bembed, c.vocab, d, m->prompt, m->state, m->x, s));
+    float* q = m->qkv;
+    float* k = q + m->q_dim;
+    float* v = k + m->kv_dim;
+    for (int l = 0; l < c.n_layers; l++) {
+        const auto& L = m->layers[l];
+        TRY(launch_rmsnorm(m->xn, m->x, L.attn_norm, c.eps, d, 1, m->isa, s));
+        const uint16_t* wqkv[3] = {L.bq, L.bk, L.bv};
+        float* oqkv[3] = {q, k, v};
+        const int rqkv[3] = {m->q_dim, m->kv_dim, m->kv_dim};
+        TRY(launch_bf16_gemv(wqkv, oqkv, rqkv, 3, d, m->xn, kEpiStore, nullptr, m->isa, s));
+        AttnArgs a{};
+        a.q = q;
+        a.k = k;
+        a.v = v;
+        a.q_norm = L.q_norm;
+        a.k_norm = L.k_norm;
+        a.eps = c.eps;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.pos_dev = &m->state->pos;
+        a.cache_k = m->cache_k + (size_t)l * m->max_ctx * m->kv_dim;
+        a.cache_v = m->cache_v + (size_t)l * m->v_rows * m->kv_dim;
+        a.vt_stride = m->vt_stride;
+        a.scores = m->scores;
+        a.out = m->attn;
+        a.n_head = c.n_heads;
+        a.kv_heads = c.n_kv_heads;
+        a.head_dim = c.head_dim;
+        a.kv_stride = c.head_dim;
+        a.head_stride = m->max_ctx * c.head_dim;
+        a.max_ctx = m->max_ctx;
+        a.scale = (float)(1.0 / sqrt((double)c.head_dim));
+        a.fused = 1;
+        a.isa = m->isa;
+        a.counters = m->attn_counters;
+        TRY(launch_attention_decode(a, s));
+        const int rd[1] = {d};
+        float* xo[1] = {m->x};
+        TRY(launch_bf16_gemv(&L.bo, xo, rd, 1, m->q_dim, m->attn, kEpiResAdd, nullptr, m->isa, s));
+        TRY(launch_rmsnorm(m->xn, m->x, L.ffn_norm, c.eps, d, 1, m->isa, s));
+        const uint16_t* wgu[2] = {L.bgate, L.bup};
+        float* ogu[2] = {m->act, m->up};
+        const int rgu[2] = {c.ffn, c.ffn};
+        TRY(launch_bf16_gemv(wgu, ogu, rgu, 2, d, m->xn, kEpiStore, nullptr, m->isa, s));
+        TRY(launch_silu_mul(m->act, m->up, m->act, c.ffn, s));  // ffn.go:66-86 act = silu(gate) * up
+        TRY(launch_bf16_gemv(&L.bdown, xo, rd, 1, c.ffn, m->act, kEpiResAdd, nullptr, m->isa, s));
+    }
+    TRY(launch_rmsnorm(m->xn, m->x, m->final_norm, c.eps, d, 1, m->isa, s));
+    float* lo[1] = {m->logits};
+    const int rv[1] = {c.vocab};
+    TRY(launch_bf16_gemv(&m->blm_head, lo, rv, 1, d, m->xn, kEpiArgmax, m->state->argmax_keys, m->isa, s));
+    TRY(launch_finish_step(m->state, m->out_tokens, s));
+#undef TRY
+    return hipSuccess;
+}
+
 static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
+    if (m->bf16) return enqueue_step_bf16(m, s);
     const mantleHipQwen3Config& c = m->cfg;
     hipError_t e;
 #define TRY(x)                         \
@@ -190,7 +267,7 @@ static bool json_number(const std::string& js, const char* key, double* out) {
 static void free_model(mantleHipModel* m) {
     if (!m) return;
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
-    void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->attn_counters, m->qx, m->xs, m->cache_k,
+    void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->attn_counters, m->xn, m->up, m->qx, m->xs, m->cache_k,
                     m->cache_v, m->rope_cos, m->rope_sin, m->state, m->prompt, m->out_tokens};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -276,6 +353,18 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
         return hipErrorInvalidValue;
     }
 
+    // Rank-2 weights are all k4 or all raw bf16 (the embedding's dtype decides).
+    {
+        const int ei = f.find("model.embed_tokens.weight");
+        m->bf16 = ei >= 0 && f.tensors()[ei].dtype == kDTypeBF16;
+    }
+    c.weight_dtype = m->bf16 ? kDTypeBF16 : kDTypeK4;
+    const uint16_t wdt = m->bf16 ? (uint16_t)kDTypeBF16 : (uint16_t)kDTypeK4;
+    if (m->bf16 && (c.d_model % 8 || m->q_dim % 8 || c.ffn % 8)) {
+        fprintf(stderr, "mantle_hip: bf16 weights need row lengths that are multiples of 8\n");
+        free_model(m);
+        return hipErrorInvalidValue;
+    }
     // Tensor plan: (name, expected dtype, rows, cols); qwen3Spec names (internal/model/modelspec.go:173-240).
     struct Want {
         std::string name;
@@ -285,21 +374,21 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     };
     std::vector<Want> wants;
     auto lname = [](int l, const char* s) { return "model.layers." + std::to_string(l) + "." + s; };
-    wants.push_back({"model.embed_tokens.weight", kDTypeK4, c.vocab, c.d_model, 0});
-    if (!c.tie_embeddings) wants.push_back({"lm_head.weight", kDTypeK4, c.vocab, c.d_model, 0});
+    wants.push_back({"model.embed_tokens.weight", wdt, c.vocab, c.d_model, 0});
+    if (!c.tie_embeddings) wants.push_back({"lm_head.weight", wdt, c.vocab, c.d_model, 0});
     wants.push_back({"model.norm.weight", kDTypeF32, c.d_model, 1, 0});
     for (int l = 0; l < c.n_layers; l++) {
         wants.push_back({lname(l, "input_layernorm.weight"), kDTypeF32, c.d_model, 1, 0});
         wants.push_back({lname(l, "post_attention_layernorm.weight"), kDTypeF32, c.d_model, 1, 0});
         wants.push_back({lname(l, "self_attn.q_norm.weight"), kDTypeF32, c.head_dim, 1, 0});
         wants.push_back({lname(l, "self_attn.k_norm.weight"), kDTypeF32, c.head_dim, 1, 0});
-        wants.push_back({lname(l, "self_attn.q_proj.weight"), kDTypeK4, m->q_dim, c.d_model, 0});
-        wants.push_back({lname(l, "self_attn.k_proj.weight"), kDTypeK4, m->kv_dim, c.d_model, 0});
-        wants.push_back({lname(l, "self_attn.v_proj.weight"), kDTypeK4, m->kv_dim, c.d_model, 0});
-        wants.push_back({lname(l, "self_attn.o_proj.weight"), kDTypeK4, c.d_model, m->q_dim, 0});
-        wants.push_back({lname(l, "mlp.gate_proj.weight"), kDTypeK4, c.ffn, c.d_model, 0});
-        wants.push_back({lname(l, "mlp.up_proj.weight"), kDTypeK4, c.ffn, c.d_model, 0});
-        wants.push_back({lname(l, "mlp.down_proj.weight"), kDTypeK4, c.d_model, c.ffn, 0});
+        wants.push_back({lname(l, "self_attn.q_proj.weight"), wdt, m->q_dim, c.d_model, 0});
+        wants.push_back({lname(l, "self_attn.k_proj.weight"), wdt, m->kv_dim, c.d_model, 0});
+        wants.push_back({lname(l, "self_attn.v_proj.weight"), wdt, m->kv_dim, c.d_model, 0});
+        wants.push_back({lname(l, "self_attn.o_proj.weight"), wdt, c.d_model, m->q_dim, 0});
+        wants.push_back({lname(l, "mlp.gate_proj.weight"), wdt, c.ffn, c.d_model, 0});
+        wants.push_back({lname(l, "mlp.up_proj.weight"), wdt, c.ffn, c.d_model, 0});
+        wants.push_back({lname(l, "mlp.down_proj.weight"), wdt, c.d_model, c.ffn, 0});
     }
     size_t total = 0;
     std::vector<int> tidx;
@@ -311,7 +400,7 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
             return hipErrorInvalidValue;
         }
         const McfTensor& t = f.tensors()[i];
-        bool shape_ok = w.dtype == kDTypeK4
+        bool shape_ok = w.dtype != kDTypeF32
                             ? (t.shape.size() == 2 && (int64_t)t.shape[0] == w.rows && (int64_t)t.shape[1] == w.cols)
                             : (t.shape.size() == 1 && (int64_t)t.shape[0] == w.rows);
         if (t.dtype != w.dtype || !shape_ok) {
@@ -341,8 +430,14 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     size_t wi = 0;
     auto nextk = [&](int rows, int cols) { return k4_mat_from_payload(m->arena + wants[wi++].arena_off, rows, cols); };
     auto nextf = [&]() { return reinterpret_cast<const float*>(m->arena + wants[wi++].arena_off); };
-    m->embed = nextk(c.vocab, c.d_model);
-    m->lm_head = c.tie_embeddings ? m->embed : nextk(c.vocab, c.d_model);
+    auto nextb = [&]() { return reinterpret_cast<const uint16_t*>(m->arena + wants[wi++].arena_off); };
+    if (m->bf16) {
+        m->bembed = nextb();
+        m->blm_head = c.tie_embeddings ? m->bembed : nextb();
+    } else {
+        m->embed = nextk(c.vocab, c.d_model);
+        m->lm_head = c.tie_embeddings ? m->embed : nextk(c.vocab, c.d_model);
+    }
     m->final_norm = nextf();
     m->layers.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; l++) {
@@ -351,6 +446,16 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
         Ly.ffn_norm = nextf();
         Ly.q_norm = nextf();
         Ly.k_norm = nextf();
+        if (m->bf16) {
+            Ly.bq = nextb();
+            Ly.bk = nextb();
+            Ly.bv = nextb();
+            Ly.bo = nextb();
+            Ly.bgate = nextb();
+            Ly.bup = nextb();
+            Ly.bdown = nextb();
+            continue;
+        }
         Ly.wq = nextk(m->q_dim, c.d_model);
         Ly.wk = nextk(m->kv_dim, c.d_model);
         Ly.wv = nextk(m->kv_dim, c.d_model);
@@ -366,6 +471,10 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     CHECK(hipMalloc((void**)&m->qkv, sizeof(float) * (m->q_dim + 2 * m->kv_dim)));
     CHECK(hipMalloc((void**)&m->attn, sizeof(float) * m->q_dim));
     CHECK(hipMalloc((void**)&m->act, sizeof(float) * c.ffn));
+    if (m->bf16) {
+        CHECK(hipMalloc((void**)&m->xn, sizeof(float) * c.d_model));
+        CHECK(hipMalloc((void**)&m->up, sizeof(float) * c.ffn));
+    }
     CHECK(hipMalloc((void**)&m->logits, sizeof(float) * c.vocab));
     CHECK(hipMalloc((void**)&m->scores, sizeof(float) * (size_t)c.n_heads * max_ctx));
     CHECK(hipMalloc((void**)&m->attn_counters, sizeof(unsigned) * c.n_heads));

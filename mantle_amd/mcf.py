@@ -26,10 +26,17 @@ QWEN3_8B = dict(n_layers=36, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=12
                 vocab=151936, rope_base=1e6, eps=1e-6, tie_embeddings=0)
 
 
+DTYPE_BF16 = 3
+
+
 def make_config(**kw) -> Qwen3Config:
+    """Config struct from a model dict; "weights": "bf16" selects raw bf16 tensors."""
     cfg = Qwen3Config()
     for k, v in kw.items():
-        setattr(cfg, k, v)
+        if k == "weights":
+            cfg.weight_dtype = DTYPE_BF16 if v == "bf16" else 0
+        else:
+            setattr(cfg, k, v)
     return cfg
 
 

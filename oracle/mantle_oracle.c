@@ -571,6 +571,87 @@ int64_t mo_argmax(const float* x, int64_t n) {
 }
 
 /* ------------------------------------------------------------------------- */
+/* bf16 dense GEMV: internal/backend/simd/matvec.go:406-416 (matVecRangeBF16
+ * dispatch), :419-488 (Scalar), :490-713 (SIMD = AVX2), :715-979 (AVX512);
+ * bf16 -> f32 is internal/backend/core/dtype.go:67-69 (bits << 16), the f32 ->
+ * bf16 packer pkg/mcf/pack.go:789-793 (round to nearest even).
+ *
+ * Every row-grouping (4 / 2 / 1 rows at a time) of a path evaluates each row
+ * in the same order, so rows are independent here.  Go does not fuse the
+ * scalar a*b + c (GOAMD64=v1); archsimd MulAdd is an FMA. */
+
+float mo_bf16_to_f32(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t mo_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+static float bf16_row_avx512(const uint16_t* row, const float* x, int64_t c) {
+    /* matvec.go:738-834: acc (16 lanes) takes j = 32k + l, acc_2 j = 32k + 16 + l;
+     * a remaining 16-chunk goes into acc; acc += acc_2; lanes summed in order;
+     * the scalar tail follows. */
+    float acc[16] = {0}, acc2[16] = {0};
+    int64_t j = 0;
+    for (; j + 32 <= c; j += 32)
+        for (int l = 0; l < 16; l++) {
+            acc[l] = fmaf(mo_bf16_to_f32(row[j + l]), x[j + l], acc[l]);
+            acc2[l] = fmaf(mo_bf16_to_f32(row[j + 16 + l]), x[j + 16 + l], acc2[l]);
+        }
+    for (; j + 16 <= c; j += 16)
+        for (int l = 0; l < 16; l++) acc[l] = fmaf(mo_bf16_to_f32(row[j + l]), x[j + l], acc[l]);
+    float sum = 0.0f;
+    for (int l = 0; l < 16; l++) sum += acc[l] + acc2[l];
+    for (; j < c; j++) sum += mo_bf16_to_f32(row[j]) * x[j];
+    return sum;
+}
+
+static float bf16_row_avx2(const uint16_t* row, const float* x, int64_t c) {
+    /* matvec.go:513-610: one 8-lane accumulator, lane l takes j = 8m + l (the
+     * 16-wide loop feeds it twice per step); sum += t0 + t1 + ... + t7 left to
+     * right; the scalar tail follows. */
+    float acc[8] = {0};
+    int64_t j = 0;
+    for (; j + 8 <= c; j += 8)
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(mo_bf16_to_f32(row[j + l]), x[j + l], acc[l]);
+    float h = acc[0];
+    for (int l = 1; l < 8; l++) h += acc[l];
+    float sum = 0.0f;
+    sum += h;
+    for (; j < c; j++) sum += mo_bf16_to_f32(row[j]) * x[j];
+    return sum;
+}
+
+static float bf16_row_scalar(const uint16_t* row, const float* x, int64_t c) {
+    /* matvec.go:419-445: sum += p0 + p1 + ... + p7 per 8-chunk, then the tail. */
+    float sum = 0.0f;
+    int64_t j = 0;
+    for (; j + 7 < c; j += 8) {
+        float g = mo_bf16_to_f32(row[j]) * x[j];
+        for (int e = 1; e < 8; e++) g += mo_bf16_to_f32(row[j + e]) * x[j + e];
+        sum += g;
+    }
+    for (; j < c; j++) sum += mo_bf16_to_f32(row[j]) * x[j];
+    return sum;
+}
+
+void mo_bf16_matvec(int isa, const uint16_t* w, int64_t rows, int64_t cols, const float* x, float* y) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const uint16_t* row = w + r * cols;
+        y[r] = isa == MO_ISA_AVX512 ? bf16_row_avx512(row, x, cols)
+             : isa == MO_ISA_AVX2   ? bf16_row_avx2(row, x, cols)
+                                    : bf16_row_scalar(row, x, cols);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
 /* Qwen3 decoder: internal/backend/simd/runtime_greedy.go:12-67 (ForwardTokenGreedy),
  * internal/backend/simd/runtime_decode.go:29-203 (runDecoderLayers),
  * internal/backend/simd/attn.go:83-419 (CPU branch), internal/backend/simd/ffn.go:18-91. */
@@ -634,9 +715,21 @@ int mo_model_pos(const mo_model* m) { return m->pos; }
 void mo_model_hidden(const mo_model* m, float* out) { memcpy(out, m->x, sizeof(float) * (size_t)m->c.d_model); }
 
 static void quant_then_matvec(mo_model* m, const uint8_t* W, int64_t rows, int64_t cols, const float* x, float* y) {
+    if (m->c.wdtype == MO_W_BF16) {  /* matvec.go:154-172: no activation quantisation for bf16 */
+        mo_bf16_matvec(m->c.isa, (const uint16_t*)W, rows, cols, x, y);
+        return;
+    }
     int64_t blocks = (cols + 31) / 32;
     mo_quantize_vec_blocks(x, cols, blocks, m->qx, m->qs);
     mo_k4_matvec_w4a8_q(W, rows, cols, m->qx, m->qs, y);
+}
+
+/* The shared-activation GEMVs of Q/K/V and up/gate (attn.go:180-205,
+ * ffn.go:41-57): the int8 activation is prepared once (k4); bf16 runs the
+ * plain GEMV on x. */
+static void shared_matvec(mo_model* m, const uint8_t* W, int64_t rows, int64_t cols, const float* x, float* y) {
+    if (m->c.wdtype == MO_W_BF16) mo_bf16_matvec(m->c.isa, (const uint16_t*)W, rows, cols, x, y);
+    else mo_k4_matvec_w4a8_q(W, rows, cols, m->qx, m->qs, y);
 }
 
 int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
@@ -646,7 +739,12 @@ int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
     if (m->pos >= m->max_ctx) return -2;
     const int pos = m->pos;
     /* runtime_decode.go:29-51: x = Embeddings.RowTo(tok) */
-    mo_k4_row_to_f32(m->w.embed, c->vocab, d, tok, m->x);
+    if (c->wdtype == MO_W_BF16) {
+        const uint16_t* er = (const uint16_t*)m->w.embed + tok * d;
+        for (int64_t i = 0; i < d; i++) m->x[i] = mo_bf16_to_f32(er[i]);
+    } else {
+        mo_k4_row_to_f32(m->w.embed, c->vocab, d, tok, m->x);
+    }
     const float scale = (float)(1.0 / sqrt((double)hd)); /* attn.go:311-314 */
     mo_rope_tables(c->rope_base, (int)hd, pos, m->cosv, m->sinv);
     for (int l = 0; l < c->n_layers; l++) {
@@ -654,10 +752,10 @@ int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
         mo_rmsnorm(c->isa, m->tmp, m->x, m->w.attn_norm[l], d, c->eps);
         /* attn.go:180-205: one PrepareQuantVec shared by Q, K, V */
         int64_t blocks = (d + 31) / 32;
-        mo_quantize_vec_blocks(m->tmp, d, blocks, m->qx, m->qs);
-        mo_k4_matvec_w4a8_q(m->w.wq[l], m->q_dim, d, m->qx, m->qs, m->q);
-        mo_k4_matvec_w4a8_q(m->w.wk[l], m->kv_dim, d, m->qx, m->qs, m->k);
-        mo_k4_matvec_w4a8_q(m->w.wv[l], m->kv_dim, d, m->qx, m->qs, m->v);
+        if (c->wdtype != MO_W_BF16) mo_quantize_vec_blocks(m->tmp, d, blocks, m->qx, m->qs);
+        shared_matvec(m, m->w.wq[l], m->q_dim, d, m->tmp, m->q);
+        shared_matvec(m, m->w.wk[l], m->kv_dim, d, m->tmp, m->k);
+        shared_matvec(m, m->w.wv[l], m->kv_dim, d, m->tmp, m->v);
         /* attn.go:265-286 per-head RMSNorm */
         for (int h = 0; h < c->n_heads; h++)
             mo_rmsnorm(c->isa, m->q + h * hd, m->q + h * hd, m->w.q_norm[l], hd, c->eps);
@@ -678,9 +776,9 @@ int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
         for (int64_t i = 0; i < d; i++) m->x[i] += m->proj[i];
         /* runtime_decode.go:159 RMSNorm(ffn) ; ffn.go:41-57 shared qx for up, gate */
         mo_rmsnorm(c->isa, m->tmp, m->x, m->w.ffn_norm[l], d, c->eps);
-        mo_quantize_vec_blocks(m->tmp, d, blocks, m->qx, m->qs);
-        mo_k4_matvec_w4a8_q(m->w.w_up[l], f, d, m->qx, m->qs, m->up);
-        mo_k4_matvec_w4a8_q(m->w.w_gate[l], f, d, m->qx, m->qs, m->gate);
+        if (c->wdtype != MO_W_BF16) mo_quantize_vec_blocks(m->tmp, d, blocks, m->qx, m->qs);
+        shared_matvec(m, m->w.w_up[l], f, d, m->tmp, m->up);
+        shared_matvec(m, m->w.w_gate[l], f, d, m->tmp, m->gate);
         mo_silu_mul(m->act, m->gate, m->up, f);
         quant_then_matvec(m, m->w.w_down[l], d, f, m->act, m->down);
         for (int64_t i = 0; i < d; i++) m->x[i] += m->down[i];

@@ -58,6 +58,13 @@ int mo_k4_matvec_w4a8_q(const uint8_t* payload, int64_t rows, int64_t cols,
 /* W4A32: Mantle's non-AVX2 path (fp32 activations, scalar block dots). */
 int mo_k4_matvec_w4a32(const uint8_t* payload, int64_t rows, int64_t cols, const float* x, float* y);
 
+/* ---- bf16 dense GEMV (fp32 activations) ---- */
+/* Mantle's matVecRangeBF16 in each ISA's order (AVX-512: 32 lane chains, AVX2:
+ * 8, scalar: 8-term groups); bf16 -> fp32 is exact (bits << 16). */
+float mo_bf16_to_f32(uint16_t b);
+uint16_t mo_f32_to_bf16(float f);
+void mo_bf16_matvec(int isa, const uint16_t* w, int64_t rows, int64_t cols, const float* x, float* y);
+
 /* ---- elementwise / reductions ---- */
 float mo_dot(int isa, const float* a, const float* b, int64_t n);
 void mo_rmsnorm(int isa, float* dst, const float* src, const float* w, int64_t n, float eps);
@@ -78,7 +85,9 @@ typedef struct {
     double rope_base;
     float eps;
     int isa;
+    int wdtype; /* MO_W_K4: the matrix pointers below are k4 payloads; MO_W_BF16: bf16 [rows][cols] */
 } mo_config;
+enum { MO_W_K4 = 0, MO_W_BF16 = 1 };
 
 typedef struct {
     const uint8_t* embed;       /* k4 [vocab, d] */

@@ -24,7 +24,7 @@ F = C.c_float
 
 class Config(C.Structure):
     _fields_ = [("n_layers", I), ("d_model", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I), ("ffn", I),
-                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I)]
+                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I)]
 
 
 class Weights(C.Structure):
@@ -42,6 +42,9 @@ _SIGS = {
     "mo_k4_matvec_w4a8": (I, [P, I64, I64, P, P]),
     "mo_k4_matvec_w4a8_q": (I, [P, I64, I64, P, P, P]),
     "mo_k4_matvec_w4a32": (I, [P, I64, I64, P, P]),
+    "mo_bf16_to_f32": (F, [C.c_uint16]),
+    "mo_f32_to_bf16": (C.c_uint16, [F]),
+    "mo_bf16_matvec": (None, [I, P, I64, I64, P, P]),
     "mo_dot": (F, [I, P, P, I64]),
     "mo_rmsnorm": (None, [I, P, P, P, I64, F]),
     "mo_fast_exp": (F, [F]),
@@ -159,6 +162,22 @@ def matvec_w4a32(payload: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np
     return y
 
 
+def f32_to_bf16(x) -> np.ndarray:
+    """pkg/mcf/pack.go:789-793: round to nearest even on the dropped 16 bits."""
+    x = _f32(x)
+    return np.array([lib().mo_f32_to_bf16(float(v)) for v in x.ravel()], dtype=np.uint16).reshape(x.shape)
+
+
+def bf16_matvec(isa: int, w_bits: np.ndarray, x) -> np.ndarray:
+    """Mantle's matVecRangeBF16 (internal/backend/simd/matvec.go:406-979) in the ISA's order."""
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    rows, cols = w_bits.shape
+    x = _f32(x)
+    y = np.empty(rows, dtype=np.float32)
+    lib().mo_bf16_matvec(int(isa), _ptr(w_bits), rows, cols, _ptr(x), _ptr(y))
+    return y
+
+
 def dot(isa: int, a, b) -> float:
     a, b = _f32(a), _f32(b)
     return float(lib().mo_dot(isa, _ptr(a), _ptr(b), len(a)))
@@ -225,7 +244,8 @@ def argmax(x) -> int:
 
 
 class Model:
-    """Qwen3-shaped k4 decoder on the CPU (the greedy-token oracle).
+    """Qwen3-shaped decoder on the CPU (the greedy-token oracle), k4 weights or,
+    with cfg["weights"] == "bf16", bf16 ones.
 
     `tensors(name) -> np.uint8 payload / np.float32 gains` supplies the weights
     (e.g. views into an MCF file); they must outlive the model.
@@ -259,7 +279,7 @@ class Model:
                               ("w_down", "mlp.down_proj.weight")):
             setattr(w, field, arr([lname(l, suffix) for l in range(L)]))
         c = Config(cfg["n_layers"], cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"],
-                   cfg["vocab"], cfg["rope_base"], cfg["eps"], isa)
+                   cfg["vocab"], cfg["rope_base"], cfg["eps"], isa, 1 if cfg.get("weights") == "bf16" else 0)
         self._keep = keep
         self._w = w
         self._c = c

@@ -312,3 +312,60 @@ def test_argmax_first_max():
     x = np.array([1, 3, 3, -1, 3], dtype=np.float32)
     assert o.argmax(x) == 1
     assert o.argmax(np.array([-5.0], dtype=np.float32)) == 0
+
+
+# ---- bf16 dense GEMV (internal/backend/simd/matvec.go:406-979) ----
+
+@pytest.mark.parametrize("bits_in,bits_out", [(0x3F800000, 0x3F80), (0x3F808000, 0x3F80), (0x3F818000, 0x3F82),
+                                              (0x3F808001, 0x3F81), (0xBF7FFFFF, 0xBF80), (0x00000000, 0x0000)])
+def test_f32_to_bf16_round_nearest_even_kat(bits_in, bits_out):
+    """pkg/mcf/pack.go:789-793: ties go to the even bf16, anything above rounds up."""
+    f = np.frombuffer(np.uint32(bits_in).tobytes(), np.float32)[0]
+    assert o.lib().mo_f32_to_bf16(float(f)) == bits_out
+
+
+@pytest.mark.parametrize("cols", [8, 37, 100, 1000, 4104])
+def test_bf16_matvec_exact_integer_kat(cols):
+    """Small-integer bf16 weights and x in multiples of 1/8: every partial sum is
+    exact in fp32, so all three orders must give the integer result."""
+    rng = np.random.default_rng(cols)
+    wi = rng.integers(-8, 9, size=(9, cols))
+    xi = rng.integers(-16, 17, size=cols)
+    wb = o.f32_to_bf16(wi.astype(np.float32))
+    x = (xi / 8.0).astype(np.float32)
+    want = (wi @ xi) / 8.0
+    for isa in (o.ISA_SCALAR, o.ISA_AVX2, o.ISA_AVX512):
+        np.testing.assert_array_equal(o.bf16_matvec(isa, wb, x), want.astype(np.float32))
+
+
+def test_bf16_matvec_order_closed_form():
+    """One row where the three orders differ, worked by hand from the Go source
+    (x = 1): w_0 = 2^24, w_16 = -2^24, w_1..w_15 = 1.
+      AVX-512 (32 lane chains, acc + acc_2 per lane): lane 0 holds 2^24 and -2^24 -> 0, lanes 1..15
+        hold 1 -> 15.
+      AVX2 (8 lane chains): lane 0 takes 2^24 + 1 (rounds to 2^24) - 2^24 = 0, lanes 1..7 take two 1s
+        -> 14.
+      scalar (8-term groups): 2^24 + 1 + ... stays 2^24, + 8 = 2^24 + 8, + (-2^24 + 0...) -> 8."""
+    w = np.zeros((1, 32), np.float32)
+    w[0, 0], w[0, 16], w[0, 1:16] = 2.0 ** 24, -2.0 ** 24, 1.0
+    wb = o.f32_to_bf16(w)
+    x = np.ones(32, np.float32)
+    assert float(o.bf16_matvec(o.ISA_AVX512, wb, x)[0]) == 15.0
+    assert float(o.bf16_matvec(o.ISA_AVX2, wb, x)[0]) == 14.0
+    assert float(o.bf16_matvec(o.ISA_SCALAR, wb, x)[0]) == 8.0
+
+
+@pytest.mark.parametrize("rows,cols", [(17, 256), (19, 10240)])
+def test_bf16_matvec_simd_matches_scalar(rows, cols):
+    """TestMatVecBF16MatchesScalar (internal/backend/simd/matvec_bf16_test.go:11-50):
+    uniform(-1, 1) bf16 weights and x, every SIMD order within 5e-4 of the scalar
+    one; and all within float64 rounding of the exact product."""
+    rng = np.random.default_rng(1)
+    wb = o.f32_to_bf16(((rng.random((rows, cols)) - 0.5) * 2).astype(np.float32))
+    x = ((rng.random(cols) - 0.5) * 2).astype(np.float32)
+    scalar = o.bf16_matvec(o.ISA_SCALAR, wb, x)
+    exact = (wb.astype(np.uint32) << 16).view(np.float32).astype(np.float64) @ x.astype(np.float64)
+    for isa in (o.ISA_AVX2, o.ISA_AVX512):
+        assert np.abs(o.bf16_matvec(isa, wb, x) - scalar).max() <= 5e-4
+    for isa in (o.ISA_SCALAR, o.ISA_AVX2, o.ISA_AVX512):
+        assert np.abs(o.bf16_matvec(isa, wb, x) - exact).max() <= 1e-4 * np.sqrt(cols)
