@@ -109,7 +109,7 @@ __device__ __forceinline__ void stage_x(const Bf16Params& p, float* sx, int nt) 
 // AVX-512 order, four lanes per row, 16 rows per wave.  Weight loads run U
 // steps (of 32 elements) ahead of their FMAs, double-buffered; the first U are
 // issued before x is staged, so x's latency hides behind theirs.
-constexpr int kAvx512Unroll = 8;
+constexpr int kAvx512Unroll = 16;
 
 template <int EPI, int NW>
 __global__ __launch_bounds__(NW * 64) void bf16_gemv_avx512(Bf16Params p) {
