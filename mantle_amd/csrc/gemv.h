@@ -87,6 +87,17 @@ static inline int lane_small_rows() {
     return v;
 }
 
+// Matrices of at least this many blocks take the large-matrix launch (one
+// unit per multi-wave workgroup) even with few rows: measured on Qwen3-4B's
+// 6144 x 2560 QKV, 11.4 -> 7.6 us.
+static inline int64_t lane_large_blocks() {
+    static int64_t v = [] {
+        const char* e = getenv("MANTLE_HIP_GEMV_LARGE_BLOCKS");
+        return e ? (int64_t)atoll(e) : (int64_t)262144;
+    }();
+    return v;
+}
+
 static inline int gemv_max_wgs() {
     static int v = [] {
         const char* e = getenv("MANTLE_HIP_GEMV_MAX_WGS");

@@ -512,12 +512,21 @@ static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
     // two matrices' blocks per lane (gate and up) with the SiLU epilogue: at most 4
     constexpr int C16 = piece_bpl<T16, EPI == kEpiSiluMul ? 4 : 6>();
     constexpr bool L8 = BPR % 32 == 0 && BPR / 8 <= 8;  // whole 8-lane rows (u6 words: 4k blocks per lane)
+    constexpr int T8 = BPR / 8;
+    constexpr int C8 = piece_bpl<T8, 4>();
     int rows = 0;
     for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
     const bool q32 = EPI == kEpiSiluMul && p.q_out;
+    const bool large = rows > lane_small_rows() || (int64_t)rows * BPR >= lane_large_blocks();
+    if constexpr (BPR >= 80) {
+        // wide gate/up rows with the quantising SiLU epilogue: 32-row units of
+        // four waves at 8 lanes per row, in pieces; two such workgroups fit a
+        // CU, so the 4B/8B unit counts (304, 384) run in a single round
+        if (q32) return launch_lane_gemv<EPI, 8, C8, NB, 4, PRO, 2, T8>(p, stream);
+    }
     // (16-lane rows make 16-row units at four waves: the quantising SiLU
     // epilogue takes the eight-wave instance below)
-    if (rows > lane_small_rows() && (L8 || !q32)) {
+    if (large && (L8 || !q32)) {
         if constexpr (L8) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 1>(p, stream);
         else if constexpr (C16 == T16) return launch_lane_gemv<EPI, 16, T16, NB, 4, PRO, 1>(p, stream);
         else return launch_lane_gemv<EPI, 16, C16, NB, 4, PRO, 2, T16>(p, stream);
