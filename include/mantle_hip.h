@@ -110,6 +110,26 @@ int mantleHipStoreKVF32Row(float* cache, const float* src, int cachePos, int kvS
 int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const float* cacheV, float* out,
                                     float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
                                     int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
+/* Decode attention over Mantle's f16 KV cache (--cache-type-k/v f16, the CLI
+ * default: cmd/mantle/run.go:183-195); replaces mantleCudaAttentionInnerF16CacheF32
+ * (internal/backend/cuda/native/softmax.h:70-83), with the CPU arithmetic of
+ * internal/backend/simd/attnpool.go:103-106, :127-135 (DotF16 in the scalar
+ * order, p_t * f16(v) summed in key order).  Layout [pos][kvStride] uint16;
+ * scoresScratch as in mantleHipAttentionInnerF32Cache.  Split attention
+ * paths only (MANTLE_HIP_ATTN_SPLIT / _FUSED). */
+int mantleHipAttentionInnerF16CacheF32(const float* q, const uint16_t* cacheK, const uint16_t* cacheV, float* out,
+                                       float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
+                                       int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
+/* StoreKV into an f16 cache row; replaces mantleCudaStoreKVF16Row
+ * (internal/backend/cuda/native/attn_fused.cu:91-107) but converts as the CPU
+ * does (Float32ToFloat16: truncating, flush to zero, internal/backend/simd/float16.go:7-46). */
+int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int kvStride, mantleHipStream_t stream);
+/* KV cache element type of models loaded afterwards (LoadModelOptions.CacheTypeK/V,
+ * internal/backend/core/load_options.go:7-8): MANTLE_HIP_KV_F32 or MANTLE_HIP_KV_F16. */
+#define MANTLE_HIP_KV_F32 0
+#define MANTLE_HIP_KV_F16 1
+int mantleHipSetKVCacheType(int type);
+int mantleHipGetKVCacheType(void);
 /* Causal GQA attention over a whole prompt, bf16 inputs, on MFMA (head_dim 128).  Mantle
  * prefills k4 models position by position, RunAttnHeads over keys 0..t after RoPE
  * (internal/backend/simd/runtime_prefill.go:11-30, attnpool.go:77-153); its

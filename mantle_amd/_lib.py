@@ -38,6 +38,10 @@ _SIGS = {
     "mantleHipGetAttentionPath": (I, []),
     "mantleHipGetParityISA": (I, []),
     "mantleHipMatVecBF16F32": (I, [P, P, P, I, I, P]),
+    "mantleHipAttentionInnerF16CacheF32": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "mantleHipStoreKVF16Row": (I, [P, P, I, I, P]),
+    "mantleHipSetKVCacheType": (I, [I]),
+    "mantleHipGetKVCacheType": (I, []),
     "mantleHipQuantMatVecK4F32": (I, [P, P, P, P, P, I, I, I, P]),
     "mantleHipQuantMatVecK4W4A8F32": (I, [P, P, P, P, P, I, I, I, I, P, P, P]),
     "mantleHipQuantMatVecK4W4A8QF32": (I, [P, P, P, P, P, P, I, I, I, I, P]),

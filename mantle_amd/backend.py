@@ -29,10 +29,17 @@ class Backend:
     def name(self) -> str:
         return "hip"
 
-    def load_model(self, path: str, max_context: int = 4096, parity_isa: str = "avx512") -> "Runtime":
+    def load_model(self, path: str, max_context: int = 4096, parity_isa: str = "avx512",
+                   kv_cache: str = "f32") -> "Runtime":
+        """kv_cache: "f32" (Mantle's loader default) or "f16" (`mantle run`'s
+        --cache-type-k/v default, cmd/mantle/run.go:183-195)."""
         call("mantleHipSetParityISA", ISA[parity_isa])
+        call("mantleHipSetKVCacheType", {"f32": 0, "f16": 1}[kv_cache])
         h = P()
-        call("mantleHipModelLoadMCF", path.encode(), int(max_context), C.byref(h))
+        try:
+            call("mantleHipModelLoadMCF", path.encode(), int(max_context), C.byref(h))
+        finally:
+            call("mantleHipSetKVCacheType", 0)
         return Runtime(h, max_context)
 
     def load_model_image(self, image, max_context: int = 4096, parity_isa: str = "avx512") -> "Runtime":

@@ -357,6 +357,49 @@ __device__ __forceinline__ void chunk_store_v4(const ChunkRegs& c, float* dst, i
     if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
 }
 
+// The f16-cache form of ChunkRegs / chunk_issue_t / chunk_store_v4: four
+// f16 keys-elements (8 bytes) per load, widened to fp32 when staged.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+struct ChunkRegs16 {
+    u32x2 r[8];
+    int off[8];
+};
+
+template <int HD>
+__device__ __forceinline__ void chunk_issue16_t(ChunkRegs16& c, const uint16_t* __restrict__ base, int stride, int t0,
+                                                int nk, int kp, int skip) {
+    constexpr int hd4 = HD / 4;
+    const int total4 = nk * hd4;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int e = j * kThreads + threadIdx.x;
+        const bool live = e < total4;
+        const int ee = live ? e : 0;
+        const int tl = ee / hd4;
+        const int i4 = ee - tl * hd4;
+        const int t = t0 + tl;
+        c.r[j] = *reinterpret_cast<const u32x2*>(base + (size_t)t * stride + 4 * i4);
+        c.off[j] = (!live || t == skip) ? -1 : tl * kp + 4 * i4;
+    }
+}
+
+__device__ __forceinline__ void chunk_store16(const ChunkRegs16& c, float* dst, int kp, const float* cur, int t0,
+                                              int nk, int skip, int hd) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int o = c.off[j];
+        if (o < 0) continue;
+        f32x4 v;
+        v.x = mantle_f16_to_f32((uint16_t)(c.r[j].x & 0xFFFFu));
+        v.y = mantle_f16_to_f32((uint16_t)(c.r[j].x >> 16));
+        v.z = mantle_f16_to_f32((uint16_t)(c.r[j].y & 0xFFFFu));
+        v.w = mantle_f16_to_f32((uint16_t)(c.r[j].y >> 16));
+        *reinterpret_cast<f32x4*>(dst + o) = v;
+    }
+    // the step's own row: `cur` already holds its f16-rounded values
+    if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
+}
+
 static constexpr int kAttnV4Hdr = 704;  // sq, sk, sv (128 each), two 128-float wave stagings, 64 reduction
 
 // RMS scale of one head vector held two values per lane (x0 = element i,
@@ -437,12 +480,28 @@ __device__ __forceinline__ void prep_finish(const AttnArgs& a, PrepRegs r, int k
         x0 = y0;
         x1 = y1;
     }
+    if (a.kv_f16 && wave > 0) {  // the f16 cache holds (and the step reads back) the rounded row
+        x0 = f16_cache_round(x0);
+        x1 = f16_cache_round(x1);
+    }
     if (lane < half && (wave == 0 || a.fused)) {
         float* dst = wave == 0 ? sq : (wave == 1 ? sk : sv);
         dst[lane] = x0;
         dst[lane + half] = x1;
         if (a.fused && wave > 0 && append) {
-            if (wave == 2 && a.vt_stride > 0) {  // transposed V: one column per row of the cache
+            if (a.kv_f16) {
+                uint16_t* c16 = reinterpret_cast<uint16_t*>(wave == 1 ? a.cache_k : a.cache_v);
+                const uint16_t h0 = mantle_f32_to_f16_trunc(x0), h1 = mantle_f32_to_f16_trunc(x1);
+                if (wave == 2 && a.vt_stride > 0) {
+                    uint16_t* col = c16 + (size_t)(kvh * HD + lane) * a.vt_stride + pos;
+                    col[0] = h0;
+                    col[(size_t)half * a.vt_stride] = h1;
+                } else {
+                    uint16_t* row = c16 + (size_t)kvh * a.head_stride + (size_t)pos * a.kv_stride;
+                    row[lane] = h0;
+                    row[lane + half] = h1;
+                }
+            } else if (wave == 2 && a.vt_stride > 0) {  // transposed V: one column per row of the cache
                 float* col = a.cache_v + (size_t)(kvh * HD + lane) * a.vt_stride + pos;
                 col[0] = x0;
                 col[(size_t)half * a.vt_stride] = x1;
@@ -672,6 +731,14 @@ int attention_path() {
     return g_attn_path.load();
 }
 
+static std::atomic<int> g_kv_type{0};
+int kv_cache_type() { return g_kv_type.load(); }
+bool set_kv_cache_type(int t) {
+    if (t != 0 && t != 1) return false;
+    g_kv_type.store(t);
+    return true;
+}
+
 bool set_attention_path(int path) {
     if (path != kAttnPathSplit && path != kAttnPathSingle && path != kAttnPathGeneral && path != kAttnPathFused)
         return false;
@@ -690,8 +757,10 @@ static hipError_t allow_lds(void (*kern)(AttnArgs), size_t bytes) {
 }
 
 // Scores of head h, chunks sidx, sidx + S, ... into the scores buffer (the
-// body of attention_scores_split; attention_split_fused runs it first).
-template <int HD>
+// body of attention_scores_split; attention_split_fused runs it first).  F16:
+// the f16 cache, whose dot is DotF16 -- the scalar order in every ISA
+// (internal/backend/simd/ops.go:35-46).
+template <int HD, bool F16>
 __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* lds, int h, int sidx, int S, int pos) {
     float* sq = lds;
     float* sk = lds + 128;
@@ -704,12 +773,19 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
     const int kvh = h * a.kv_heads / a.n_head;
     const int nchunks = pos / kc + 1;
     const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
+    const uint16_t* kbase16 = reinterpret_cast<const uint16_t*>(a.cache_k) + (size_t)kvh * a.head_stride;
     const int skip = a.fused ? pos : -1;
     float* sg = a.scores + (size_t)h * a.max_ctx;
     const PrepRegs pr = prep_load<HD>(a, h, kvh, pos);
     __builtin_amdgcn_sched_barrier(0);
     ChunkRegs ck;
-    chunk_issue_t<HD>(ck, kbase, a.kv_stride, sidx * kc, min(kc, pos + 1 - sidx * kc), HD, kp, skip);
+    ChunkRegs16 ck16;
+    auto issue = [&](int c) {
+        const int nk = min(kc, pos + 1 - c * kc);
+        if constexpr (F16) chunk_issue16_t<HD>(ck16, kbase16, a.kv_stride, c * kc, nk, kp, skip);
+        else chunk_issue_t<HD>(ck, kbase, a.kv_stride, c * kc, nk, HD, kp, skip);
+    };
+    issue(sidx);
     PHASE(1);
     prep_finish<HD>(a, pr, kvh, pos, a.fused && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
     __syncthreads();
@@ -717,19 +793,22 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
     for (int c = sidx; c < nchunks; c += S) {
         const int t0 = c * kc;
         const int nk = min(kc, pos + 1 - t0);
-        chunk_store_v4(ck, kt, kp, sk, t0, nk, skip, HD);
+        if constexpr (F16) chunk_store16(ck16, kt, kp, sk, t0, nk, skip, HD);
+        else chunk_store_v4(ck, kt, kp, sk, t0, nk, skip, HD);
         __syncthreads();
         const int cn = c + S;
-        if (cn < nchunks) chunk_issue_t<HD>(ck, kbase, a.kv_stride, cn * kc, min(kc, pos + 1 - cn * kc), HD, kp, skip);
-        if (tid < nk)
-            sg[t0 + tid] = dot_v4_isa<HD>(reinterpret_cast<const float4*>(sq),
-                                          reinterpret_cast<const float4*>(kt + tid * kp), a.isa) * a.scale;
+        if (cn < nchunks) issue(cn);
+        if (tid < nk) {
+            const float4* qv = reinterpret_cast<const float4*>(sq);
+            const float4* kv = reinterpret_cast<const float4*>(kt + tid * kp);
+            sg[t0 + tid] = (F16 ? dot_parity_v4<HD, kIsaScalar>(qv, kv) : dot_v4_isa<HD>(qv, kv, a.isa)) * a.scale;
+        }
         __syncthreads();
     }
     PHASE(3);
 }
 
-template <int HD>
+template <int HD, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
@@ -738,20 +817,23 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     if (sidx >= pos / kAttnKeys + 1) return;  // whole workgroup: no chunk of this context for it
     PHASE_SLOT();
     PHASE(0);
-    scores_split_chunks<HD>(a, lds, h, sidx, S, pos);
+    scores_split_chunks<HD, F16>(a, lds, h, sidx, S, pos);
 }
 
 // V column d of one head for the V sum out_d = sum_t p_t * v_t,d (key order,
 // no FMA), streamed into a register ring of NG groups of VG keys that is
 // filled ahead of its use.  VT (transposed cache): the column's keys are
-// contiguous and one 16-byte load brings four of them; otherwise one 4-byte
-// load per key (rows kv_stride apart).  `own` (the fused step's V row, a
-// workgroup of this launch may still be appending it) replaces key `skip`.
-template <bool VT>
+// contiguous and one load brings four of them (16 bytes, or 8 from an F16
+// cache, widened when used); otherwise one load per key (rows kv_stride
+// apart).  `own` (the fused step's V row, a workgroup of this launch may still
+// be appending it) replaces key `skip`.
+template <bool VT, bool F16 = false>
 struct VColumn {
     static constexpr int VG = 32, NG = 5;
     f32x4 r[NG][VG / 4];
+    u32x2 h[F16 && VT ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
     const float* col;
+    const uint16_t* col16;
     size_t step;
     float own;
     int skip, pos;
@@ -759,35 +841,56 @@ struct VColumn {
     __device__ __forceinline__ void init(const AttnArgs& a, int kvh, int hd, int d, int pos_) {
         pos = pos_;
         skip = a.fused ? pos : -1;
+        const uint16_t* c16 = reinterpret_cast<const uint16_t*>(a.cache_v);
         if (VT) {
             col = a.cache_v + (size_t)(kvh * hd + d) * a.vt_stride;
+            col16 = c16 + (size_t)(kvh * hd + d) * a.vt_stride;
             step = 1;
         } else {
             col = a.cache_v + (size_t)kvh * a.head_stride + d;
+            col16 = c16 + (size_t)kvh * a.head_stride + d;
             step = (size_t)a.kv_stride;
         }
-        own = a.fused ? a.v[kvh * hd + d] : 0.0f;
+        own = a.fused ? (F16 ? f16_cache_round(a.v[kvh * hd + d]) : a.v[kvh * hd + d]) : 0.0f;
     }
+    __device__ __forceinline__ f32x4 patch(f32x4 v, int t) const {
+        if (skip >= 0) {
+            v.x = t == skip ? own : v.x;
+            v.y = t + 1 == skip ? own : v.y;
+            v.z = t + 2 == skip ? own : v.z;
+            v.w = t + 3 == skip ? own : v.w;
+        }
+        return v;
+    }
+    __device__ __forceinline__ int vt_key(int t0, int k4) const { return t0 + 4 * k4 <= pos ? t0 + 4 * k4 : (pos & ~3); }
     __device__ __forceinline__ void issue(int g, int t0) {
         if (VT) {
 #pragma unroll
             for (int k4 = 0; k4 < VG / 4; k4++) {
-                const int t = t0 + 4 * k4 <= pos ? t0 + 4 * k4 : (pos & ~3);
-                f32x4 v = *reinterpret_cast<const f32x4*>(col + t);  // keys past pos are read, never added
-                if (skip >= 0) {
-                    v.x = t == skip ? own : v.x;
-                    v.y = t + 1 == skip ? own : v.y;
-                    v.z = t + 2 == skip ? own : v.z;
-                    v.w = t + 3 == skip ? own : v.w;
-                }
-                r[g][k4] = v;
+                const int t = vt_key(t0, k4);  // keys past pos are read, never added
+                if constexpr (F16) h[g][k4] = *reinterpret_cast<const u32x2*>(col16 + t);
+                else r[g][k4] = patch(*reinterpret_cast<const f32x4*>(col + t), t);
             }
         } else {
 #pragma unroll
             for (int k = 0; k < VG; k++) {
                 const int t = t0 + k <= pos ? t0 + k : pos;
-                const float v = col[(size_t)t * step];
+                const float v = F16 ? mantle_f16_to_f32(col16[(size_t)t * step]) : col[(size_t)t * step];
                 r[g][k >> 2][k & 3] = t == skip ? own : v;
+            }
+        }
+    }
+    // Group g as fp32 (an F16 transposed ring is widened here, when its loads are needed).
+    __device__ __forceinline__ void widen(int g, int t0) {
+        if constexpr (F16 && VT) {
+#pragma unroll
+            for (int k4 = 0; k4 < VG / 4; k4++) {
+                f32x4 v;
+                v.x = mantle_f16_to_f32((uint16_t)(h[g][k4].x & 0xFFFFu));
+                v.y = mantle_f16_to_f32((uint16_t)(h[g][k4].x >> 16));
+                v.z = mantle_f16_to_f32((uint16_t)(h[g][k4].y & 0xFFFFu));
+                v.w = mantle_f16_to_f32((uint16_t)(h[g][k4].y >> 16));
+                r[g][k4] = patch(v, vt_key(t0, k4));
             }
         }
     }
@@ -805,6 +908,7 @@ struct VColumn {
             for (int gi = 0; gi < NG; gi++) {
                 const int t0 = (g0 + gi) * VG;
                 if (t0 <= pos) {
+                    widen(gi, t0);
                     float pg[VG];
 #pragma unroll
                     for (int i4 = 0; i4 < VG / 4; i4++) {
@@ -876,7 +980,7 @@ __device__ __forceinline__ void store_attn_out(const AttnArgs& a, int gi, float 
 // Softmax and the V sum of all of head h's columns, by the last of the head's
 // S score workgroups to finish (attention_split_fused), one column per lane of
 // waves 0 .. HD/64-1.
-template <int HD, bool PG, bool VT>
+template <int HD, bool PG, bool VT, bool F16>
 __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, int h, int pos) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvh = h * a.kv_heads / a.n_head;
@@ -885,7 +989,7 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
     float* red = PG ? lds : lds + (a.max_ctx + 31) / 32 * 32;
     const bool pv_wave = wave < HD / 64;
     const int d = wave * 64 + lane;
-    VColumn<VT> vc;
+    VColumn<VT, F16> vc;
     vc.init(a, kvh, HD, pv_wave ? d : 0, pos);
     if (pv_wave) vc.prime();  // the ring fills while the softmax runs
     head_softmax<PG>(sg, p, red, pos);
@@ -900,7 +1004,7 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
 // with a device-scope fence before counting) resets the counter and runs
 // softmax_pv_head.  Every workgroup counts, with or without a chunk, so the
 // last one always arrives and every wave exits.
-template <int HD, bool PG, bool VT>
+template <int HD, bool PG, bool VT, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
@@ -908,7 +1012,7 @@ __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     PHASE_SLOT();
     PHASE(0);
-    if (sidx < pos / kAttnKeys + 1) scores_split_chunks<HD>(a, lds, h, sidx, S, pos);
+    if (sidx < pos / kAttnKeys + 1) scores_split_chunks<HD, F16>(a, lds, h, sidx, S, pos);
     __threadfence();  // this workgroup's scores (and cache rows) before its arrival
     __syncthreads();
     __shared__ int is_last;  // outside the dynamic LDS that the softmax overwrites
@@ -922,10 +1026,10 @@ __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     if (!is_last) return;
     __threadfence();  // the other workgroups' scores, seen after their arrivals
     PHASE(4);
-    softmax_pv_head<HD, PG, VT>(a, lds, h, pos);
+    softmax_pv_head<HD, PG, VT, F16>(a, lds, h, pos);
 }
 
-template <int HD, bool VT>
+template <int HD, bool VT, bool F16>
 __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     constexpr int DB = 32;  // output columns per workgroup: one int8 block of the Wo activation
@@ -941,7 +1045,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     // wave 0 (lanes 0-31 the columns; 32-63 shadow them) streams its V
     // columns into a register ring from the start
     const int d = db * DB + (lane & 31);
-    VColumn<VT> vc;
+    VColumn<VT, F16> vc;
     vc.init(a, kvh, HD, d, pos);
     vc.skip = -1;  // the previous launch appended the step's row
     if (wave == 0) vc.prime();
@@ -995,6 +1099,8 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     const bool split_ok = fast_hd && a.scores && (mode == kAttnPathSplit || mode == kAttnPathFused);
     if (vt && (!split_ok || (a.vt_stride & 3) || a.vt_stride < (a.max_ctx + 3) / 4 * 4))
         return hipErrorInvalidValue;  // the transposed V cache is read by the split kernels only
+    if (a.kv_f16 && !split_ok) return hipErrorInvalidValue;  // the f16 cache is read by the split kernels only
+    const bool f16 = a.kv_f16 != 0;
     if (split_ok && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
         AttnArgs f = a;
         if (!f.counters) f.counters = library_counters(a.n_head);
@@ -1005,13 +1111,17 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         const bool pg = smem_p > 64 * 1024;  // probabilities in place in the scores buffer
         const size_t smem = pg || smem_p < smem_a ? smem_a : smem_p;
         const dim3 grid(a.n_head * S);
-        // kernel[hd 128][pg][vt]
-        void (*const kerns[2][2][2])(AttnArgs) = {
-            {{attention_split_fused<64, false, false>, attention_split_fused<64, false, true>},
-             {attention_split_fused<64, true, false>, attention_split_fused<64, true, true>}},
-            {{attention_split_fused<128, false, false>, attention_split_fused<128, false, true>},
-             {attention_split_fused<128, true, false>, attention_split_fused<128, true, true>}}};
-        hipLaunchKernelGGL(kerns[a.head_dim == 128][pg][vt], grid, dim3(kThreads), smem, stream, f);
+        // kernel[hd 128][pg][vt][f16]
+        void (*const kerns[2][2][2][2])(AttnArgs) = {
+            {{{attention_split_fused<64, false, false, false>, attention_split_fused<64, false, false, true>},
+              {attention_split_fused<64, false, true, false>, attention_split_fused<64, false, true, true>}},
+             {{attention_split_fused<64, true, false, false>, attention_split_fused<64, true, false, true>},
+              {attention_split_fused<64, true, true, false>, attention_split_fused<64, true, true, true>}}},
+            {{{attention_split_fused<128, false, false, false>, attention_split_fused<128, false, false, true>},
+              {attention_split_fused<128, false, true, false>, attention_split_fused<128, false, true, true>}},
+             {{attention_split_fused<128, true, false, false>, attention_split_fused<128, true, false, true>},
+              {attention_split_fused<128, true, true, false>, attention_split_fused<128, true, true, true>}}}};
+        hipLaunchKernelGGL(kerns[a.head_dim == 128][pg][vt][f16], grid, dim3(kThreads), smem, stream, f);
         return hipGetLastError();
     }
     if (split_ok) {
@@ -1019,15 +1129,17 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
         const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
         const int nd = a.head_dim / 32;
-        void (*const pv[2][2])(AttnArgs) = {{attention_pv_split<64, false>, attention_pv_split<64, true>},
-                                            {attention_pv_split<128, false>, attention_pv_split<128, true>}};
-        auto pvk = pv[a.head_dim == 128][vt];
+        void (*const pv[2][2][2])(AttnArgs) = {
+            {{attention_pv_split<64, false, false>, attention_pv_split<64, false, true>},
+             {attention_pv_split<64, true, false>, attention_pv_split<64, true, true>}},
+            {{attention_pv_split<128, false, false>, attention_pv_split<128, false, true>},
+             {attention_pv_split<128, true, false>, attention_pv_split<128, true, true>}}};
+        void (*const sc[2][2])(AttnArgs) = {{attention_scores_split<64, false>, attention_scores_split<64, true>},
+                                            {attention_scores_split<128, false>, attention_scores_split<128, true>}};
+        auto pvk = pv[a.head_dim == 128][vt][f16];
         const hipError_t e = allow_lds(pvk, smem_b);
         if (e != hipSuccess) return e;
-        if (a.head_dim == 128)
-            hipLaunchKernelGGL(attention_scores_split<128>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
-        else
-            hipLaunchKernelGGL(attention_scores_split<64>, dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
+        hipLaunchKernelGGL(sc[a.head_dim == 128][f16], dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
         hipLaunchKernelGGL(pvk, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
         return hipGetLastError();
     }

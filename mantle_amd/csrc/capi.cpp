@@ -159,6 +159,39 @@ int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const f
     return launch_attention_decode(a, S(stream));
 }
 
+int mantleHipAttentionInnerF16CacheF32(const float* q, const uint16_t* cacheK, const uint16_t* cacheV, float* out,
+                                       float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
+                                       int kvHeads, int cacheLen, float scale, mantleHipStream_t stream) {
+    if (start != 0 || (cacheLen > 0 && cacheLen <= pos) || pos < 0 || kvHeads <= 0 || nHead % kvHeads)
+        return hipErrorInvalidValue;
+    AttnArgs a{};
+    a.q = q;
+    a.cache_k = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheK));  // f16 values (kv_f16)
+    a.cache_v = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheV));
+    a.kv_f16 = 1;
+    a.scores = scoresScratch;
+    a.out = out;
+    a.pos_host = pos;
+    a.n_head = nHead;
+    a.kv_heads = kvHeads;
+    a.head_dim = headDim;
+    a.kv_stride = kvStride;
+    a.head_stride = headDim;
+    a.max_ctx = pos + 1;
+    a.scale = scale;
+    a.fused = 0;
+    a.isa = g_isa.load();
+    return launch_attention_decode(a, S(stream));
+}
+
+int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int kvStride, mantleHipStream_t stream) {
+    return launch_store_kv_row_f16(cache, src, cachePos, kvStride, S(stream));
+}
+
+int mantleHipSetKVCacheType(int type) { return set_kv_cache_type(type) ? hipSuccess : hipErrorInvalidValue; }
+
+int mantleHipGetKVCacheType(void) { return kv_cache_type(); }
+
 int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ropeCos,
                                   const float* ropeSin, float* out, int seqLen, int nHead, int kvHeads, int headDim,
                                   float scale, void* workspace, size_t workspaceBytes, mantleHipStream_t stream) {

@@ -24,6 +24,26 @@ __device__ __forceinline__ float mantle_f16_to_f32(uint16_t h) {
     return u2f(sign | ((exp + 112u) << 23) | (mant << 13));
 }
 
+// Mantle's fp32 -> fp16 for the f16 KV cache (internal/backend/simd/float16.go:7-46,
+// via StoreKV's Float32ToFloat16Slice): the mantissa is truncated, values too
+// small for a normal fp16 become signed zero, too large ones infinity, NaN a
+// quiet NaN with payload 0x200.
+__device__ __forceinline__ uint16_t mantle_f32_to_f16_trunc(float f) {
+    const uint32_t b = __float_as_uint(f);
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const int e = (int)((b >> 23) & 0xFFu);
+    const uint32_t m = b & 0x7FFFFFu;
+    if (e == 0) return (uint16_t)sign;
+    if (e == 0xFF) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0u));
+    const int ne = e - 112;  // e - 127 + 15
+    if (ne >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (ne <= 0) return (uint16_t)sign;
+    return (uint16_t)(sign | ((uint32_t)ne << 10) | (m >> 13));
+}
+
+// The value an f16 cache slot holds for x (store, then Mantle's load).
+__device__ __forceinline__ float f16_cache_round(float x) { return mantle_f16_to_f32(mantle_f32_to_f16_trunc(x)); }
+
 // k4 block scale (internal/backend/core/quant_cache.go:77-100):
 // super * (float(u6)/32), zero when either factor is zero.
 __device__ __forceinline__ float k4_scale(uint16_t super_bits, uint8_t sub) {

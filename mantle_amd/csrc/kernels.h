@@ -111,6 +111,8 @@ struct AttnArgs {
     int isa;
     int8_t* q_out;         // optional: out also as Mantle's int8 blocks (permuted layout) ...
     float* q_scale;        // ... and their scales, for the next W4A8 GEMV (head_dim % 32 == 0)
+    int kv_f16;            // cache_k / cache_v hold Mantle's truncating f16 (uint16) values
+                           // (--cache-type-k/v f16, split paths only)
     int vt_stride;         // > 0: V is stored transposed, element (t, d) of kv head g at
                            // cache_v + (g*head_dim + d)*vt_stride + t (split paths only)
     unsigned* counters;    // [n_head] zeroed arrival counters of the one-launch split path (null: the
@@ -153,5 +155,10 @@ hipError_t launch_rope_table(float* x, const float* cosv, const float* sinv, int
 hipError_t launch_rope_f64(float* x, const double* inv_freq, int pos, float attn_scale, int head_dim, int half,
                            int n_heads, hipStream_t stream);
 hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, int kv_stride, hipStream_t stream);
+hipError_t launch_store_kv_row_f16(uint16_t* cache, const float* src, int cache_pos, int kv_stride,
+                                   hipStream_t stream);
+// KV cache element type of models loaded from now on (0 f32, 1 f16).
+int kv_cache_type();
+bool set_kv_cache_type(int t);
 
 }  // namespace mantle

@@ -764,6 +764,21 @@ __global__ void store_kv_row_kernel(float* cache, const float* src, int cache_po
         cache[(size_t)cache_pos * kv_stride + i] = src[i];
 }
 
+// StoreKV into an f16 cache (ops_runtime.go:112-131, Float32ToFloat16Slice):
+// Mantle's truncating conversion.
+__global__ void store_kv_row_f16_kernel(uint16_t* cache, const float* src, int cache_pos, int kv_stride) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kv_stride; i += gridDim.x * blockDim.x)
+        cache[(size_t)cache_pos * kv_stride + i] = mantle_f32_to_f16_trunc(src[i]);
+}
+
+hipError_t launch_store_kv_row_f16(uint16_t* cache, const float* src, int cache_pos, int kv_stride,
+                                   hipStream_t stream) {
+    if (!cache || !src || cache_pos < 0 || kv_stride <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(store_kv_row_f16_kernel, dim3((kv_stride + kThreads - 1) / kThreads), dim3(kThreads), 0, stream,
+                       cache, src, cache_pos, kv_stride);
+    return hipGetLastError();
+}
+
 hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, int kv_stride, hipStream_t stream) {
     if (!cache || !src || cache_pos < 0 || kv_stride <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(store_kv_row_kernel, dim3((kv_stride + kThreads - 1) / kThreads), dim3(kThreads), 0, stream,

@@ -62,6 +62,7 @@ struct mantleHipModel {
     // keys contiguous, so the V sum loads four keys per 16 bytes.
     int vt_stride = 0;
     int v_rows = 0;  // per layer and kv column: max_ctx or vt_stride
+    int kv_f16 = 0;  // caches hold Mantle's truncating f16 (--cache-type-k/v f16)
     float *rope_cos = nullptr, *rope_sin = nullptr;
     DecodeState* state = nullptr;
     int* prompt = nullptr;
@@ -70,6 +71,12 @@ struct mantleHipModel {
     bool use_graph = true;
     hipGraphExec_t graph = nullptr;
 };
+
+// Layer l's base in a KV cache of `rows` keys per kv column (f32 or f16 elements).
+static float* layer_cache(const mantleHipModel* m, float* base, int l, int rows) {
+    const size_t elems = (size_t)l * rows * m->kv_dim;
+    return m->kv_f16 ? reinterpret_cast<float*>(reinterpret_cast<uint16_t*>(base) + elems) : base + elems;
+}
 
 // One decode step with raw-bf16 weights: Mantle's same layer loop
 // (runtime_decode.go:81-203) with every GEMV the plain bf16 one on fp32 x
@@ -105,8 +112,9 @@ static hipError_t enqueue_step_bf16(mantleHipModel* m, hipStream_t s) {
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
         a.pos_dev = &m->state->pos;
-        a.cache_k = m->cache_k + (size_t)l * m->max_ctx * m->kv_dim;
-        a.cache_v = m->cache_v + (size_t)l * m->v_rows * m->kv_dim;
+        a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx);
+        a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows);
+        a.kv_f16 = m->kv_f16;
         a.vt_stride = m->vt_stride;
         a.scores = m->scores;
         a.out = m->attn;
@@ -172,8 +180,9 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
         a.pos_dev = &m->state->pos;
-        a.cache_k = m->cache_k + (size_t)l * m->max_ctx * m->kv_dim;
-        a.cache_v = m->cache_v + (size_t)l * m->v_rows * m->kv_dim;
+        a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx);
+        a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows);
+        a.kv_f16 = m->kv_f16;
         a.vt_stride = m->vt_stride;
         a.scores = m->scores;
         a.out = m->attn;
@@ -487,8 +496,15 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     m->vt_stride = split ? (max_ctx + 3) / 4 * 4 : 0;
     m->v_rows = split ? m->vt_stride : max_ctx;
     const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
-    CHECK(hipMalloc((void**)&m->cache_k, sizeof(float) * kv_elems));
-    CHECK(hipMalloc((void**)&m->cache_v, sizeof(float) * v_elems));
+    m->kv_f16 = kv_cache_type() == 1;
+    if (m->kv_f16 && !split) {
+        fprintf(stderr, "mantle_hip: the f16 KV cache needs head_dim 64/128 and a split attention path\n");
+        free_model(m);
+        return hipErrorInvalidValue;
+    }
+    const size_t kv_elem = m->kv_f16 ? 2 : 4;
+    CHECK(hipMalloc((void**)&m->cache_k, kv_elem * kv_elems));
+    CHECK(hipMalloc((void**)&m->cache_v, kv_elem * v_elems));
     CHECK(hipMalloc((void**)&m->state, sizeof(DecodeState)));
     CHECK(hipMalloc((void**)&m->prompt, sizeof(int) * max_ctx));
     CHECK(hipMalloc((void**)&m->out_tokens, sizeof(int) * max_ctx));
@@ -510,8 +526,8 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     CHECK(hipMemset(m->state, 0, sizeof(DecodeState)));
     CHECK(hipMemset(m->prompt, 0, sizeof(int) * max_ctx));
     CHECK(hipMemset(m->out_tokens, 0, sizeof(int) * max_ctx));
-    CHECK(hipMemset(m->cache_k, 0, sizeof(float) * kv_elems));
-    CHECK(hipMemset(m->cache_v, 0, sizeof(float) * v_elems));
+    CHECK(hipMemset(m->cache_k, 0, kv_elem * kv_elems));
+    CHECK(hipMemset(m->cache_v, 0, kv_elem * v_elems));
     CHECK(hipDeviceSynchronize());
 #undef CHECK
     *out = m;

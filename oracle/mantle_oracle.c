@@ -560,6 +560,36 @@ void mo_attn_heads(int isa, const float* q, const float* ck, const float* cv, fl
     }
 }
 
+/* RunAttnHeads over an f16 KV cache (internal/backend/simd/attnpool.go:103-106,
+ * :127-135; the cache written by StoreKV's Float32ToFloat16Slice,
+ * ops_runtime.go:112-131): scores = DotF16(q, k) * scale, where DotF16 is the
+ * scalar sequential sum of q_i * f16(k_i) in every ISA (ops.go:35-46); the V
+ * sum adds p_t * f16(v_t) in key order.  Caches hold Mantle's truncating f16. */
+void mo_attn_heads_f16(const float* q, const uint16_t* ck, const uint16_t* cv, float* out, int pos, int start,
+                       int kv_stride, int head_dim, int n_head, int kv_heads, float scale) {
+    int win = pos - start + 1;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int h = 0; h < n_head; h++) {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)win);
+        int kvh = h * kv_heads / n_head;
+        const float* qh = q + (int64_t)h * head_dim;
+        for (int t = start; t <= pos; t++) {
+            const uint16_t* kt = ck + (int64_t)t * kv_stride + (int64_t)kvh * head_dim;
+            float sum = 0.0f;
+            for (int i = 0; i < head_dim; i++) sum += qh[i] * mo_f16_to_f32(kt[i]);
+            scores[t - start] = sum * scale;
+        }
+        mo_softmax(scores, win);
+        for (int d = 0; d < head_dim; d++) {
+            float sum = 0.0f;
+            for (int t = start; t <= pos; t++)
+                sum += scores[t - start] * mo_f16_to_f32(cv[(int64_t)t * kv_stride + (int64_t)kvh * head_dim + d]);
+            out[(int64_t)h * head_dim + d] = sum;
+        }
+        free(scores);
+    }
+}
+
 /* internal/backend/simd/runtime_greedy.go:70-82 (argmaxHost: strict '>'). */
 int64_t mo_argmax(const float* x, int64_t n) {
     if (n <= 0) return -1;
@@ -692,6 +722,7 @@ mo_model* mo_model_create(const mo_config* cfg, const mo_weights* w, int max_ctx
     m->act = calloc((size_t)f, 4);
     m->down = calloc((size_t)d, 4);
     m->logits = calloc((size_t)cfg->vocab, 4);
+    /* f32 cache, or (kv_f16) uint16 f16 values in the same [L][max_ctx][kv_dim] slots */
     m->cache_k = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx * m->kv_dim), 4);
     m->cache_v = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx * m->kv_dim), 4);
     m->cosv = calloc((size_t)cfg->head_dim, 4);
@@ -767,9 +798,21 @@ int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
         /* ops_runtime.go:40-131 StoreKV + RunAttnHeads */
         float* ck = m->cache_k + (int64_t)l * m->max_ctx * m->kv_dim;
         float* cv = m->cache_v + (int64_t)l * m->max_ctx * m->kv_dim;
-        memcpy(ck + (int64_t)pos * m->kv_dim, m->k, sizeof(float) * (size_t)m->kv_dim);
-        memcpy(cv + (int64_t)pos * m->kv_dim, m->v, sizeof(float) * (size_t)m->kv_dim);
-        mo_attn_heads(c->isa, m->q, ck, cv, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads, c->n_kv_heads, scale);
+        if (c->kv_f16) {  /* loader.go:645-663 --cache-type-k/v f16 */
+            uint16_t* ck16 = (uint16_t*)ck;
+            uint16_t* cv16 = (uint16_t*)cv;
+            for (int64_t i = 0; i < m->kv_dim; i++) {
+                ck16[(int64_t)pos * m->kv_dim + i] = mo_f32_to_f16(m->k[i]);
+                cv16[(int64_t)pos * m->kv_dim + i] = mo_f32_to_f16(m->v[i]);
+            }
+            mo_attn_heads_f16(m->q, ck16, cv16, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads, c->n_kv_heads,
+                              scale);
+        } else {
+            memcpy(ck + (int64_t)pos * m->kv_dim, m->k, sizeof(float) * (size_t)m->kv_dim);
+            memcpy(cv + (int64_t)pos * m->kv_dim, m->v, sizeof(float) * (size_t)m->kv_dim);
+            mo_attn_heads(c->isa, m->q, ck, cv, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads, c->n_kv_heads,
+                          scale);
+        }
         /* attn.go:417 Wo (re-quantises attnOut) */
         quant_then_matvec(m, m->w.wo[l], d, m->q_dim, m->attn, m->proj);
         /* runtime.go:278-289 addResidual */

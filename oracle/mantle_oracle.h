@@ -77,6 +77,9 @@ void mo_rope_tables(double base, int rot_dim, int pos, float* cos_out, float* si
 void mo_apply_rope(float* x, int n_head, int head_dim, int half, const float* cosv, const float* sinv);
 void mo_attn_heads(int isa, const float* q, const float* cache_k, const float* cache_v, float* out,
                    int pos, int start, int kv_stride, int head_dim, int n_head, int kv_heads, float scale);
+/* The same over an f16 cache [pos][kv_stride] (DotF16 is scalar in every ISA). */
+void mo_attn_heads_f16(const float* q, const uint16_t* cache_k, const uint16_t* cache_v, float* out, int pos, int start,
+                       int kv_stride, int head_dim, int n_head, int kv_heads, float scale);
 int64_t mo_argmax(const float* x, int64_t n);
 
 /* ---- Qwen3-shaped decoder (k4 weights, f32 KV cache) ---- */
@@ -86,6 +89,7 @@ typedef struct {
     float eps;
     int isa;
     int wdtype; /* MO_W_K4: the matrix pointers below are k4 payloads; MO_W_BF16: bf16 [rows][cols] */
+    int kv_f16; /* KV cache in Mantle's f16 (--cache-type-k/v f16) instead of f32 */
 } mo_config;
 enum { MO_W_K4 = 0, MO_W_BF16 = 1 };
 

@@ -24,7 +24,7 @@ F = C.c_float
 
 class Config(C.Structure):
     _fields_ = [("n_layers", I), ("d_model", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I), ("ffn", I),
-                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I)]
+                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I), ("kv_f16", I)]
 
 
 class Weights(C.Structure):
@@ -55,6 +55,7 @@ _SIGS = {
     "mo_rope_tables": (None, [C.c_double, I, I, P, P]),
     "mo_apply_rope": (None, [P, I, I, I, P, P]),
     "mo_attn_heads": (None, [I, P, P, P, P, I, I, I, I, I, I, F]),
+    "mo_attn_heads_f16": (None, [P, P, P, P, I, I, I, I, I, I, F]),
     "mo_argmax": (I64, [P, I64]),
     "mo_model_create": (P, [C.POINTER(Config), C.POINTER(Weights), I]),
     "mo_model_free": (None, [P]),
@@ -238,6 +239,18 @@ def attn_heads(isa: int, q, cache_k, cache_v, pos: int, kv_stride: int, head_dim
     return out
 
 
+def attn_heads_f16(q, cache_k16, cache_v16, pos: int, kv_stride: int, head_dim: int, n_head: int, kv_heads: int,
+                   scale: float) -> np.ndarray:
+    """RunAttnHeads over an f16 cache (attnpool.go:103-106, :127-135): uint16 f16 bits [pos+1][kv_stride]."""
+    q = _f32(q)
+    ck = np.ascontiguousarray(cache_k16, dtype=np.uint16)
+    cv = np.ascontiguousarray(cache_v16, dtype=np.uint16)
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    lib().mo_attn_heads_f16(_ptr(q), _ptr(ck), _ptr(cv), _ptr(out), int(pos), 0, int(kv_stride), int(head_dim),
+                            int(n_head), int(kv_heads), float(scale))
+    return out
+
+
 def argmax(x) -> int:
     x = _f32(x)
     return int(lib().mo_argmax(_ptr(x), len(x)))
@@ -245,7 +258,8 @@ def argmax(x) -> int:
 
 class Model:
     """Qwen3-shaped decoder on the CPU (the greedy-token oracle), k4 weights or,
-    with cfg["weights"] == "bf16", bf16 ones.
+    with cfg["weights"] == "bf16", bf16 ones; cfg["kv_cache"] == "f16" stores the
+    KV cache in Mantle's truncating f16.
 
     `tensors(name) -> np.uint8 payload / np.float32 gains` supplies the weights
     (e.g. views into an MCF file); they must outlive the model.
@@ -279,7 +293,8 @@ class Model:
                               ("w_down", "mlp.down_proj.weight")):
             setattr(w, field, arr([lname(l, suffix) for l in range(L)]))
         c = Config(cfg["n_layers"], cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"],
-                   cfg["vocab"], cfg["rope_base"], cfg["eps"], isa, 1 if cfg.get("weights") == "bf16" else 0)
+                   cfg["vocab"], cfg["rope_base"], cfg["eps"], isa, 1 if cfg.get("weights") == "bf16" else 0,
+                   1 if cfg.get("kv_cache") == "f16" else 0)
         self._keep = keep
         self._w = w
         self._c = c

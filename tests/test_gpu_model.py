@@ -70,6 +70,30 @@ def test_wide_rows_logits_bitexact(hip, tmp_models, shape):
         om.close()
 
 
+@pytest.mark.parametrize("path", ["split", "fused"])
+def test_lane_f16_kv_cache_bitexact(hip, lane_path, path):
+    """`mantle run`'s default --cache-type-k/v f16 (cmd/mantle/run.go:183-195): 100
+    fused steps with the f16 cache (transposed V) on both split paths, logits
+    bit-identical to the oracle's f16-cache decode."""
+    import mantle_amd
+    from mantle_amd import _lib
+    _lib.call("mantleHipSetAttentionPath", {"split": 0, "fused": 3}[path])
+    try:
+        rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=128, kv_cache="f16")
+        cfg = dict(models.LANE, kv_cache="f16")
+        om = models.oracle_model(lane_path, cfg, 128)
+        toks = models.prompt(100, models.LANE["vocab"], 6)
+        for step, tok in enumerate(toks):
+            logits = rt.forward_token(tok)
+            _, want = om.forward_greedy(tok, want_logits=True)
+            if step % 10 == 9 or step < 3:
+                np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+        rt.close()
+        om.close()
+    finally:
+        _lib.call("mantleHipSetAttentionPath", 0)
+
+
 @pytest.mark.parametrize("path", ["fused", "split", "single", "general"])
 def test_lane_long_context_attention_paths(hip, lane_path, path):
     """140 fused steps (past two 64-key chunks, the step's own K/V row inside
@@ -145,21 +169,23 @@ def test_context_limit_and_bad_token(hip, tiny_path):
         rt.close()
 
 
-def test_qwen3_0_6b_first_64_tokens(hip, tmp_models):
+@pytest.mark.parametrize("kv_cache", ["f32", "f16"])
+def test_qwen3_0_6b_first_64_tokens(hip, tmp_models, kv_cache):
     """Qwen3-0.6B shape, weights seed 0, 31-token prompt seed 1:
-    the first 64 greedy tokens equal the CPU oracle's."""
+    the first 64 greedy tokens equal the CPU oracle's, with Mantle's f32 cache
+    (the loader default) and its f16 cache (`mantle run`'s default)."""
     import mantle_amd
     from mantle_amd.mcf import QWEN3_0_6B
     from oracle import oracle as o
     path = models.pack(str(tmp_models / "qwen3_0_6b_k4.mcf"), 0, QWEN3_0_6B)
     p = models.prompt(31, QWEN3_0_6B["vocab"], 1)
-    rt = mantle_amd.new_backend().load_model(path, max_context=128)
+    rt = mantle_amd.new_backend().load_model(path, max_context=128, kv_cache=kv_cache)
     try:
         got = rt.generate_greedy(p, 64)
     finally:
         rt.close()
     o.set_threads(16)
-    om = models.oracle_model(path, QWEN3_0_6B, 128)
+    om = models.oracle_model(path, dict(QWEN3_0_6B, kv_cache=kv_cache), 128)
     try:
         want = om.generate_greedy(p, 64)
     finally:

@@ -168,3 +168,47 @@ def test_attention_long_context_bitexact(hip, oracle, path):
         g.assert_bitexact(g.host(out), want, "attention")
     finally:
         g.call("mantleHipSetAttentionPath", 0)
+
+
+def _f16(oracle, x):
+    return np.array([oracle.f32_to_f16(float(v)) for v in np.ravel(x)], dtype=np.uint16)
+
+
+@pytest.mark.parametrize("path", ["split", "fused"])
+@pytest.mark.parametrize("isa", [2, 0])
+@pytest.mark.parametrize("n_head,kv_heads,head_dim,pos", [(16, 8, 128, 0), (16, 8, 128, 130), (32, 8, 128, 1100),
+                                                         (8, 2, 64, 300)])
+def test_attention_f16_cache_bitexact(hip, oracle, path, isa, n_head, kv_heads, head_dim, pos):
+    """RunAttnHeads over Mantle's f16 cache (attnpool.go:103-106, :127-135): DotF16
+    is the scalar order in every ISA, so the parity ISA must not change the bits."""
+    kv = kv_heads * head_dim
+    rng = np.random.default_rng(pos + 7)
+    q = rng.standard_normal(n_head * head_dim).astype(np.float32)
+    ck = _f16(oracle, rng.standard_normal((pos + 1) * kv))
+    cv = _f16(oracle, rng.standard_normal((pos + 1) * kv))
+    scale = np.float32(1.0 / np.sqrt(head_dim))
+    g.call("mantleHipSetParityISA", isa)
+    g.call("mantleHipSetAttentionPath", ATTN_PATHS[path])
+    try:
+        out = g.empty(n_head * head_dim)
+        scratch = g.empty(n_head * (pos + 1))
+        g.call("mantleHipAttentionInnerF16CacheF32", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)),
+               g.ptr(out), g.ptr(scratch), pos, 0, kv, head_dim, n_head, kv_heads, pos + 1, ctypes.c_float(scale),
+               g.stream())
+        got = g.host(out)
+    finally:
+        g.call("mantleHipSetAttentionPath", 0)
+        g.call("mantleHipSetParityISA", 2)
+    g.assert_bitexact(got, oracle.attn_heads_f16(q, ck, cv, pos, kv, head_dim, n_head, kv_heads, float(scale)),
+                      "f16 attention")
+
+
+def test_store_kv_f16_row_truncates(hip, oracle):
+    """Float32ToFloat16 (internal/backend/simd/float16.go:7-46): truncation, FTZ, inf, NaN."""
+    vals = np.array([1.0, -2.5, 0.1, 65504.0, 70000.0, 1e-6, -1e-8, np.inf, np.nan, 3.14159, -0.0, 6.1e-5],
+                    dtype=np.float32)
+    kv = vals.size
+    cache = g.empty(3 * kv, torch.int16)
+    g.call("mantleHipStoreKVF16Row", g.ptr(cache), g.ptr(g.keep(vals)), 2, kv, g.stream())
+    got = g.host(cache).view(np.uint16)[2 * kv:]
+    np.testing.assert_array_equal(got, _f16(oracle, vals))

@@ -369,3 +369,64 @@ def test_bf16_matvec_simd_matches_scalar(rows, cols):
         assert np.abs(o.bf16_matvec(isa, wb, x) - scalar).max() <= 5e-4
     for isa in (o.ISA_SCALAR, o.ISA_AVX2, o.ISA_AVX512):
         assert np.abs(o.bf16_matvec(isa, wb, x) - exact).max() <= 1e-4 * np.sqrt(cols)
+
+
+# ---- f16 KV cache (internal/backend/simd/attnpool.go:103-106, :127-135) ----
+
+def _f16_bits(x):
+    return np.array([o.f32_to_f16(float(v)) for v in np.ravel(x)], dtype=np.uint16)
+
+
+def test_attn_f16_is_scalar_attention_on_the_decoded_cache():
+    """DotF16 is dotScalarF16 whatever the ISA (ops.go:35-46) and the V sum reads
+    Float16ToFloat32 values: over an f16 cache, RunAttnHeads equals the f32
+    attention in the scalar order on the decoded values."""
+    rng = np.random.default_rng(4)
+    nh, kvh, hd, pos = 4, 2, 64, 70
+    kv = kvh * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k16 = _f16_bits(rng.standard_normal((pos + 1) * kv) * 3)
+    v16 = _f16_bits(rng.standard_normal((pos + 1) * kv))
+    kf = np.array([o.f16_to_f32(int(b)) for b in k16], np.float32)
+    vf = np.array([o.f16_to_f32(int(b)) for b in v16], np.float32)
+    got = o.attn_heads_f16(q, k16, v16, pos, kv, hd, nh, kvh, 0.125)
+    np.testing.assert_array_equal(got, o.attn_heads(o.ISA_SCALAR, q, kf, vf, pos, kv, hd, nh, kvh, 0.125))
+
+
+def test_attn_f16_dot_order_closed_form():
+    """Worked by hand (hd 128, one head, keys 0 = all ones, 1 = all zeros, V rows
+    1 and 0): q_0 = 2^24, q_64 = -2^24, q_1..63 = 1.  The scalar DotF16 of key 0
+    loses every +1 against 2^24, then cancels to 0 -> scores equal -> out 0.5.
+    (The AVX-512 f32 Dot pairs q_0 with q_64 in one lane and keeps the 63 ones.)"""
+    hd = 128
+    q = np.zeros(hd, np.float32)
+    q[0], q[64], q[1:64] = 2.0 ** 24, -2.0 ** 24, 1.0
+    k16 = np.concatenate([np.full(hd, 0x3C00, np.uint16), np.zeros(hd, np.uint16)])
+    v16 = np.concatenate([np.full(hd, 0x3C00, np.uint16), np.zeros(hd, np.uint16)])
+    got = o.attn_heads_f16(q, k16, v16, 1, hd, hd, 1, 1, 1.0)
+    np.testing.assert_array_equal(got, np.full(hd, 0.5, np.float32))
+    f32 = o.attn_heads(o.ISA_AVX512, q, np.repeat([1.0, 0.0], hd).astype(np.float32),
+                       np.repeat([1.0, 0.0], hd).astype(np.float32), 1, hd, hd, 1, 1, 1.0)
+    assert float(f32[0]) > 0.99  # score 63 vs 0
+
+
+def test_attn_f16_vs_float64():
+    """TestRunAttnHeadsMatchesReference's tolerance (attn_test.go:10-86, 1e-5) against
+    float64 softmax attention over the f16-decoded cache."""
+    rng = np.random.default_rng(5)
+    nh, kvh, hd, pos = 8, 2, 128, 300
+    kv = kvh * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k16 = _f16_bits(rng.standard_normal((pos + 1) * kv))
+    v16 = _f16_bits(rng.standard_normal((pos + 1) * kv))
+    kf = np.array([o.f16_to_f32(int(b)) for b in k16]).reshape(pos + 1, kvh, hd)
+    vf = np.array([o.f16_to_f32(int(b)) for b in v16]).reshape(pos + 1, kvh, hd)
+    got = o.attn_heads_f16(q, k16, v16, pos, kv, hd, nh, kvh, float(1 / np.sqrt(hd)))
+    want = np.empty(nh * hd)
+    for h in range(nh):
+        g = h * kvh // nh
+        s = kf[:, g] @ q[h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        want[h * hd:(h + 1) * hd] = p @ vf[:, g]
+    np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-5)
