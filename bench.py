@@ -275,17 +275,19 @@ def large_model_run(args):
     mcf.pack_cached(path, seed, cfg)
     log(f"model ready in {time.perf_counter() - t0:.1f} s: {path}")
     prompt = mcf.uniform_tokens(plen, cfg["vocab"], 1)
-    rt = mantle_amd.new_backend("hip").load_model(path, max_context=plen + args.warmup + args.steps + 8)
+    rt = mantle_amd.new_backend("hip").load_model(path, max_context=plen + args.warmup + args.steps + 8,
+                                                  kv_cache=args.kv_cache)
     try:
         dt, prefill_tps = decode_run(rt, prompt, args.warmup, args.steps)
     finally:
         rt.close()
     tps = args.steps / dt
     wb = weight_bytes_per_token(cfg)
-    kv_mid = 2 * cfg["n_layers"] * cfg["n_kv_heads"] * cfg["head_dim"] * 4 * (plen + args.warmup + args.steps // 2)
-    log(f"{args.model} {args.weights}: decode {tps:.1f} tok/s, prefill {prefill_tps:.1f} tok/s")
+    kv_elem = 2 if args.kv_cache == "f16" else 4
+    kv_mid = 2 * cfg["n_layers"] * cfg["n_kv_heads"] * cfg["head_dim"] * kv_elem * (plen + args.warmup + args.steps // 2)
+    log(f"{args.model} {args.weights} kv {args.kv_cache}: decode {tps:.1f} tok/s, prefill {prefill_tps:.1f} tok/s")
     print(json.dumps({
-        "metric": f"decode tok/s @batch1, {args.model} {args.weights} after a {plen}-token prompt",
+        "metric": f"decode tok/s @batch1, {args.model} {args.weights} after a {plen}-token prompt, {args.kv_cache} KV cache",
         "value": round(tps, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
@@ -316,6 +318,8 @@ def main():
     ap.add_argument("--model", default="qwen3-0.6b", choices=["qwen3-0.6b", *LARGE_MODELS],
                     help="qwen3-4b / qwen3-8b: configs 4 / 5, a decode line of their own (not the headline)")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length for --model qwen3-4b / qwen3-8b")
+    ap.add_argument("--kv-cache", default="f32", choices=["f32", "f16"],
+                    help="KV cache element type for --model qwen3-4b / qwen3-8b (f16: `mantle run`'s default)")
     ap.add_argument("--weights", default="k4", choices=["k4", "bf16"],
                     help="weight format for --model qwen3-4b / qwen3-8b (config 5 runs both)")
     ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))

@@ -390,10 +390,10 @@ __device__ __forceinline__ void chunk_store16(const ChunkRegs16& c, float* dst, 
         const int o = c.off[j];
         if (o < 0) continue;
         f32x4 v;
-        v.x = mantle_f16_to_f32((uint16_t)(c.r[j].x & 0xFFFFu));
-        v.y = mantle_f16_to_f32((uint16_t)(c.r[j].x >> 16));
-        v.z = mantle_f16_to_f32((uint16_t)(c.r[j].y & 0xFFFFu));
-        v.w = mantle_f16_to_f32((uint16_t)(c.r[j].y >> 16));
+        v.x = f16_cache_value((uint16_t)(c.r[j].x & 0xFFFFu));
+        v.y = f16_cache_value((uint16_t)(c.r[j].x >> 16));
+        v.z = f16_cache_value((uint16_t)(c.r[j].y & 0xFFFFu));
+        v.w = f16_cache_value((uint16_t)(c.r[j].y >> 16));
         *reinterpret_cast<f32x4*>(dst + o) = v;
     }
     // the step's own row: `cur` already holds its f16-rounded values
@@ -875,7 +875,7 @@ struct VColumn {
 #pragma unroll
             for (int k = 0; k < VG; k++) {
                 const int t = t0 + k <= pos ? t0 + k : pos;
-                const float v = F16 ? mantle_f16_to_f32(col16[(size_t)t * step]) : col[(size_t)t * step];
+                const float v = F16 ? f16_cache_value(col16[(size_t)t * step]) : col[(size_t)t * step];
                 r[g][k >> 2][k & 3] = t == skip ? own : v;
             }
         }
@@ -886,10 +886,10 @@ struct VColumn {
 #pragma unroll
             for (int k4 = 0; k4 < VG / 4; k4++) {
                 f32x4 v;
-                v.x = mantle_f16_to_f32((uint16_t)(h[g][k4].x & 0xFFFFu));
-                v.y = mantle_f16_to_f32((uint16_t)(h[g][k4].x >> 16));
-                v.z = mantle_f16_to_f32((uint16_t)(h[g][k4].y & 0xFFFFu));
-                v.w = mantle_f16_to_f32((uint16_t)(h[g][k4].y >> 16));
+                v.x = f16_cache_value((uint16_t)(h[g][k4].x & 0xFFFFu));
+                v.y = f16_cache_value((uint16_t)(h[g][k4].x >> 16));
+                v.z = f16_cache_value((uint16_t)(h[g][k4].y & 0xFFFFu));
+                v.w = f16_cache_value((uint16_t)(h[g][k4].y >> 16));
                 r[g][k4] = patch(v, vt_key(t0, k4));
             }
         }

@@ -6,6 +6,7 @@
 // bit for bit (Go at GOAMD64=v1 never fuses; archsimd MulAdd always does).
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -39,6 +40,15 @@ __device__ __forceinline__ uint16_t mantle_f32_to_f16_trunc(float f) {
     if (ne >= 31) return (uint16_t)(sign | 0x7C00u);
     if (ne <= 0) return (uint16_t)sign;
     return (uint16_t)(sign | ((uint32_t)ne << 10) | (m >> 13));
+}
+
+// mantle_f16_to_f32 for f16 KV-cache values, on the hardware conversion
+// (v_cvt_f32_f16 is exact for normals, zero and infinity; Mantle flushes
+// subnormals to a signed zero).  NaNs come back quiet: the same bits as Mantle's
+// for every NaN mantle_f32_to_f16_trunc writes (payload 0x200).
+__device__ __forceinline__ float f16_cache_value(uint16_t h) {
+    const float f = __half2float(__ushort_as_half(h));
+    return fabsf(f) < 6.103515625e-05f ? __uint_as_float(__float_as_uint(f) & 0x80000000u) : f;
 }
 
 // The value an f16 cache slot holds for x (store, then Mantle's load).
