@@ -786,10 +786,8 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
         else chunk_issue_t<HD>(ck, kbase, a.kv_stride, c * kc, nk, HD, kp, skip);
     };
     issue(sidx);
-    PHASE(1);
     prep_finish<HD>(a, pr, kvh, pos, a.fused && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
     __syncthreads();
-    PHASE(2);
     for (int c = sidx; c < nchunks; c += S) {
         const int t0 = c * kc;
         const int nk = min(kc, pos + 1 - t0);
@@ -805,7 +803,6 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
         }
         __syncthreads();
     }
-    PHASE(3);
 }
 
 template <int HD, bool F16>
@@ -829,9 +826,11 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
 // be appending it) replaces key `skip`.
 template <bool VT, bool F16 = false>
 struct VColumn {
-    static constexpr int VG = 32, NG = 5;
-    f32x4 r[NG][VG / 4];
-    u32x2 h[F16 && VT ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
+    // an f16 transposed ring costs half the registers per key: twice the groups
+    static constexpr int VG = 32, NG = F16 && VT ? 10 : 5;
+    static constexpr bool RAW = F16 && VT;
+    f32x4 r[RAW ? 1 : NG][VG / 4];  // fp32 keys (for RAW: the group being summed, slot 0)
+    u32x2 h[RAW ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
     const float* col;
     const uint16_t* col16;
     size_t step;
@@ -864,7 +863,15 @@ struct VColumn {
     }
     __device__ __forceinline__ int vt_key(int t0, int k4) const { return t0 + 4 * k4 <= pos ? t0 + 4 * k4 : (pos & ~3); }
     __device__ __forceinline__ void issue(int g, int t0) {
-        if (VT) {
+        if (VT && t0 + VG <= pos) {
+            // the whole group lies below pos: no clamp and no own row, so the
+            // loads are one base address plus immediate offsets
+#pragma unroll
+            for (int k4 = 0; k4 < VG / 4; k4++) {
+                if constexpr (F16) h[g][k4] = reinterpret_cast<const u32x2*>(col16 + t0)[k4];
+                else r[g][k4] = reinterpret_cast<const f32x4*>(col + t0)[k4];
+            }
+        } else if (VT) {
 #pragma unroll
             for (int k4 = 0; k4 < VG / 4; k4++) {
                 const int t = vt_key(t0, k4);  // keys past pos are read, never added
@@ -883,6 +890,7 @@ struct VColumn {
     // Group g as fp32 (an F16 transposed ring is widened here, when its loads are needed).
     __device__ __forceinline__ void widen(int g, int t0) {
         if constexpr (F16 && VT) {
+            const bool whole = t0 + VG <= pos;  // as in issue(): no own row to patch
 #pragma unroll
             for (int k4 = 0; k4 < VG / 4; k4++) {
                 f32x4 v;
@@ -890,7 +898,7 @@ struct VColumn {
                 v.y = f16_cache_value((uint16_t)(h[g][k4].x >> 16));
                 v.z = f16_cache_value((uint16_t)(h[g][k4].y & 0xFFFFu));
                 v.w = f16_cache_value((uint16_t)(h[g][k4].y >> 16));
-                r[g][k4] = patch(v, vt_key(t0, k4));
+                r[0][k4] = whole ? v : patch(v, vt_key(t0, k4));
             }
         }
     }
@@ -909,6 +917,7 @@ struct VColumn {
                 const int t0 = (g0 + gi) * VG;
                 if (t0 <= pos) {
                     widen(gi, t0);
+                    const int ri = RAW ? 0 : gi;
                     float pg[VG];
 #pragma unroll
                     for (int i4 = 0; i4 < VG / 4; i4++) {
@@ -917,11 +926,11 @@ struct VColumn {
                     }
                     if (t0 + VG <= pos + 1) {
 #pragma unroll
-                        for (int k = 0; k < VG; k++) acc = acc + pg[k] * r[gi][k >> 2][k & 3];
+                        for (int k = 0; k < VG; k++) acc = acc + pg[k] * r[ri][k >> 2][k & 3];
                     } else {
 #pragma unroll
                         for (int k = 0; k < VG; k++) {
-                            const float nacc = acc + pg[k] * r[gi][k >> 2][k & 3];
+                            const float nacc = acc + pg[k] * r[ri][k >> 2][k & 3];
                             acc = t0 + k <= pos ? nacc : acc;
                         }
                     }
@@ -993,7 +1002,6 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
     vc.init(a, kvh, HD, pv_wave ? d : 0, pos);
     if (pv_wave) vc.prime();  // the ring fills while the softmax runs
     head_softmax<PG>(sg, p, red, pos);
-    PHASE(5);
     if (!pv_wave) return;
     store_attn_out(a, h * HD + d, vc.sum(p), true);
 }
