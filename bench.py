@@ -373,7 +373,7 @@ def main():
     if head:
         roofline = dict(bound="hbm", achieved=round(head["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
                         frac=round(head["frac"], 4), traffic=traffic_from_profile(),
-                        kernel="k4_gemv_lane_kernel<0,8,4,1,4,0,1> (W4A8 store, 8 lanes/row, 4-wave one-unit workgroups) 151936x1024 B=1",
+                        kernel="k4_gemv_lane_kernel<0,8,4,1,4,0,1,0> (W4A8 store, 8 lanes/row, 4-wave one-unit workgroups) 151936x1024 B=1",
                         avg_launch_us=round(head["avg_us"], 3), algo_bytes_per_launch=head["algo_bytes"])
     cpu = None
     if not args.no_cpu:
