@@ -283,7 +283,7 @@ def large_model_run(args):
         rt.close()
     tps = args.steps / dt
     wb = weight_bytes_per_token(cfg)
-    kv_elem = 2 if args.kv_cache == "f16" else 4
+    kv_elem = {"f16": 2, "q8_0": 1}.get(args.kv_cache, 4)
     kv_mid = 2 * cfg["n_layers"] * cfg["n_kv_heads"] * cfg["head_dim"] * kv_elem * (plen + args.warmup + args.steps // 2)
     log(f"{args.model} {args.weights} kv {args.kv_cache}: decode {tps:.1f} tok/s, prefill {prefill_tps:.1f} tok/s")
     print(json.dumps({
@@ -318,7 +318,7 @@ def main():
     ap.add_argument("--model", default="qwen3-0.6b", choices=["qwen3-0.6b", *LARGE_MODELS],
                     help="qwen3-4b / qwen3-8b: configs 4 / 5, a decode line of their own (not the headline)")
     ap.add_argument("--prompt", type=int, default=0, help="prompt length for --model qwen3-4b / qwen3-8b")
-    ap.add_argument("--kv-cache", default="f32", choices=["f32", "f16"],
+    ap.add_argument("--kv-cache", default="f32", choices=["f32", "f16", "q8_0"],
                     help="KV cache element type for --model qwen3-4b / qwen3-8b (f16: `mantle run`'s default)")
     ap.add_argument("--weights", default="k4", choices=["k4", "bf16"],
                     help="weight format for --model qwen3-4b / qwen3-8b (config 5 runs both)")

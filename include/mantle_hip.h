@@ -124,10 +124,28 @@ int mantleHipAttentionInnerF16CacheF32(const float* q, const uint16_t* cacheK, c
  * (internal/backend/cuda/native/attn_fused.cu:91-107) but converts as the CPU
  * does (Float32ToFloat16: truncating, flush to zero, internal/backend/simd/float16.go:7-46). */
 int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int kvStride, mantleHipStream_t stream);
+/* Decode attention over Mantle's q8_0 KV cache (--cache-type-k/v q8_0, cmd/mantle/run.go:183-195;
+ * a CPU-only cache type in Mantle, no CUDA counterpart), the arithmetic of
+ * internal/backend/simd/attnpool.go:100-102, :122-130: score = DotQ8(q, k_t, kScales[t]) * scale
+ * (ops.go:240-246, the scalar order), out_d = sum_t (p_t * v_t,d) * vScales[t] in key order.
+ * Layout [pos][kvStride] int8 (kvStride a multiple of 16, 16-byte aligned rows), one scale
+ * per position; scoresScratch as in mantleHipAttentionInnerF32Cache; positions up to 32768.
+ * Split attention paths only (MANTLE_HIP_ATTN_SPLIT / _FUSED, both take the two-launch form). */
+int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, const int8_t* cacheV,
+                                      const float* kScales, const float* vScales, float* out, float* scoresScratch,
+                                      int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
+                                      int cacheLen, float scale, mantleHipStream_t stream);
+/* StoreKV into a q8_0 cache (internal/backend/simd/ops_runtime.go:112-168, storeQ8): row cachePos
+ * of cacheK / cacheV ([pos][kvStride] int8) and kScales / vScales[cachePos], each row quantised
+ * with scale max|x|/127 over all kvStride values (kvStride <= 4096). */
+int mantleHipStoreKVQ8Row(int8_t* cacheK, int8_t* cacheV, float* kScales, float* vScales, const float* k,
+                          const float* v, int cachePos, int kvStride, mantleHipStream_t stream);
 /* KV cache element type of models loaded afterwards (LoadModelOptions.CacheTypeK/V,
- * internal/backend/core/load_options.go:7-8): MANTLE_HIP_KV_F32 or MANTLE_HIP_KV_F16. */
+ * internal/backend/core/load_options.go:7-8): MANTLE_HIP_KV_F32, MANTLE_HIP_KV_F16 or
+ * MANTLE_HIP_KV_Q8_0 (K and V of one type). */
 #define MANTLE_HIP_KV_F32 0
 #define MANTLE_HIP_KV_F16 1
+#define MANTLE_HIP_KV_Q8_0 2
 int mantleHipSetKVCacheType(int type);
 int mantleHipGetKVCacheType(void);
 /* Causal GQA attention over a whole prompt, bf16 inputs, on MFMA (head_dim 128).  Mantle

@@ -40,6 +40,8 @@ _SIGS = {
     "mantleHipMatVecBF16F32": (I, [P, P, P, I, I, P]),
     "mantleHipAttentionInnerF16CacheF32": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "mantleHipStoreKVF16Row": (I, [P, P, I, I, P]),
+    "mantleHipAttentionInnerQ8CacheF32": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "mantleHipStoreKVQ8Row": (I, [P, P, P, P, P, P, I, I, P]),
     "mantleHipSetKVCacheType": (I, [I]),
     "mantleHipGetKVCacheType": (I, []),
     "mantleHipQuantMatVecK4F32": (I, [P, P, P, P, P, I, I, I, P]),

@@ -31,10 +31,10 @@ class Backend:
 
     def load_model(self, path: str, max_context: int = 4096, parity_isa: str = "avx512",
                    kv_cache: str = "f32") -> "Runtime":
-        """kv_cache: "f32" (Mantle's loader default) or "f16" (`mantle run`'s
-        --cache-type-k/v default, cmd/mantle/run.go:183-195)."""
+        """kv_cache: "f32" (Mantle's loader default), "f16" (`mantle run`'s
+        --cache-type-k/v default, cmd/mantle/run.go:183-195) or "q8_0"."""
         call("mantleHipSetParityISA", ISA[parity_isa])
-        call("mantleHipSetKVCacheType", {"f32": 0, "f16": 1}[kv_cache])
+        call("mantleHipSetKVCacheType", {"f32": 0, "f16": 1, "q8_0": 2}[kv_cache])
         h = P()
         try:
             call("mantleHipModelLoadMCF", path.encode(), int(max_context), C.byref(h))

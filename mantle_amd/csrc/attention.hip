@@ -400,6 +400,52 @@ __device__ __forceinline__ void chunk_store16(const ChunkRegs16& c, float* dst, 
     if (skip >= t0 && skip < t0 + nk && (int)threadIdx.x < hd) dst[(skip - t0) * kp + threadIdx.x] = cur[threadIdx.x];
 }
 
+// The q8_0-cache form: sixteen int8 key elements (16 bytes) per load, up to
+// two loads per lane for a 64-key chunk of head_dim <= 128, widened to fp32
+// (exactly) when staged.  The step's own row is already in the cache.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+struct ChunkRegs8 {
+    u32x4 r[2];
+    int off[2];
+};
+
+__device__ __forceinline__ float q8_byte(uint32_t w, int c) { return (float)(int8_t)(uint8_t)(w >> (8 * c)); }
+
+template <int HD>
+__device__ __forceinline__ void chunk_issue8_t(ChunkRegs8& c, const int8_t* __restrict__ base, int stride, int t0,
+                                               int nk, int kp) {
+    constexpr int hd16 = HD / 16;
+    const int total = nk * hd16;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int e = j * kThreads + threadIdx.x;
+        const bool live = e < total;
+        const int ee = live ? e : 0;
+        const int tl = ee / hd16;
+        const int i16 = ee - tl * hd16;
+        c.r[j] = *reinterpret_cast<const u32x4*>(base + (size_t)(t0 + tl) * stride + 16 * i16);
+        c.off[j] = live ? tl * kp + 16 * i16 : -1;
+    }
+}
+
+__device__ __forceinline__ void chunk_store8(const ChunkRegs8& c, float* dst) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int o = c.off[j];
+        if (o < 0) continue;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t x = c.r[j][w];
+            f32x4 v;
+            v.x = q8_byte(x, 0);
+            v.y = q8_byte(x, 1);
+            v.z = q8_byte(x, 2);
+            v.w = q8_byte(x, 3);
+            *reinterpret_cast<f32x4*>(dst + o + 4 * w) = v;
+        }
+    }
+}
+
 static constexpr int kAttnV4Hdr = 704;  // sq, sk, sv (128 each), two 128-float wave stagings, 64 reduction
 
 // RMS scale of one head vector held two values per lane (x0 = element i,
@@ -438,6 +484,26 @@ struct PrepRegs {
     bool has_norm, rope;
 };
 
+// Per-head RMSNorm (attn.go:265-286, gains g0 / g1) and RoPE
+// (ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)) of one
+// vector held as RoPE pairs (x0 = element i, x1 = element i + HD/2, lanes
+// i < HD/2).  `norm` must be wave-uniform; buf: HD floats of wave-private LDS.
+template <int HD>
+__device__ __forceinline__ void prep_pair(float& x0, float& x1, float g0, float g1, float cs, float sn, bool norm,
+                                          bool rope, float eps, int isa, float* buf) {
+    if (norm) {
+        const float s = wave_rms_scale(x0, x1, HD, eps, isa, buf);
+        x0 = (x0 * s) * g0;
+        x1 = (x1 * s) * g1;
+    }
+    if (rope) {
+        const float y0 = x0 * cs - x1 * sn;
+        const float y1 = __builtin_fmaf(x0, sn, x1 * cs);
+        x0 = y0;
+        x1 = y1;
+    }
+}
+
 template <int HD>
 __device__ __forceinline__ PrepRegs prep_load(const AttnArgs& a, int h, int kvh, int pos) {
     constexpr int half = HD / 2;
@@ -469,17 +535,7 @@ __device__ __forceinline__ void prep_finish(const AttnArgs& a, PrepRegs r, int k
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (wave >= 3) return;
     float x0 = r.x0, x1 = r.x1;
-    if (r.has_norm) {  // attn.go:265-286 per-head RMSNorm
-        const float s = wave_rms_scale(x0, x1, HD, a.eps, a.isa, wbuf + wave * 128);
-        x0 = (x0 * s) * r.g0;
-        x1 = (x1 * s) * r.g1;
-    }
-    if (r.rope && wave < 2) {  // ops_avx512.go:162-190: y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c)
-        const float y0 = x0 * r.cs - x1 * r.sn;
-        const float y1 = __builtin_fmaf(x0, r.sn, x1 * r.cs);
-        x0 = y0;
-        x1 = y1;
-    }
+    prep_pair<HD>(x0, x1, r.g0, r.g1, r.cs, r.sn, r.has_norm, r.rope && wave < 2, a.eps, a.isa, wbuf + wave * 128);
     if (a.kv_f16 && wave > 0) {  // the f16 cache holds (and the step reads back) the rounded row
         x0 = f16_cache_round(x0);
         x1 = f16_cache_round(x1);
@@ -713,7 +769,7 @@ static constexpr int kSplitWgs = 16;
 //
 // Measured on MI355X, the one-launch form is the slower one where both apply
 // (Qwen3-0.6B decode 1135 -> 986 tok/s; Qwen3-8B after 16k tokens, 29 tok/s
-// against XXX for the split form): its V sum runs in one workgroup per
+// against 44 for the split form, both before the transposed V): its V sum runs in one workgroup per
 // head, whose CU's memory pipeline then bounds the head's V stream, while the
 // second launch of the split form spreads it over head_dim / 32 workgroups.
 static std::atomic<int> g_attn_path{-1};
@@ -734,7 +790,7 @@ int attention_path() {
 static std::atomic<int> g_kv_type{0};
 int kv_cache_type() { return g_kv_type.load(); }
 bool set_kv_cache_type(int t) {
-    if (t != 0 && t != 1) return false;
+    if (t != kKvF32 && t != kKvF16 && t != kKvQ8) return false;
     g_kv_type.store(t);
     return true;
 }
@@ -757,11 +813,14 @@ static hipError_t allow_lds(void (*kern)(AttnArgs), size_t bytes) {
 }
 
 // Scores of head h, chunks sidx, sidx + S, ... into the scores buffer (the
-// body of attention_scores_split; attention_split_fused runs it first).  F16:
-// the f16 cache, whose dot is DotF16 -- the scalar order in every ISA
-// (internal/backend/simd/ops.go:35-46).
-template <int HD, bool F16>
+// body of attention_scores_split; attention_split_fused runs it first).  KV:
+// the cache element type.  kKvF16: DotF16, the scalar order in every ISA
+// (internal/backend/simd/ops.go:35-46).  kKvQ8: DotQ8 (ops.go:240-246, the
+// scalar order, then times the position's scale) as attnpool.go:100-102 calls
+// it; the step's row is already in the cache, so nothing is appended here.
+template <int HD, int KV>
 __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* lds, int h, int sidx, int S, int pos) {
+    constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
     float* sq = lds;
     float* sk = lds + 128;
     float* sv = lds + 256;
@@ -774,24 +833,28 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
     const int nchunks = pos / kc + 1;
     const float* kbase = a.cache_k + (size_t)kvh * a.head_stride;
     const uint16_t* kbase16 = reinterpret_cast<const uint16_t*>(a.cache_k) + (size_t)kvh * a.head_stride;
-    const int skip = a.fused ? pos : -1;
+    const int8_t* kbase8 = reinterpret_cast<const int8_t*>(a.cache_k) + (size_t)kvh * a.head_stride;
+    const int skip = a.fused && !Q8 ? pos : -1;
     float* sg = a.scores + (size_t)h * a.max_ctx;
     const PrepRegs pr = prep_load<HD>(a, h, kvh, pos);
     __builtin_amdgcn_sched_barrier(0);
     ChunkRegs ck;
     ChunkRegs16 ck16;
+    ChunkRegs8 ck8;
     auto issue = [&](int c) {
         const int nk = min(kc, pos + 1 - c * kc);
-        if constexpr (F16) chunk_issue16_t<HD>(ck16, kbase16, a.kv_stride, c * kc, nk, kp, skip);
+        if constexpr (Q8) chunk_issue8_t<HD>(ck8, kbase8, a.kv_stride, c * kc, nk, kp);
+        else if constexpr (F16) chunk_issue16_t<HD>(ck16, kbase16, a.kv_stride, c * kc, nk, kp, skip);
         else chunk_issue_t<HD>(ck, kbase, a.kv_stride, c * kc, nk, HD, kp, skip);
     };
     issue(sidx);
-    prep_finish<HD>(a, pr, kvh, pos, a.fused && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
+    prep_finish<HD>(a, pr, kvh, pos, a.fused && !Q8 && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
     __syncthreads();
     for (int c = sidx; c < nchunks; c += S) {
         const int t0 = c * kc;
         const int nk = min(kc, pos + 1 - t0);
-        if constexpr (F16) chunk_store16(ck16, kt, kp, sk, t0, nk, skip, HD);
+        if constexpr (Q8) chunk_store8(ck8, kt);
+        else if constexpr (F16) chunk_store16(ck16, kt, kp, sk, t0, nk, skip, HD);
         else chunk_store_v4(ck, kt, kp, sk, t0, nk, skip, HD);
         __syncthreads();
         const int cn = c + S;
@@ -799,13 +862,14 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
         if (tid < nk) {
             const float4* qv = reinterpret_cast<const float4*>(sq);
             const float4* kv = reinterpret_cast<const float4*>(kt + tid * kp);
-            sg[t0 + tid] = (F16 ? dot_parity_v4<HD, kIsaScalar>(qv, kv) : dot_v4_isa<HD>(qv, kv, a.isa)) * a.scale;
+            if constexpr (Q8) sg[t0 + tid] = (dot_parity_v4<HD, kIsaScalar>(qv, kv) * a.k_scale[t0 + tid]) * a.scale;
+            else sg[t0 + tid] = (F16 ? dot_parity_v4<HD, kIsaScalar>(qv, kv) : dot_v4_isa<HD>(qv, kv, a.isa)) * a.scale;
         }
         __syncthreads();
     }
 }
 
-template <int HD, bool F16>
+template <int HD, int KV>
 __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
@@ -814,43 +878,55 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     if (sidx >= pos / kAttnKeys + 1) return;  // whole workgroup: no chunk of this context for it
     PHASE_SLOT();
     PHASE(0);
-    scores_split_chunks<HD, F16>(a, lds, h, sidx, S, pos);
+    scores_split_chunks<HD, KV>(a, lds, h, sidx, S, pos);
 }
 
 // V column d of one head for the V sum out_d = sum_t p_t * v_t,d (key order,
 // no FMA), streamed into a register ring of NG groups of VG keys that is
 // filled ahead of its use.  VT (transposed cache): the column's keys are
-// contiguous and one load brings four of them (16 bytes, or 8 from an F16
-// cache, widened when used); otherwise one load per key (rows kv_stride
-// apart).  `own` (the fused step's V row, a workgroup of this launch may still
-// be appending it) replaces key `skip`.
-template <bool VT, bool F16 = false>
+// contiguous and one load brings several of them (16 bytes of fp32, 8 of f16
+// or 16 of int8, widened when used); otherwise one load per key (rows
+// kv_stride apart).  `own` (the fused step's V row, a workgroup of this
+// launch may still be appending it) replaces key `skip`.  KV = kKvQ8: the sum
+// is sum_t (p_t * q_t,d) * s_t (attnpool.go:122-130); lane k of the wave holds
+// the scale of key t0 + k of each group in flight, read back per key with
+// readlane.
+template <bool VT, int KV = kKvF32>
 struct VColumn {
-    // an f16 transposed ring costs half the registers per key: twice the groups
-    static constexpr int VG = 32, NG = F16 && VT ? 10 : 5;
-    static constexpr bool RAW = F16 && VT;
+    static constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
+    // a narrow transposed ring costs fewer registers per key: twice the groups
+    static constexpr int VG = 32, NG = (F16 || Q8) && VT ? 10 : 5;
+    static constexpr bool RAW = (F16 || Q8) && VT;
     f32x4 r[RAW ? 1 : NG][VG / 4];  // fp32 keys (for RAW: the group being summed, slot 0)
-    u32x2 h[RAW ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
+    u32x2 h[F16 && VT ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
+    u32x4 b[Q8 && VT ? NG : 1][VG / 16];  // raw int8 keys (VT) until used
+    float sr[Q8 ? NG : 1];                // Q8: per-key scales, key t0 + k in lane k
     const float* col;
     const uint16_t* col16;
+    const int8_t* col8;
+    const float* vscale;
     size_t step;
     float own;
     int skip, pos;
 
     __device__ __forceinline__ void init(const AttnArgs& a, int kvh, int hd, int d, int pos_) {
         pos = pos_;
-        skip = a.fused ? pos : -1;
+        skip = a.fused && !Q8 ? pos : -1;
         const uint16_t* c16 = reinterpret_cast<const uint16_t*>(a.cache_v);
+        const int8_t* c8 = reinterpret_cast<const int8_t*>(a.cache_v);
+        vscale = a.v_scale;
         if (VT) {
             col = a.cache_v + (size_t)(kvh * hd + d) * a.vt_stride;
             col16 = c16 + (size_t)(kvh * hd + d) * a.vt_stride;
+            col8 = c8 + (size_t)(kvh * hd + d) * a.vt_stride;
             step = 1;
         } else {
             col = a.cache_v + (size_t)kvh * a.head_stride + d;
             col16 = c16 + (size_t)kvh * a.head_stride + d;
+            col8 = c8 + (size_t)kvh * a.head_stride + d;
             step = (size_t)a.kv_stride;
         }
-        own = a.fused ? (F16 ? f16_cache_round(a.v[kvh * hd + d]) : a.v[kvh * hd + d]) : 0.0f;
+        own = skip >= 0 ? (F16 ? f16_cache_round(a.v[kvh * hd + d]) : a.v[kvh * hd + d]) : 0.0f;
     }
     __device__ __forceinline__ f32x4 patch(f32x4 v, int t) const {
         if (skip >= 0) {
@@ -863,33 +939,64 @@ struct VColumn {
     }
     __device__ __forceinline__ int vt_key(int t0, int k4) const { return t0 + 4 * k4 <= pos ? t0 + 4 * k4 : (pos & ~3); }
     __device__ __forceinline__ void issue(int g, int t0) {
+        if constexpr (Q8) {
+            const int tk = t0 + (int)(threadIdx.x & 31);
+            sr[g] = vscale[tk <= pos ? tk : pos];
+        }
         if (VT && t0 + VG <= pos) {
             // the whole group lies below pos: no clamp and no own row, so the
             // loads are one base address plus immediate offsets
+            if constexpr (Q8) {
 #pragma unroll
-            for (int k4 = 0; k4 < VG / 4; k4++) {
-                if constexpr (F16) h[g][k4] = reinterpret_cast<const u32x2*>(col16 + t0)[k4];
-                else r[g][k4] = reinterpret_cast<const f32x4*>(col + t0)[k4];
+                for (int j = 0; j < VG / 16; j++) b[g][j] = reinterpret_cast<const u32x4*>(col8 + t0)[j];
+            } else {
+#pragma unroll
+                for (int k4 = 0; k4 < VG / 4; k4++) {
+                    if constexpr (F16) h[g][k4] = reinterpret_cast<const u32x2*>(col16 + t0)[k4];
+                    else r[g][k4] = reinterpret_cast<const f32x4*>(col + t0)[k4];
+                }
             }
         } else if (VT) {
+            if constexpr (Q8) {
 #pragma unroll
-            for (int k4 = 0; k4 < VG / 4; k4++) {
-                const int t = vt_key(t0, k4);  // keys past pos are read, never added
-                if constexpr (F16) h[g][k4] = *reinterpret_cast<const u32x2*>(col16 + t);
-                else r[g][k4] = patch(*reinterpret_cast<const f32x4*>(col + t), t);
+                for (int j = 0; j < VG / 16; j++) {
+                    const int t = t0 + 16 * j <= pos ? t0 + 16 * j : (pos & ~15);  // read, never added
+                    b[g][j] = *reinterpret_cast<const u32x4*>(col8 + t);
+                }
+            } else {
+#pragma unroll
+                for (int k4 = 0; k4 < VG / 4; k4++) {
+                    const int t = vt_key(t0, k4);  // keys past pos are read, never added
+                    if constexpr (F16) h[g][k4] = *reinterpret_cast<const u32x2*>(col16 + t);
+                    else r[g][k4] = patch(*reinterpret_cast<const f32x4*>(col + t), t);
+                }
             }
         } else {
 #pragma unroll
             for (int k = 0; k < VG; k++) {
                 const int t = t0 + k <= pos ? t0 + k : pos;
-                const float v = F16 ? f16_cache_value(col16[(size_t)t * step]) : col[(size_t)t * step];
+                const float v = Q8 ? (float)col8[(size_t)t * step]
+                                   : (F16 ? f16_cache_value(col16[(size_t)t * step]) : col[(size_t)t * step]);
                 r[g][k >> 2][k & 3] = t == skip ? own : v;
             }
         }
     }
-    // Group g as fp32 (an F16 transposed ring is widened here, when its loads are needed).
+    // Group g as fp32 (a narrow transposed ring is widened here, when its loads are needed).
     __device__ __forceinline__ void widen(int g, int t0) {
-        if constexpr (F16 && VT) {
+        if constexpr (Q8 && VT) {
+#pragma unroll
+            for (int j = 0; j < VG / 16; j++)
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t x = b[g][j][w];
+                    f32x4 v;
+                    v.x = q8_byte(x, 0);
+                    v.y = q8_byte(x, 1);
+                    v.z = q8_byte(x, 2);
+                    v.w = q8_byte(x, 3);
+                    r[0][4 * j + w] = v;
+                }
+        } else if constexpr (F16 && VT) {
             const bool whole = t0 + VG <= pos;  // as in issue(): no own row to patch
 #pragma unroll
             for (int k4 = 0; k4 < VG / 4; k4++) {
@@ -900,6 +1007,15 @@ struct VColumn {
                 v.w = f16_cache_value((uint16_t)(h[g][k4].y >> 16));
                 r[0][k4] = whole ? v : patch(v, vt_key(t0, k4));
             }
+        }
+    }
+    // Term k of group g: p * v, or for Q8 (p * q) * s.
+    __device__ __forceinline__ float term(float p, float v, int g, int k) const {
+        if constexpr (Q8) {
+            const float sk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sr[g]), k));
+            return (p * v) * sk;
+        } else {
+            return p * v;
         }
     }
     // Fill the ring (before the probabilities are ready).
@@ -926,11 +1042,11 @@ struct VColumn {
                     }
                     if (t0 + VG <= pos + 1) {
 #pragma unroll
-                        for (int k = 0; k < VG; k++) acc = acc + pg[k] * r[ri][k >> 2][k & 3];
+                        for (int k = 0; k < VG; k++) acc = acc + term(pg[k], r[ri][k >> 2][k & 3], gi, k);
                     } else {
 #pragma unroll
                         for (int k = 0; k < VG; k++) {
-                            const float nacc = acc + pg[k] * r[ri][k >> 2][k & 3];
+                            const float nacc = acc + term(pg[k], r[ri][k >> 2][k & 3], gi, k);
                             acc = t0 + k <= pos ? nacc : acc;
                         }
                     }
@@ -989,7 +1105,7 @@ __device__ __forceinline__ void store_attn_out(const AttnArgs& a, int gi, float 
 // Softmax and the V sum of all of head h's columns, by the last of the head's
 // S score workgroups to finish (attention_split_fused), one column per lane of
 // waves 0 .. HD/64-1.
-template <int HD, bool PG, bool VT, bool F16>
+template <int HD, bool PG, bool VT, int KV>
 __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, int h, int pos) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvh = h * a.kv_heads / a.n_head;
@@ -998,7 +1114,7 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
     float* red = PG ? lds : lds + (a.max_ctx + 31) / 32 * 32;
     const bool pv_wave = wave < HD / 64;
     const int d = wave * 64 + lane;
-    VColumn<VT, F16> vc;
+    VColumn<VT, KV> vc;
     vc.init(a, kvh, HD, pv_wave ? d : 0, pos);
     if (pv_wave) vc.prime();  // the ring fills while the softmax runs
     head_softmax<PG>(sg, p, red, pos);
@@ -1012,7 +1128,7 @@ __device__ __forceinline__ void softmax_pv_head(const AttnArgs& a, float* lds, i
 // with a device-scope fence before counting) resets the counter and runs
 // softmax_pv_head.  Every workgroup counts, with or without a chunk, so the
 // last one always arrives and every wave exits.
-template <int HD, bool PG, bool VT, bool F16>
+template <int HD, bool PG, bool VT, int KV>
 __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
@@ -1020,7 +1136,7 @@ __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
     PHASE_SLOT();
     PHASE(0);
-    if (sidx < pos / kAttnKeys + 1) scores_split_chunks<HD, F16>(a, lds, h, sidx, S, pos);
+    if (sidx < pos / kAttnKeys + 1) scores_split_chunks<HD, KV>(a, lds, h, sidx, S, pos);
     __threadfence();  // this workgroup's scores (and cache rows) before its arrival
     __syncthreads();
     __shared__ int is_last;  // outside the dynamic LDS that the softmax overwrites
@@ -1034,10 +1150,10 @@ __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     if (!is_last) return;
     __threadfence();  // the other workgroups' scores, seen after their arrivals
     PHASE(4);
-    softmax_pv_head<HD, PG, VT, F16>(a, lds, h, pos);
+    softmax_pv_head<HD, PG, VT, KV>(a, lds, h, pos);
 }
 
-template <int HD, bool VT, bool F16>
+template <int HD, bool VT, int KV>
 __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     constexpr int DB = 32;  // output columns per workgroup: one int8 block of the Wo activation
@@ -1053,7 +1169,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     // wave 0 (lanes 0-31 the columns; 32-63 shadow them) streams its V
     // columns into a register ring from the start
     const int d = db * DB + (lane & 31);
-    VColumn<VT, F16> vc;
+    VColumn<VT, KV> vc;
     vc.init(a, kvh, HD, d, pos);
     vc.skip = -1;  // the previous launch appended the step's row
     if (wave == 0) vc.prime();
@@ -1108,8 +1224,16 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (vt && (!split_ok || (a.vt_stride & 3) || a.vt_stride < (a.max_ctx + 3) / 4 * 4))
         return hipErrorInvalidValue;  // the transposed V cache is read by the split kernels only
     if (a.kv_f16 && !split_ok) return hipErrorInvalidValue;  // the f16 cache is read by the split kernels only
+    if (a.kv_q8) {
+        // the q8_0 cache: the two-launch split form only, 16-byte int8 rows
+        // and (transposed V) 16-key groups of a column
+        if (!split_ok || a.kv_f16 || a.max_ctx > kSplitMaxCtx || !a.k_scale || !a.v_scale || (a.kv_stride & 15) ||
+            (a.head_stride & 15) || (vt && ((a.vt_stride & 15) || a.vt_stride < (a.max_ctx + 15) / 16 * 16)))
+            return hipErrorInvalidValue;
+    }
     const bool f16 = a.kv_f16 != 0;
-    if (split_ok && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
+    const int kvt = a.kv_q8 ? kKvQ8 : (f16 ? kKvF16 : kKvF32);
+    if (split_ok && !a.kv_q8 && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
         AttnArgs f = a;
         if (!f.counters) f.counters = library_counters(a.n_head);
         if (!f.counters) return hipErrorInvalidValue;
@@ -1137,17 +1261,24 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
         const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
         const int nd = a.head_dim / 32;
-        void (*const pv[2][2][2])(AttnArgs) = {
-            {{attention_pv_split<64, false, false>, attention_pv_split<64, false, true>},
-             {attention_pv_split<64, true, false>, attention_pv_split<64, true, true>}},
-            {{attention_pv_split<128, false, false>, attention_pv_split<128, false, true>},
-             {attention_pv_split<128, true, false>, attention_pv_split<128, true, true>}}};
-        void (*const sc[2][2])(AttnArgs) = {{attention_scores_split<64, false>, attention_scores_split<64, true>},
-                                            {attention_scores_split<128, false>, attention_scores_split<128, true>}};
-        auto pvk = pv[a.head_dim == 128][vt][f16];
+        // kernel[hd 128][vt][cache type]
+        void (*const pv[2][2][3])(AttnArgs) = {
+            {{attention_pv_split<64, false, kKvF32>, attention_pv_split<64, false, kKvF16>,
+              attention_pv_split<64, false, kKvQ8>},
+             {attention_pv_split<64, true, kKvF32>, attention_pv_split<64, true, kKvF16>,
+              attention_pv_split<64, true, kKvQ8>}},
+            {{attention_pv_split<128, false, kKvF32>, attention_pv_split<128, false, kKvF16>,
+              attention_pv_split<128, false, kKvQ8>},
+             {attention_pv_split<128, true, kKvF32>, attention_pv_split<128, true, kKvF16>,
+              attention_pv_split<128, true, kKvQ8>}}};
+        void (*const sc[2][3])(AttnArgs) = {
+            {attention_scores_split<64, kKvF32>, attention_scores_split<64, kKvF16>, attention_scores_split<64, kKvQ8>},
+            {attention_scores_split<128, kKvF32>, attention_scores_split<128, kKvF16>,
+             attention_scores_split<128, kKvQ8>}};
+        auto pvk = pv[a.head_dim == 128][vt][kvt];
         const hipError_t e = allow_lds(pvk, smem_b);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(sc[a.head_dim == 128][f16], dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
+        hipLaunchKernelGGL(sc[a.head_dim == 128][kvt], dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
         hipLaunchKernelGGL(pvk, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
         return hipGetLastError();
     }
@@ -1163,6 +1294,100 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     const int kc = a.head_dim <= 128 ? kAttnKeys : (kThreads * 32) / a.head_dim;
     const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kc * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
     hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), smem, stream, a);
+    return hipGetLastError();
+}
+
+// storeQ8's element (ops_runtime.go:158-168): q = int32(v*inv + 0.5), or
+// int32(v*inv - 0.5) for v < 0, clamped to +-127.  Go's float32 -> int32 on
+// amd64 (CVTTSS2SL) gives INT32_MIN for NaN and out-of-range values, which the
+// clamp then takes to -127; the GPU conversion saturates, so that case is
+// made explicit (it arises when 127 / maxAbs overflows to +Inf).
+__device__ __forceinline__ int8_t q8_store_value(float v, float inv) {
+    const float t = v * inv;
+    const float r = v < 0.0f ? t - 0.5f : t + 0.5f;
+    int q = (r >= -2147483648.0f && r < 2147483648.0f) ? (int)r : INT32_MIN;
+    q = q > 127 ? 127 : (q < -127 ? -127 : q);
+    return (int8_t)q;
+}
+
+// One workgroup: the step's K and V rows (K prepared first when PREP: the
+// per-head RMSNorm and RoPE of the fused attention step, prep_pair), each
+// row's max |x| over all kv heads, its scale maxAbs / 127 and the int8 row
+// (storeQ8, ops_runtime.go:132-168).  LDS: both rows, 4 wave stagings, 8
+// reduction floats.
+template <int PREP_HD>
+__global__ __launch_bounds__(kThreads) void kv_append_q8_kernel(KvQ8Args a) {
+    extern __shared__ __align__(16) float lds[];
+    const int n = a.kv_heads * a.head_dim;
+    float* sk = lds;
+    float* sv = lds + n;
+    float* wbuf = sv + n;
+    float* red = wbuf + 4 * 128;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    if constexpr (PREP_HD > 0) {
+        constexpr int HD = PREP_HD, half = HD / 2;
+        const int li = lane < half ? lane : 0;
+        const bool norm = a.k_norm != nullptr, rope = a.rope_cos != nullptr;
+        for (int g = wave; g < a.kv_heads; g += kThreads / 64) {
+            float x0 = a.k[g * HD + li], x1 = a.k[g * HD + li + half];
+            const float g0 = norm ? a.k_norm[li] : 0.0f, g1 = norm ? a.k_norm[li + half] : 0.0f;
+            const float cs = rope ? a.rope_cos[(size_t)pos * half + li] : 0.0f;
+            const float sn = rope ? a.rope_sin[(size_t)pos * half + li] : 0.0f;
+            prep_pair<HD>(x0, x1, g0, g1, cs, sn, norm, rope, a.eps, a.isa, wbuf + wave * 128);
+            if (lane < half) {
+                sk[g * HD + lane] = x0;
+                sk[g * HD + lane + half] = x1;
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += kThreads) sk[i] = a.k[i];
+    }
+    for (int i = tid; i < n; i += kThreads) sv[i] = a.v[i];
+    __syncthreads();
+    float mk = 0.0f, mv = 0.0f;
+    for (int i = tid; i < n; i += kThreads) {
+        mk = fmaxf(mk, fabsf(sk[i]));
+        mv = fmaxf(mv, fabsf(sv[i]));
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        mk = fmaxf(mk, __shfl_down(mk, off, 64));
+        mv = fmaxf(mv, __shfl_down(mv, off, 64));
+    }
+    if (lane == 0) {
+        red[wave] = mk;
+        red[4 + wave] = mv;
+    }
+    __syncthreads();
+    const float max_k = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float max_v = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+    // a zero row: scale 0 and zeros (ops_runtime.go:147-153)
+    const float inv_k = max_k == 0.0f ? 0.0f : 127.0f / max_k;
+    const float inv_v = max_v == 0.0f ? 0.0f : 127.0f / max_v;
+    for (int i = tid; i < n; i += kThreads) {
+        const int g = i / a.head_dim, d = i - g * a.head_dim;
+        const size_t row = (size_t)g * a.head_stride + (size_t)pos * a.row_stride + d;
+        a.cache_k[row] = max_k == 0.0f ? (int8_t)0 : q8_store_value(sk[i], inv_k);
+        const int8_t qv = max_v == 0.0f ? (int8_t)0 : q8_store_value(sv[i], inv_v);
+        if (a.vt_stride > 0) a.cache_v[(size_t)i * a.vt_stride + pos] = qv;
+        else a.cache_v[row] = qv;
+    }
+    if (tid == 0) {
+        a.k_scale[pos] = max_k / 127.0f;
+        a.v_scale[pos] = max_v / 127.0f;
+    }
+}
+
+hipError_t launch_kv_append_q8(const KvQ8Args& a, hipStream_t stream) {
+    if (!a.k || !a.v || !a.cache_k || !a.cache_v || !a.k_scale || !a.v_scale || a.kv_heads <= 0 || a.head_dim <= 0 ||
+        a.kv_heads * a.head_dim > kKvQ8MaxRow || a.head_stride < 0 || a.row_stride < 0 || a.vt_stride < 0)
+        return hipErrorInvalidValue;
+    if (!a.pos_dev && a.pos_host < 0) return hipErrorInvalidValue;
+    if (a.prep && a.head_dim != 64 && a.head_dim != 128) return hipErrorInvalidValue;
+    if (a.rope_cos && !a.rope_sin) return hipErrorInvalidValue;
+    const size_t smem = sizeof(float) * (2 * (size_t)a.kv_heads * a.head_dim + 4 * 128 + 8);
+    auto k = !a.prep ? kv_append_q8_kernel<0> : (a.head_dim == 128 ? kv_append_q8_kernel<128> : kv_append_q8_kernel<64>);
+    hipLaunchKernelGGL(k, dim3(1), dim3(kThreads), smem, stream, a);
     return hipGetLastError();
 }
 

@@ -188,6 +188,52 @@ int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int 
     return launch_store_kv_row_f16(cache, src, cachePos, kvStride, S(stream));
 }
 
+int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, const int8_t* cacheV,
+                                      const float* kScales, const float* vScales, float* out, float* scoresScratch,
+                                      int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
+                                      int cacheLen, float scale, mantleHipStream_t stream) {
+    if (start != 0 || (cacheLen > 0 && cacheLen <= pos) || pos < 0 || kvHeads <= 0 || nHead % kvHeads)
+        return hipErrorInvalidValue;
+    AttnArgs a{};
+    a.q = q;
+    a.cache_k = reinterpret_cast<float*>(const_cast<int8_t*>(cacheK));  // int8 values (kv_q8)
+    a.cache_v = reinterpret_cast<float*>(const_cast<int8_t*>(cacheV));
+    a.kv_q8 = 1;
+    a.k_scale = kScales;
+    a.v_scale = vScales;
+    a.scores = scoresScratch;
+    a.out = out;
+    a.pos_host = pos;
+    a.n_head = nHead;
+    a.kv_heads = kvHeads;
+    a.head_dim = headDim;
+    a.kv_stride = kvStride;
+    a.head_stride = headDim;
+    a.max_ctx = pos + 1;
+    a.scale = scale;
+    a.fused = 0;
+    a.isa = g_isa.load();
+    return launch_attention_decode(a, S(stream));
+}
+
+int mantleHipStoreKVQ8Row(int8_t* cacheK, int8_t* cacheV, float* kScales, float* vScales, const float* k,
+                          const float* v, int cachePos, int kvStride, mantleHipStream_t stream) {
+    if (cachePos < 0 || kvStride <= 0) return hipErrorInvalidValue;
+    KvQ8Args a{};
+    a.k = k;
+    a.v = v;
+    a.pos_host = cachePos;
+    a.kv_heads = 1;
+    a.head_dim = kvStride;
+    a.cache_k = cacheK;
+    a.cache_v = cacheV;
+    a.head_stride = 0;
+    a.row_stride = kvStride;
+    a.k_scale = kScales;
+    a.v_scale = vScales;
+    return launch_kv_append_q8(a, S(stream));
+}
+
 int mantleHipSetKVCacheType(int type) { return set_kv_cache_type(type) ? hipSuccess : hipErrorInvalidValue; }
 
 int mantleHipGetKVCacheType(void) { return kv_cache_type(); }

@@ -117,6 +117,10 @@ struct AttnArgs {
                            // cache_v + (g*head_dim + d)*vt_stride + t (split paths only)
     unsigned* counters;    // [n_head] zeroed arrival counters of the one-launch split path (null: the
                            // library's own, for callers that serialise their launches on one stream)
+    int kv_q8;             // cache_k / cache_v hold int8 rows with one scale per position in
+    const float* k_scale;  // k_scale / v_scale [max_ctx] (--cache-type-k/v q8_0; two-launch split
+    const float* v_scale;  // path only).  The step's own rows must already be in the cache (fused:
+                           // q alone is prepared here, launch_kv_append_q8 prepares and appends K / V)
 };
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 // Decode-attention kernel variant for head_dim 64 / 128 (other sizes always
@@ -158,6 +162,30 @@ hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, in
 hipError_t launch_store_kv_row_f16(uint16_t* cache, const float* src, int cache_pos, int kv_stride,
                                    hipStream_t stream);
 // KV cache element type of models loaded from now on (0 f32, 1 f16).
+// The q8_0 KV append (ops_runtime.go:112-157 StoreKV / storeQ8): one int8
+// row of kv_heads*head_dim values per position for K and for V, each with one
+// scale (max |x| / 127 over the whole row).  prep: K is first given the
+// per-head RMSNorm (k_norm, when not null) and RoPE (rope_cos / rope_sin at
+// the position, when not null) of the fused attention step.
+struct KvQ8Args {
+    const float *k, *v;
+    const float* k_norm;
+    const float *rope_cos, *rope_sin;  // [max_ctx][head_dim/2]
+    const int* pos_dev;                // device position, or pos_host when null
+    int pos_host;
+    float eps;
+    int isa;
+    int kv_heads, head_dim;
+    int8_t *cache_k, *cache_v;  // element (t, d) of kv head g: g*head_stride + t*row_stride + d
+    int head_stride, row_stride;
+    int vt_stride;  // > 0: V transposed, (g*head_dim + d)*vt_stride + t
+    float *k_scale, *v_scale;  // [max_ctx]
+    int prep;
+};
+static constexpr int kKvQ8MaxRow = 4096;  // kv_heads*head_dim: both rows staged in LDS
+hipError_t launch_kv_append_q8(const KvQ8Args& a, hipStream_t stream);
+// KV cache element types (kv_cache_type): Mantle's CacheTypeF32 / F16 / Q8_0.
+enum KvCacheType : int { kKvF32 = 0, kKvF16 = 1, kKvQ8 = 2 };
 int kv_cache_type();
 bool set_kv_cache_type(int t);
 

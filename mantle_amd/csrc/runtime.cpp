@@ -63,6 +63,8 @@ struct mantleHipModel {
     int vt_stride = 0;
     int v_rows = 0;  // per layer and kv column: max_ctx or vt_stride
     int kv_f16 = 0;  // caches hold Mantle's truncating f16 (--cache-type-k/v f16)
+    int kv_q8 = 0;   // caches hold int8 rows, one scale per position (--cache-type-k/v q8_0)
+    float *k_scale = nullptr, *v_scale = nullptr;  // q8_0: [layer][max_ctx]
     float *rope_cos = nullptr, *rope_sin = nullptr;
     DecodeState* state = nullptr;
     int* prompt = nullptr;
@@ -72,10 +74,48 @@ struct mantleHipModel {
     hipGraphExec_t graph = nullptr;
 };
 
-// Layer l's base in a KV cache of `rows` keys per kv column (f32 or f16 elements).
+// Layer l's base in a KV cache of `rows` keys per kv column (f32, f16 or int8 elements).
 static float* layer_cache(const mantleHipModel* m, float* base, int l, int rows) {
     const size_t elems = (size_t)l * rows * m->kv_dim;
-    return m->kv_f16 ? reinterpret_cast<float*>(reinterpret_cast<uint16_t*>(base) + elems) : base + elems;
+    const size_t elem = m->kv_q8 ? 1 : (m->kv_f16 ? 2 : 4);
+    return reinterpret_cast<float*>(reinterpret_cast<char*>(base) + elems * elem);
+}
+
+// The layer's KV cache in the attention arguments; a q8_0 cache first gets the
+// step's prepared K / V rows from launch_kv_append_q8 (the attention launch
+// then prepares q only and reads the step's rows from the cache).
+static hipError_t attention_cache(const mantleHipModel* m, int l, AttnArgs& a, hipStream_t s) {
+    const mantleHipQwen3Config& c = m->cfg;
+    a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx);
+    a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows);
+    a.kv_f16 = m->kv_f16;
+    a.vt_stride = m->vt_stride;
+    a.kv_stride = c.head_dim;                 // head-major cache:
+    a.head_stride = m->max_ctx * c.head_dim;  // [layer][kv_head][max_ctx][head_dim]
+    if (!m->kv_q8) return hipSuccess;
+    a.kv_q8 = 1;
+    a.k_scale = m->k_scale + (size_t)l * m->max_ctx;
+    a.v_scale = m->v_scale + (size_t)l * m->max_ctx;
+    KvQ8Args q{};
+    q.k = a.k;
+    q.v = a.v;
+    q.k_norm = a.k_norm;
+    q.rope_cos = a.rope_cos;
+    q.rope_sin = a.rope_sin;
+    q.pos_dev = a.pos_dev;
+    q.eps = a.eps;
+    q.isa = a.isa;
+    q.kv_heads = c.n_kv_heads;
+    q.head_dim = c.head_dim;
+    q.cache_k = reinterpret_cast<int8_t*>(a.cache_k);
+    q.cache_v = reinterpret_cast<int8_t*>(a.cache_v);
+    q.head_stride = a.head_stride;
+    q.row_stride = a.kv_stride;
+    q.vt_stride = a.vt_stride;
+    q.k_scale = const_cast<float*>(a.k_scale);
+    q.v_scale = const_cast<float*>(a.v_scale);
+    q.prep = 1;
+    return launch_kv_append_q8(q, s);
 }
 
 // One decode step with raw-bf16 weights: Mantle's same layer loop
@@ -112,22 +152,17 @@ static hipError_t enqueue_step_bf16(mantleHipModel* m, hipStream_t s) {
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
         a.pos_dev = &m->state->pos;
-        a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx);
-        a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows);
-        a.kv_f16 = m->kv_f16;
-        a.vt_stride = m->vt_stride;
         a.scores = m->scores;
         a.out = m->attn;
         a.n_head = c.n_heads;
         a.kv_heads = c.n_kv_heads;
         a.head_dim = c.head_dim;
-        a.kv_stride = c.head_dim;
-        a.head_stride = m->max_ctx * c.head_dim;
         a.max_ctx = m->max_ctx;
         a.scale = (float)(1.0 / sqrt((double)c.head_dim));
         a.fused = 1;
         a.isa = m->isa;
         a.counters = m->attn_counters;
+        TRY(attention_cache(m, l, a, s));
         TRY(launch_attention_decode(a, s));
         const int rd[1] = {d};
         float* xo[1] = {m->x};
@@ -180,17 +215,11 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.rope_cos = m->rope_cos;
         a.rope_sin = m->rope_sin;
         a.pos_dev = &m->state->pos;
-        a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx);
-        a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows);
-        a.kv_f16 = m->kv_f16;
-        a.vt_stride = m->vt_stride;
         a.scores = m->scores;
         a.out = m->attn;
         a.n_head = c.n_heads;
         a.kv_heads = c.n_kv_heads;
         a.head_dim = c.head_dim;
-        a.kv_stride = c.head_dim;                          // head-major cache:
-        a.head_stride = m->max_ctx * c.head_dim;           // [layer][kv_head][max_ctx][head_dim]
         a.max_ctx = m->max_ctx;
         a.scale = (float)(1.0 / sqrt((double)c.head_dim));  // attn.go:311-314
         a.fused = 1;
@@ -199,6 +228,7 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.q_out = qattn ? m->qx : nullptr;
         a.q_scale = qattn ? m->xs : nullptr;
         a.counters = m->attn_counters;
+        TRY(attention_cache(m, l, a, s));
         TRY(launch_attention_decode(a, s));
         // attn.go:417 Wo on the re-quantised attention output (quantised by the
         // attention kernel), residual folded in
@@ -277,7 +307,7 @@ static void free_model(mantleHipModel* m) {
     if (!m) return;
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->attn_counters, m->xn, m->up, m->qx, m->xs, m->cache_k,
-                    m->cache_v, m->rope_cos, m->rope_sin, m->state, m->prompt, m->out_tokens};
+                    m->cache_v, m->k_scale, m->v_scale, m->rope_cos, m->rope_sin, m->state, m->prompt, m->out_tokens};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (m->stream) (void)hipStreamDestroy(m->stream);
@@ -493,18 +523,33 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     const size_t kv_elems = (size_t)c.n_layers * max_ctx * m->kv_dim;
     const int apath = attention_path();
     const bool split = (c.head_dim == 64 || c.head_dim == 128) && (apath == kAttnPathSplit || apath == kAttnPathFused);
-    m->vt_stride = split ? (max_ctx + 3) / 4 * 4 : 0;
-    m->v_rows = split ? m->vt_stride : max_ctx;
-    const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
-    m->kv_f16 = kv_cache_type() == 1;
-    if (m->kv_f16 && !split) {
-        fprintf(stderr, "mantle_hip: the f16 KV cache needs head_dim 64/128 and a split attention path\n");
+    m->kv_f16 = kv_cache_type() == kKvF16;
+    m->kv_q8 = kv_cache_type() == kKvQ8;
+    if ((m->kv_f16 || m->kv_q8) && !split) {
+        fprintf(stderr, "mantle_hip: the f16 / q8_0 KV cache needs head_dim 64/128 and a split attention path\n");
         free_model(m);
         return hipErrorInvalidValue;
     }
-    const size_t kv_elem = m->kv_f16 ? 2 : 4;
+    if (m->kv_q8 && (max_ctx > 32768 || m->kv_dim > kKvQ8MaxRow)) {
+        fprintf(stderr, "mantle_hip: the q8_0 KV cache supports up to 32768 positions and %d values per row\n",
+                kKvQ8MaxRow);
+        free_model(m);
+        return hipErrorInvalidValue;
+    }
+    // transposed V: a column's keys padded to 16 bytes (4 fp32, 8 f16, 16 int8 keys)
+    const int vt_pad = m->kv_q8 ? 16 : 4;
+    m->vt_stride = split ? (max_ctx + vt_pad - 1) / vt_pad * vt_pad : 0;
+    m->v_rows = split ? m->vt_stride : max_ctx;
+    const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
+    const size_t kv_elem = m->kv_q8 ? 1 : (m->kv_f16 ? 2 : 4);
     CHECK(hipMalloc((void**)&m->cache_k, kv_elem * kv_elems));
     CHECK(hipMalloc((void**)&m->cache_v, kv_elem * v_elems));
+    if (m->kv_q8) {
+        CHECK(hipMalloc((void**)&m->k_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
+        CHECK(hipMalloc((void**)&m->v_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
+        CHECK(hipMemset(m->k_scale, 0, sizeof(float) * (size_t)c.n_layers * max_ctx));
+        CHECK(hipMemset(m->v_scale, 0, sizeof(float) * (size_t)c.n_layers * max_ctx));
+    }
     CHECK(hipMalloc((void**)&m->state, sizeof(DecodeState)));
     CHECK(hipMalloc((void**)&m->prompt, sizeof(int) * max_ctx));
     CHECK(hipMalloc((void**)&m->out_tokens, sizeof(int) * max_ctx));

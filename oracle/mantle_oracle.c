@@ -590,6 +590,77 @@ void mo_attn_heads_f16(const float* q, const uint16_t* ck, const uint16_t* cv, f
     }
 }
 
+/* internal/backend/simd/ops_runtime.go:132-168 storeQ8: maxAbs over the whole
+ * row by comparisons; zero row -> scale 0 and zeros; scale = maxAbs / 127,
+ * inv = 127 / maxAbs (both float32 divisions); q = int32(v*inv + 0.5), or
+ * int32(v*inv - 0.5) for v < 0 (Go does not fuse these: GOAMD64=v1), clamped
+ * to +-127.  Go's float32 -> int32 on amd64 is CVTTSS2SL: truncation toward
+ * zero, INT32_MIN for NaN or out-of-range values (then clamped to -127). */
+static int32_t go_f32_to_i32_amd64(float r) {
+    if (!(r >= -2147483648.0f && r < 2147483648.0f)) return INT32_MIN;
+    return (int32_t)r;
+}
+
+void mo_store_q8(const float* src, int8_t* dst, float* scale_out, int64_t n) {
+    float max_abs = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        float v = src[i];
+        if (v < 0) {
+            if (-v > max_abs) max_abs = -v;
+        } else if (v > max_abs) {
+            max_abs = v;
+        }
+    }
+    if (max_abs == 0.0f) {
+        *scale_out = 0.0f;
+        for (int64_t i = 0; i < n; i++) dst[i] = 0;
+        return;
+    }
+    *scale_out = max_abs / 127.0f;
+    float inv = 127.0f / max_abs;
+    for (int64_t i = 0; i < n; i++) {
+        float v = src[i];
+        float t = v * inv;
+        float r = v < 0 ? t - 0.5f : t + 0.5f;
+        int32_t q = go_f32_to_i32_amd64(r);
+        if (q > 127) q = 127;
+        else if (q < -127) q = -127;
+        dst[i] = (int8_t)q;
+    }
+}
+
+/* internal/backend/simd/attnpool.go:100-102 (DotQ8, ops.go:240-246: scalar
+ * sum += a*float32(b), then sum*scale; times ctx.Scale) and :122-130 (sum +=
+ * scores[t] * float32(q) * scale[t], evaluated left to right). */
+void mo_attn_heads_q8(const float* q, const int8_t* ck, const int8_t* cv, const float* ks, const float* vs,
+                      float* out, int pos, int start, int kv_stride, int head_dim, int n_head, int kv_heads,
+                      float scale) {
+    int win = pos - start + 1;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int h = 0; h < n_head; h++) {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)win);
+        int kvh = h * kv_heads / n_head;
+        const float* qh = q + (int64_t)h * head_dim;
+        for (int t = start; t <= pos; t++) {
+            const int8_t* kt = ck + (int64_t)t * kv_stride + (int64_t)kvh * head_dim;
+            float sum = 0.0f;
+            for (int i = 0; i < head_dim; i++) sum += qh[i] * (float)kt[i];
+            float dq = sum * ks[t];
+            scores[t - start] = dq * scale;
+        }
+        mo_softmax(scores, win);
+        for (int d = 0; d < head_dim; d++) {
+            float sum = 0.0f;
+            for (int t = start; t <= pos; t++) {
+                float pq = scores[t - start] * (float)cv[(int64_t)t * kv_stride + (int64_t)kvh * head_dim + d];
+                sum += pq * vs[t];
+            }
+            out[(int64_t)h * head_dim + d] = sum;
+        }
+        free(scores);
+    }
+}
+
 /* internal/backend/simd/runtime_greedy.go:70-82 (argmaxHost: strict '>'). */
 int64_t mo_argmax(const float* x, int64_t n) {
     if (n <= 0) return -1;
@@ -694,6 +765,7 @@ struct mo_model {
     int64_t q_dim, kv_dim;
     float *x, *tmp, *q, *k, *v, *attn, *proj, *up, *gate, *act, *down, *logits;
     float *cache_k, *cache_v; /* [L][max_ctx][kv_dim] */
+    float *kscale, *vscale;   /* q8_0: [L][max_ctx] */
     float *cosv, *sinv;
     int8_t* qx;
     float* qs;
@@ -725,6 +797,8 @@ mo_model* mo_model_create(const mo_config* cfg, const mo_weights* w, int max_ctx
     /* f32 cache, or (kv_f16) uint16 f16 values in the same [L][max_ctx][kv_dim] slots */
     m->cache_k = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx * m->kv_dim), 4);
     m->cache_v = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx * m->kv_dim), 4);
+    m->kscale = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx), 4);
+    m->vscale = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx), 4);
     m->cosv = calloc((size_t)cfg->head_dim, 4);
     m->sinv = calloc((size_t)cfg->head_dim, 4);
     m->qx = calloc((size_t)((big + 31) / 32 * 32), 1);
@@ -737,7 +811,7 @@ void mo_model_free(mo_model* m) {
     if (!m) return;
     free(m->x); free(m->tmp); free(m->q); free(m->k); free(m->v); free(m->attn);
     free(m->proj); free(m->up); free(m->gate); free(m->act); free(m->down); free(m->logits);
-    free(m->cache_k); free(m->cache_v); free(m->cosv); free(m->sinv); free(m->qx); free(m->qs);
+    free(m->cache_k); free(m->cache_v); free(m->kscale); free(m->vscale); free(m->cosv); free(m->sinv); free(m->qx); free(m->qs);
     free(m);
 }
 
@@ -798,7 +872,16 @@ int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
         /* ops_runtime.go:40-131 StoreKV + RunAttnHeads */
         float* ck = m->cache_k + (int64_t)l * m->max_ctx * m->kv_dim;
         float* cv = m->cache_v + (int64_t)l * m->max_ctx * m->kv_dim;
-        if (c->kv_f16) {  /* loader.go:645-663 --cache-type-k/v f16 */
+        if (c->kv_q8) {  /* loader.go:645-663 --cache-type-k/v q8_0; ops_runtime.go:112-131 */
+            int8_t* ck8 = (int8_t*)ck;
+            int8_t* cv8 = (int8_t*)cv;
+            float* ks = m->kscale + (int64_t)l * m->max_ctx;
+            float* vs = m->vscale + (int64_t)l * m->max_ctx;
+            mo_store_q8(m->k, ck8 + (int64_t)pos * m->kv_dim, ks + pos, m->kv_dim);
+            mo_store_q8(m->v, cv8 + (int64_t)pos * m->kv_dim, vs + pos, m->kv_dim);
+            mo_attn_heads_q8(m->q, ck8, cv8, ks, vs, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads,
+                             c->n_kv_heads, scale);
+        } else if (c->kv_f16) {  /* loader.go:645-663 --cache-type-k/v f16 */
             uint16_t* ck16 = (uint16_t*)ck;
             uint16_t* cv16 = (uint16_t*)cv;
             for (int64_t i = 0; i < m->kv_dim; i++) {

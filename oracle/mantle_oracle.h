@@ -80,6 +80,13 @@ void mo_attn_heads(int isa, const float* q, const float* cache_k, const float* c
 /* The same over an f16 cache [pos][kv_stride] (DotF16 is scalar in every ISA). */
 void mo_attn_heads_f16(const float* q, const uint16_t* cache_k, const uint16_t* cache_v, float* out, int pos, int start,
                        int kv_stride, int head_dim, int n_head, int kv_heads, float scale);
+/* q8_0 cache (--cache-type-k/v q8_0): storeQ8 of one row of n values (one
+ * scale per row), and the attention over int8 caches [pos][kv_stride] with
+ * per-position scales (DotQ8 scalar order, V terms (p * q) * s). */
+void mo_store_q8(const float* src, int8_t* dst, float* scale_out, int64_t n);
+void mo_attn_heads_q8(const float* q, const int8_t* cache_k, const int8_t* cache_v, const float* k_scale,
+                      const float* v_scale, float* out, int pos, int start, int kv_stride, int head_dim, int n_head,
+                      int kv_heads, float scale);
 int64_t mo_argmax(const float* x, int64_t n);
 
 /* ---- Qwen3-shaped decoder (k4 weights, f32 KV cache) ---- */
@@ -90,6 +97,7 @@ typedef struct {
     int isa;
     int wdtype; /* MO_W_K4: the matrix pointers below are k4 payloads; MO_W_BF16: bf16 [rows][cols] */
     int kv_f16; /* KV cache in Mantle's f16 (--cache-type-k/v f16) instead of f32 */
+    int kv_q8;  /* KV cache in Mantle's q8_0 (--cache-type-k/v q8_0) instead of f32 */
 } mo_config;
 enum { MO_W_K4 = 0, MO_W_BF16 = 1 };
 

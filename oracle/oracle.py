@@ -24,7 +24,8 @@ F = C.c_float
 
 class Config(C.Structure):
     _fields_ = [("n_layers", I), ("d_model", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I), ("ffn", I),
-                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I), ("kv_f16", I)]
+                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I), ("kv_f16", I),
+                ("kv_q8", I)]
 
 
 class Weights(C.Structure):
@@ -56,6 +57,8 @@ _SIGS = {
     "mo_apply_rope": (None, [P, I, I, I, P, P]),
     "mo_attn_heads": (None, [I, P, P, P, P, I, I, I, I, I, I, F]),
     "mo_attn_heads_f16": (None, [P, P, P, P, I, I, I, I, I, I, F]),
+    "mo_store_q8": (None, [P, P, P, C.c_int64]),
+    "mo_attn_heads_q8": (None, [P, P, P, P, P, P, I, I, I, I, I, I, F]),
     "mo_argmax": (I64, [P, I64]),
     "mo_model_create": (P, [C.POINTER(Config), C.POINTER(Weights), I]),
     "mo_model_free": (None, [P]),
@@ -251,6 +254,28 @@ def attn_heads_f16(q, cache_k16, cache_v16, pos: int, kv_stride: int, head_dim: 
     return out
 
 
+def store_q8(src):
+    """storeQ8 (ops_runtime.go:132-168) of one row: (int8 row, its scale)."""
+    src = _f32(src)
+    dst = np.empty(len(src), dtype=np.int8)
+    sc = np.zeros(1, dtype=np.float32)
+    lib().mo_store_q8(_ptr(src), _ptr(dst), _ptr(sc), len(src))
+    return dst, float(sc[0])
+
+
+def attn_heads_q8(q, cache_k8, cache_v8, k_scale, v_scale, pos: int, kv_stride: int, head_dim: int, n_head: int,
+                  kv_heads: int, scale: float) -> np.ndarray:
+    """RunAttnHeads over a q8_0 cache (attnpool.go:100-102, :122-130): int8 [pos+1][kv_stride], scales [pos+1]."""
+    q = _f32(q)
+    ck = np.ascontiguousarray(cache_k8, dtype=np.int8)
+    cv = np.ascontiguousarray(cache_v8, dtype=np.int8)
+    ks, vs = _f32(k_scale), _f32(v_scale)
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    lib().mo_attn_heads_q8(_ptr(q), _ptr(ck), _ptr(cv), _ptr(ks), _ptr(vs), _ptr(out), int(pos), 0, int(kv_stride),
+                           int(head_dim), int(n_head), int(kv_heads), float(scale))
+    return out
+
+
 def argmax(x) -> int:
     x = _f32(x)
     return int(lib().mo_argmax(_ptr(x), len(x)))
@@ -259,7 +284,7 @@ def argmax(x) -> int:
 class Model:
     """Qwen3-shaped decoder on the CPU (the greedy-token oracle), k4 weights or,
     with cfg["weights"] == "bf16", bf16 ones; cfg["kv_cache"] == "f16" stores the
-    KV cache in Mantle's truncating f16.
+    KV cache in Mantle's truncating f16, "q8_0" as int8 rows with one scale each.
 
     `tensors(name) -> np.uint8 payload / np.float32 gains` supplies the weights
     (e.g. views into an MCF file); they must outlive the model.
@@ -294,7 +319,7 @@ class Model:
             setattr(w, field, arr([lname(l, suffix) for l in range(L)]))
         c = Config(cfg["n_layers"], cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"],
                    cfg["vocab"], cfg["rope_base"], cfg["eps"], isa, 1 if cfg.get("weights") == "bf16" else 0,
-                   1 if cfg.get("kv_cache") == "f16" else 0)
+                   1 if cfg.get("kv_cache") == "f16" else 0, 1 if cfg.get("kv_cache") == "q8_0" else 0)
         self._keep = keep
         self._w = w
         self._c = c

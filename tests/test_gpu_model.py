@@ -94,6 +94,30 @@ def test_lane_f16_kv_cache_bitexact(hip, lane_path, path):
         _lib.call("mantleHipSetAttentionPath", 0)
 
 
+@pytest.mark.parametrize("path", ["split", "fused"])
+def test_lane_q8_kv_cache_bitexact(hip, lane_path, path):
+    """--cache-type-k/v q8_0 (loader.go:645-663): 400 steps (the transposed int8
+    V ring wraps past 320 keys; 420 positions pad to 432 per column), logits
+    bit-identical to the oracle's q8_0-cache decode on both split settings
+    (both take the two-launch form with a separate append)."""
+    import mantle_amd
+    from mantle_amd import _lib
+    _lib.call("mantleHipSetAttentionPath", {"split": 0, "fused": 3}[path])
+    try:
+        rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=420, kv_cache="q8_0")
+        om = models.oracle_model(lane_path, dict(models.LANE, kv_cache="q8_0"), 420)
+        toks = models.prompt(400, models.LANE["vocab"], 8)
+        for step, tok in enumerate(toks):
+            logits = rt.forward_token(tok)
+            _, want = om.forward_greedy(tok, want_logits=True)
+            if step % 25 == 24 or step < 3 or step == len(toks) - 1:
+                np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+        rt.close()
+        om.close()
+    finally:
+        _lib.call("mantleHipSetAttentionPath", 0)
+
+
 @pytest.mark.parametrize("path", ["fused", "split", "single", "general"])
 def test_lane_long_context_attention_paths(hip, lane_path, path):
     """140 fused steps (past two 64-key chunks, the step's own K/V row inside
@@ -169,11 +193,11 @@ def test_context_limit_and_bad_token(hip, tiny_path):
         rt.close()
 
 
-@pytest.mark.parametrize("kv_cache", ["f32", "f16"])
+@pytest.mark.parametrize("kv_cache", ["f32", "f16", "q8_0"])
 def test_qwen3_0_6b_first_64_tokens(hip, tmp_models, kv_cache):
     """Qwen3-0.6B shape, weights seed 0, 31-token prompt seed 1:
     the first 64 greedy tokens equal the CPU oracle's, with Mantle's f32 cache
-    (the loader default) and its f16 cache (`mantle run`'s default)."""
+    (the loader default), its f16 cache (`mantle run`'s default) and q8_0."""
     import mantle_amd
     from mantle_amd.mcf import QWEN3_0_6B
     from oracle import oracle as o

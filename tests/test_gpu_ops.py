@@ -216,3 +216,82 @@ def test_store_kv_f16_row_truncates(hip, oracle):
     g.call("mantleHipStoreKVF16Row", g.ptr(cache), g.ptr(g.keep(vals)), 2, kv, g.stream())
     got = g.host(cache).view(np.uint16)[2 * kv:]
     np.testing.assert_array_equal(got, _f16(oracle, vals))
+
+
+# storeQ8 known answers (ops_runtime.go:132-168), as the oracle tests pin them:
+# +-0.5 then truncation (0.49999997 + 0.5 rounds to 1.0 in fp32), a zero row,
+# and a row whose 127/maxAbs overflows (amd64's NaN / out-of-range -> -127).
+Q8_ROWS = [
+    np.array([127.0, 2.5, -2.5, 0.49999997, -0.49999997, 1.5, 126.5, -127.0] * 2, np.float32),
+    np.zeros(16, np.float32),
+    np.array([1e-38, 0.0, -1e-38, 5e-39] * 4, np.float32),
+]
+
+
+@pytest.mark.parametrize("case", ["kat0", "kat1", "kat2", "rand1024", "rand4096", "rand48"])
+def test_store_kv_q8_row_bitexact(hip, oracle, case):
+    if case.startswith("kat"):
+        k = Q8_ROWS[int(case[3:])]
+        v = k[::-1].copy()
+    else:
+        n = int(case[4:])
+        rng = np.random.default_rng(n)
+        k = (rng.standard_normal(n) * 3).astype(np.float32)
+        v = rng.standard_normal(n).astype(np.float32)
+    kv, pos = k.size, 3
+    ck = g.empty(5 * kv, torch.int8)
+    cv = g.empty(5 * kv, torch.int8)
+    ks = g.empty(5)
+    vs = g.empty(5)
+    g.call("mantleHipStoreKVQ8Row", g.ptr(ck), g.ptr(cv), g.ptr(ks), g.ptr(vs), g.ptr(g.keep(k)), g.ptr(g.keep(v)),
+           pos, kv, g.stream())
+    for dev, sc, src, name in ((ck, ks, k, "K"), (cv, vs, v, "V")):
+        want_q, want_s = oracle.store_q8(src)
+        np.testing.assert_array_equal(g.host(dev)[pos * kv:(pos + 1) * kv], want_q, err_msg=f"{case} {name} row")
+        assert np.float32(g.host(sc)[pos]).view(np.uint32) == np.float32(want_s).view(np.uint32), f"{case} {name} scale"
+
+
+@pytest.mark.parametrize("path", ["split", "fused"])
+@pytest.mark.parametrize("n_head,kv_heads,head_dim,pos", [(16, 8, 128, 0), (16, 8, 128, 130), (32, 8, 128, 1100),
+                                                         (8, 2, 64, 300), (16, 8, 128, 5000)])
+def test_attention_q8_cache_bitexact(hip, oracle, path, n_head, kv_heads, head_dim, pos):
+    """RunAttnHeads over the q8_0 cache (attnpool.go:100-102, :122-130): DotQ8 in
+    the scalar order times the key's scale, V terms (p * q) * s in key order;
+    rows written by storeQ8 (one scale per position over all kv heads)."""
+    kv = kv_heads * head_dim
+    rng = np.random.default_rng(pos + 11)
+    q = rng.standard_normal(n_head * head_dim).astype(np.float32)
+    ck = np.empty((pos + 1) * kv, np.int8)
+    cv = np.empty((pos + 1) * kv, np.int8)
+    ks = np.empty(pos + 1, np.float32)
+    vs = np.empty(pos + 1, np.float32)
+    for t in range(pos + 1):
+        ck[t * kv:(t + 1) * kv], ks[t] = oracle.store_q8(rng.standard_normal(kv) * (1 + t % 7))
+        cv[t * kv:(t + 1) * kv], vs[t] = oracle.store_q8(rng.standard_normal(kv))
+    scale = np.float32(1.0 / np.sqrt(head_dim))
+    g.call("mantleHipSetAttentionPath", ATTN_PATHS[path])
+    try:
+        out = g.empty(n_head * head_dim)
+        scratch = g.empty(n_head * (pos + 1))
+        g.call("mantleHipAttentionInnerQ8CacheF32", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)),
+               g.ptr(g.keep(ks)), g.ptr(g.keep(vs)), g.ptr(out), g.ptr(scratch), pos, 0, kv, head_dim, n_head,
+               kv_heads, pos + 1, ctypes.c_float(scale), g.stream())
+        got = g.host(out)
+    finally:
+        g.call("mantleHipSetAttentionPath", 0)
+    g.assert_bitexact(got, oracle.attn_heads_q8(q, ck, cv, ks, vs, pos, kv, head_dim, n_head, kv_heads, float(scale)),
+                      "q8 attention")
+
+
+def test_attention_q8_cache_rejects_unsupported(hip):
+    """The q8_0 cache needs head_dim 64/128 (the split kernels) and 16-byte rows."""
+    q = np.zeros(16 * 96, np.float32)
+    c = np.zeros(4 * 8 * 96, np.int8)
+    s = np.zeros(4, np.float32)
+    out = g.empty(16 * 96)
+    scratch = g.empty(16 * 4)
+    from mantle_amd import _lib
+    rc = _lib.lib().mantleHipAttentionInnerQ8CacheF32(g.ptr(g.keep(q)), g.ptr(g.keep(c)), g.ptr(g.keep(c)),
+                                                      g.ptr(g.keep(s)), g.ptr(g.keep(s)), g.ptr(out), g.ptr(scratch),
+                                                      3, 0, 8 * 96, 96, 16, 8, 4, ctypes.c_float(0.1), g.stream())
+    assert rc != 0

@@ -430,3 +430,102 @@ def test_attn_f16_vs_float64():
         p /= p.sum()
         want[h * hd:(h + 1) * hd] = p @ vf[:, g]
     np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- q8_0 KV cache ----
+# internal/backend/simd/ops_runtime.go:132-168 (storeQ8), attnpool.go:100-102, :122-130.
+
+def test_store_q8_kat():
+    """Worked by hand.  Row maxAbs 2: scale = 2/127, inv = 63.5, so 1 -> 63.5 + 0.5
+    = 64; -0.5 -> -31.75 - 0.5 = -32.25 -> -32 (truncation); 0.25 -> 16.375 -> 16;
+    2 -> 127.5 -> 127; -2 -> -127.  Row maxAbs 127 (inv 1): 2.5 -> 3 and -2.5 -> -3
+    (half away from zero); 0.49999997 (= 0.5 - 2^-25) + 0.5 is 1 - 2^-25, a tie
+    in fp32 that rounds to even 1.0, so it stores 1 where round() would give 0;
+    126.5 -> 127; 1.5 -> 2."""
+    q, s = o.store_q8(np.array([1.0, -0.5, 0.25, 2.0, -2.0, 0.0], np.float32))
+    assert q.tolist() == [64, -32, 16, 127, -127, 0]
+    assert np.float32(s) == np.float32(2.0) / np.float32(127.0)
+    q, s = o.store_q8(np.array([127.0, 2.5, -2.5, 0.49999997, -0.49999997, 126.5, 1.5], np.float32))
+    assert q.tolist() == [127, 3, -3, 1, -1, 127, 2]
+    assert s == 1.0
+
+
+def test_store_q8_zero_and_overflow_rows():
+    """A zero row stores scale 0 and zeros (ops_runtime.go:147-153).  A row whose
+    maxAbs is below 127 / FLT_MAX makes inv = 127/maxAbs overflow to +Inf: every
+    v*inv is +-Inf or NaN (0 * Inf), which Go's float32 -> int32 on amd64
+    (CVTTSS2SL) turns into INT32_MIN, clamped to -127 -- for every element."""
+    q, s = o.store_q8(np.zeros(32, np.float32))
+    assert s == 0.0 and not q.any()
+    q, s = o.store_q8(np.array([1e-38, 0.0, -1e-38, 5e-39], np.float32))
+    assert q.tolist() == [-127] * 4
+    assert np.float32(s) == np.float32(1e-38) / np.float32(127.0)
+
+
+def test_store_q8_round_trip_bound():
+    """|q*scale - x| <= scale/2 (+ an ulp) for every element, and the row's
+    largest element maps to +-127."""
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal(1024) * 5).astype(np.float32)
+    q, s = o.store_q8(x)
+    err = np.abs(q.astype(np.float64) * s - x)
+    assert err.max() <= s * 0.5 * (1 + 1e-5)
+    assert abs(int(q[np.argmax(np.abs(x))])) == 127
+
+
+def test_attn_q8_single_key_closed_form():
+    """pos 0: the softmax of one score is exactly 1, so out = (1 * q_v) * s_v
+    exactly, per head, from kv head h * kv_heads / n_head."""
+    nh, kvh, hd = 4, 2, 64
+    kv = kvh * hd
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k8 = rng.integers(-127, 128, kv).astype(np.int8)
+    v8 = rng.integers(-127, 128, kv).astype(np.int8)
+    ks, vs = np.float32([0.03]), np.float32([0.0625])
+    got = o.attn_heads_q8(q, k8, v8, ks, vs, 0, kv, hd, nh, kvh, 0.125)
+    for h in range(nh):
+        g = h * kvh // nh
+        np.testing.assert_array_equal(got[h * hd:(h + 1) * hd], v8[g * hd:(g + 1) * hd].astype(np.float32) * vs[0])
+
+
+def test_attn_q8_dot_order_closed_form():
+    """Worked by hand as for DotF16 (hd 128, one head): q_0 = 2^24, q_64 = -2^24,
+    q_1..63 = 1; key 0 = all ones (scale 1), key 1 = all zeros; V rows 1 and 0
+    (scale 1).  DotQ8's scalar sum loses every +1 against 2^24 and cancels to 0,
+    so both scores are 0, p = 0.5 each, out = 0.5."""
+    hd = 128
+    q = np.zeros(hd, np.float32)
+    q[0], q[64], q[1:64] = 2.0 ** 24, -2.0 ** 24, 1.0
+    k8 = np.concatenate([np.ones(hd, np.int8), np.zeros(hd, np.int8)])
+    v8 = k8.copy()
+    one = np.ones(2, np.float32)
+    got = o.attn_heads_q8(q, k8, v8, one, one, 1, hd, hd, 1, 1, 1.0)
+    np.testing.assert_array_equal(got, np.full(hd, 0.5, np.float32))
+
+
+def test_attn_q8_vs_float64():
+    """attn_test.go:10-86's tolerance (1e-5) against float64 softmax attention over
+    the dequantised cache (q * scale per position)."""
+    rng = np.random.default_rng(14)
+    nh, kvh, hd, pos = 8, 2, 128, 300
+    kv = kvh * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k8 = np.empty((pos + 1, kv), np.int8)
+    v8 = np.empty((pos + 1, kv), np.int8)
+    ks = np.empty(pos + 1, np.float32)
+    vs = np.empty(pos + 1, np.float32)
+    for t in range(pos + 1):
+        k8[t], ks[t] = o.store_q8(rng.standard_normal(kv))
+        v8[t], vs[t] = o.store_q8(rng.standard_normal(kv))
+    got = o.attn_heads_q8(q, k8, v8, ks, vs, pos, kv, hd, nh, kvh, float(1 / np.sqrt(hd)))
+    kf = (k8.astype(np.float64) * ks[:, None]).reshape(pos + 1, kvh, hd)
+    vf = (v8.astype(np.float64) * vs[:, None]).reshape(pos + 1, kvh, hd)
+    want = np.empty(nh * hd)
+    for h in range(nh):
+        g = h * kvh // nh
+        s = kf[:, g] @ q[h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        want[h * hd:(h + 1) * hd] = p @ vf[:, g]
+    np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-5)
