@@ -29,6 +29,16 @@ COMMON = [
 ]
 
 
+# Per-source flags.  attention.hip runs with f16 (and f64) denormals flushed:
+# its f16 KV cache reads convert with v_cvt_f32_f16, which then flushes
+# subnormal inputs to signed zero as Mantle's Float16ToFloat32 does; fp32 stays
+# IEEE (denormals kept) like everywhere else.
+EXTRA = {
+    "attention.hip": ["-fdenormal-fp-math=preserve-sign", "-Xclang", "-fdenormal-fp-math-f32=ieee",
+                      "-DMANTLE_F16_INPUT_FTZ=1"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
         if cand and (os.path.isabs(cand) and os.path.exists(cand) or not os.path.isabs(cand)):
@@ -38,7 +48,7 @@ def hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, src + ".o")
-    cmd = [hipcc(), *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *COMMON, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".hip"):
         cmd.insert(1, "-xhip")
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -22,7 +22,18 @@
 #include "phase_trace.h"
 #include "quant_device.h"
 
+#if !MANTLE_F16_INPUT_FTZ
+#error "attention.hip needs f16 denormal flushing: -fdenormal-fp-math=preserve-sign -Xclang -fdenormal-fp-math-f32=ieee"
+#endif
+
 namespace mantle {
+
+// An f16 KV cache element as Mantle reads it (Float16ToFloat32,
+// internal/backend/core/float16.go:42-64: subnormals flush to signed zero).
+// This file is compiled with f16 denormals flushed, so the hardware
+// conversion alone does it (one instruction per element on the V-sum chain
+// wave, against three for an explicit compare and select).
+__device__ __forceinline__ float f16_cache_load(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
 static constexpr int kAttnKeys = 64;          // keys staged in LDS per chunk (head_dim <= 128)
 static constexpr int kAttnLdsScores = 4096;    // contexts up to this keep scores in LDS
@@ -390,10 +401,10 @@ __device__ __forceinline__ void chunk_store16(const ChunkRegs16& c, float* dst, 
         const int o = c.off[j];
         if (o < 0) continue;
         f32x4 v;
-        v.x = f16_cache_value((uint16_t)(c.r[j].x & 0xFFFFu));
-        v.y = f16_cache_value((uint16_t)(c.r[j].x >> 16));
-        v.z = f16_cache_value((uint16_t)(c.r[j].y & 0xFFFFu));
-        v.w = f16_cache_value((uint16_t)(c.r[j].y >> 16));
+        v.x = f16_cache_load((uint16_t)(c.r[j].x & 0xFFFFu));
+        v.y = f16_cache_load((uint16_t)(c.r[j].x >> 16));
+        v.z = f16_cache_load((uint16_t)(c.r[j].y & 0xFFFFu));
+        v.w = f16_cache_load((uint16_t)(c.r[j].y >> 16));
         *reinterpret_cast<f32x4*>(dst + o) = v;
     }
     // the step's own row: `cur` already holds its f16-rounded values
@@ -409,7 +420,22 @@ struct ChunkRegs8 {
     int off[2];
 };
 
-__device__ __forceinline__ float q8_byte(uint32_t w, int c) { return (float)(int8_t)(uint8_t)(w >> (8 * c)); }
+// Byte C of w, sign-extended, as fp32 in one instruction (SDWA byte select).
+// Spelled out so that the compiler keeps the raw words and converts at the
+// use, instead of splitting them into one register per byte ahead of it.
+template <int C>
+__device__ __forceinline__ float q8_byte_sdwa(uint32_t w) {
+    float r;
+    if constexpr (C == 0)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (C == 1)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (C == 2)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
 
 template <int HD>
 __device__ __forceinline__ void chunk_issue8_t(ChunkRegs8& c, const int8_t* __restrict__ base, int stride, int t0,
@@ -437,10 +463,10 @@ __device__ __forceinline__ void chunk_store8(const ChunkRegs8& c, float* dst) {
         for (int w = 0; w < 4; w++) {
             const uint32_t x = c.r[j][w];
             f32x4 v;
-            v.x = q8_byte(x, 0);
-            v.y = q8_byte(x, 1);
-            v.z = q8_byte(x, 2);
-            v.w = q8_byte(x, 3);
+            v.x = q8_byte_sdwa<0>(x);
+            v.y = q8_byte_sdwa<1>(x);
+            v.z = q8_byte_sdwa<2>(x);
+            v.w = q8_byte_sdwa<3>(x);
             *reinterpret_cast<f32x4*>(dst + o + 4 * w) = v;
         }
     }
@@ -804,6 +830,7 @@ bool set_attention_path(int path) {
 // The V-sum launch keeps the probabilities in LDS: up to 128 KiB of the 160
 // KiB a gfx950 workgroup may hold.
 static constexpr int kSplitMaxCtx = 32768;
+static constexpr size_t kMaxLds = 160 * 1024;  // dynamic LDS one gfx950 workgroup may hold
 
 // Dynamic LDS above 64 KiB is allowed per kernel before its launch.
 static hipError_t allow_lds(void (*kern)(AttnArgs), size_t bytes) {
@@ -888,10 +915,11 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
 // or 16 of int8, widened when used); otherwise one load per key (rows
 // kv_stride apart).  `own` (the fused step's V row, a workgroup of this
 // launch may still be appending it) replaces key `skip`.  KV = kKvQ8: the sum
-// is sum_t (p_t * q_t,d) * s_t (attnpool.go:122-130); lane k of the wave holds
-// the scale of key t0 + k of each group in flight, read back per key with
-// readlane.
-template <bool VT, int KV = kKvF32>
+// is sum_t (p_t * q_t,d) * s_t (attnpool.go:122-130).  The scales are the same
+// for every column: SL, they are staged in LDS beside the probabilities and
+// read the same way; otherwise lane k of the wave holds the scale of key
+// t0 + k of each group in flight, read back per key with readlane.
+template <bool VT, int KV = kKvF32, bool SL = false>
 struct VColumn {
     static constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
     // a narrow transposed ring costs fewer registers per key: twice the groups
@@ -900,7 +928,7 @@ struct VColumn {
     f32x4 r[RAW ? 1 : NG][VG / 4];  // fp32 keys (for RAW: the group being summed, slot 0)
     u32x2 h[F16 && VT ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
     u32x4 b[Q8 && VT ? NG : 1][VG / 16];  // raw int8 keys (VT) until used
-    float sr[Q8 ? NG : 1];                // Q8: per-key scales, key t0 + k in lane k
+    float sr[Q8 && !SL ? NG : 1];         // Q8 without SL: per-key scales, key t0 + k in lane k
     const float* col;
     const uint16_t* col16;
     const int8_t* col8;
@@ -939,7 +967,7 @@ struct VColumn {
     }
     __device__ __forceinline__ int vt_key(int t0, int k4) const { return t0 + 4 * k4 <= pos ? t0 + 4 * k4 : (pos & ~3); }
     __device__ __forceinline__ void issue(int g, int t0) {
-        if constexpr (Q8) {
+        if constexpr (Q8 && !SL) {
             const int tk = t0 + (int)(threadIdx.x & 31);
             sr[g] = vscale[tk <= pos ? tk : pos];
         }
@@ -976,7 +1004,7 @@ struct VColumn {
             for (int k = 0; k < VG; k++) {
                 const int t = t0 + k <= pos ? t0 + k : pos;
                 const float v = Q8 ? (float)col8[(size_t)t * step]
-                                   : (F16 ? f16_cache_value(col16[(size_t)t * step]) : col[(size_t)t * step]);
+                                   : (F16 ? f16_cache_load(col16[(size_t)t * step]) : col[(size_t)t * step]);
                 r[g][k >> 2][k & 3] = t == skip ? own : v;
             }
         }
@@ -990,10 +1018,10 @@ struct VColumn {
                 for (int w = 0; w < 4; w++) {
                     const uint32_t x = b[g][j][w];
                     f32x4 v;
-                    v.x = q8_byte(x, 0);
-                    v.y = q8_byte(x, 1);
-                    v.z = q8_byte(x, 2);
-                    v.w = q8_byte(x, 3);
+                    v.x = q8_byte_sdwa<0>(x);
+                    v.y = q8_byte_sdwa<1>(x);
+                    v.z = q8_byte_sdwa<2>(x);
+                    v.w = q8_byte_sdwa<3>(x);
                     r[0][4 * j + w] = v;
                 }
         } else if constexpr (F16 && VT) {
@@ -1001,17 +1029,19 @@ struct VColumn {
 #pragma unroll
             for (int k4 = 0; k4 < VG / 4; k4++) {
                 f32x4 v;
-                v.x = f16_cache_value((uint16_t)(h[g][k4].x & 0xFFFFu));
-                v.y = f16_cache_value((uint16_t)(h[g][k4].x >> 16));
-                v.z = f16_cache_value((uint16_t)(h[g][k4].y & 0xFFFFu));
-                v.w = f16_cache_value((uint16_t)(h[g][k4].y >> 16));
+                v.x = f16_cache_load((uint16_t)(h[g][k4].x & 0xFFFFu));
+                v.y = f16_cache_load((uint16_t)(h[g][k4].x >> 16));
+                v.z = f16_cache_load((uint16_t)(h[g][k4].y & 0xFFFFu));
+                v.w = f16_cache_load((uint16_t)(h[g][k4].y >> 16));
                 r[0][k4] = whole ? v : patch(v, vt_key(t0, k4));
             }
         }
     }
-    // Term k of group g: p * v, or for Q8 (p * q) * s.
-    __device__ __forceinline__ float term(float p, float v, int g, int k) const {
-        if constexpr (Q8) {
+    // Term k of group g: p * v, or for Q8 (p * q) * s (s: sl, the key's scale read from LDS, for SL).
+    __device__ __forceinline__ float term(float p, float v, int g, int k, float sl) const {
+        if constexpr (Q8 && SL) {
+            return (p * v) * sl;
+        } else if constexpr (Q8) {
             const float sk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sr[g]), k));
             return (p * v) * sk;
         } else {
@@ -1024,8 +1054,9 @@ struct VColumn {
         for (int g = 0; g < NG; g++)
             if (g * VG <= pos) issue(g, g * VG);
     }
-    // The ordered sum over keys 0 .. pos with probabilities p[0 .. pos].
-    __device__ __forceinline__ float sum(const float* p) {
+    // The ordered sum over keys 0 .. pos with probabilities p[0 .. pos] (and,
+    // SL, the keys' scales ls[0 .. pos]; both readable up to a multiple of VG).
+    __device__ __forceinline__ float sum(const float* p, const float* ls = nullptr) {
         float acc = 0.0f;
         for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
 #pragma unroll
@@ -1040,13 +1071,21 @@ struct VColumn {
                         const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
                         pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
                     }
+                    float sg[SL ? VG : 1];
+                    if constexpr (SL) {
+#pragma unroll
+                        for (int i4 = 0; i4 < VG / 4; i4++) {
+                            const f32x4 s4 = *reinterpret_cast<const f32x4*>(ls + t0 + 4 * i4);
+                            sg[4 * i4] = s4.x; sg[4 * i4 + 1] = s4.y; sg[4 * i4 + 2] = s4.z; sg[4 * i4 + 3] = s4.w;
+                        }
+                    }
                     if (t0 + VG <= pos + 1) {
 #pragma unroll
-                        for (int k = 0; k < VG; k++) acc = acc + term(pg[k], r[ri][k >> 2][k & 3], gi, k);
+                        for (int k = 0; k < VG; k++) acc = acc + term(pg[k], r[ri][k >> 2][k & 3], gi, k, sg[SL ? k : 0]);
                     } else {
 #pragma unroll
                         for (int k = 0; k < VG; k++) {
-                            const float nacc = acc + term(pg[k], r[ri][k >> 2][k & 3], gi, k);
+                            const float nacc = acc + term(pg[k], r[ri][k >> 2][k & 3], gi, k, sg[SL ? k : 0]);
                             acc = t0 + k <= pos ? nacc : acc;
                         }
                     }
@@ -1153,7 +1192,9 @@ __global__ __launch_bounds__(kThreads) void attention_split_fused(AttnArgs a) {
     softmax_pv_head<HD, PG, VT, KV>(a, lds, h, pos);
 }
 
-template <int HD, bool VT, int KV>
+// SL (q8_0 cache): the keys' scales are staged in LDS after the probabilities
+// (pcap + 32 floats in), by all four waves before the softmax's barriers.
+template <int HD, bool VT, int KV, bool SL = false>
 __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     constexpr int DB = 32;  // output columns per workgroup: one int8 block of the Wo activation
@@ -1169,14 +1210,17 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     // wave 0 (lanes 0-31 the columns; 32-63 shadow them) streams its V
     // columns into a register ring from the start
     const int d = db * DB + (lane & 31);
-    VColumn<VT, KV> vc;
+    VColumn<VT, KV, SL> vc;
     vc.init(a, kvh, HD, d, pos);
     vc.skip = -1;  // the previous launch appended the step's row
     if (wave == 0) vc.prime();
+    float* ls = lds + pcap + 32;
+    if constexpr (SL)
+        for (int t = tid; t <= pos; t += kThreads) ls[t] = a.v_scale[t];
     head_softmax<false>(sg, lds, lds + pcap, pos);
     PHASE(1);
     if (wave != 0) return;
-    store_attn_out(a, h * HD + d, vc.sum(lds), lane < 32);
+    store_attn_out(a, h * HD + d, vc.sum(lds, ls), lane < 32);
     PHASE(2);
 }
 
@@ -1276,10 +1320,19 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
             {attention_scores_split<128, kKvF32>, attention_scores_split<128, kKvF16>,
              attention_scores_split<128, kKvQ8>}};
         auto pvk = pv[a.head_dim == 128][vt][kvt];
-        const hipError_t e = allow_lds(pvk, smem_b);
+        size_t smem_pv = smem_b;
+        const size_t smem_sl = sizeof(float) * (2 * ((size_t)(a.max_ctx + 31) / 32 * 32) + 32);
+        if (a.kv_q8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
+            void (*const pvs[2][2])(AttnArgs) = {
+                {attention_pv_split<64, false, kKvQ8, true>, attention_pv_split<64, true, kKvQ8, true>},
+                {attention_pv_split<128, false, kKvQ8, true>, attention_pv_split<128, true, kKvQ8, true>}};
+            pvk = pvs[a.head_dim == 128][vt];
+            smem_pv = smem_sl;
+        }
+        const hipError_t e = allow_lds(pvk, smem_pv);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(sc[a.head_dim == 128][kvt], dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
-        hipLaunchKernelGGL(pvk, dim3(a.n_head * nd), dim3(kThreads), smem_b, stream, a);
+        hipLaunchKernelGGL(pvk, dim3(a.n_head * nd), dim3(kThreads), smem_pv, stream, a);
         return hipGetLastError();
     }
     if (fast_hd && mode != kAttnPathGeneral) {
