@@ -924,6 +924,13 @@ struct VColumn {
     static constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
     // a narrow transposed ring costs fewer registers per key: twice the groups
     static constexpr int VG = 32, NG = (F16 || Q8) && VT ? 10 : 5;
+    // PF: a group's probabilities are read while the group before it is
+    // summed, alternating between two register buffers (NG even).  It pays
+    // for the q8_0 sum (4B after 2k tokens 237 -> 269 tok/s); the f32 / f16
+    // sums keep their deeper V rings instead (the extra buffer cost them a
+    // ring group: 310 -> 299 tok/s).
+    static constexpr bool PF = Q8 && VT;
+    static_assert(!PF || NG % 2 == 0, "groups alternate between two probability buffers");
     static constexpr bool RAW = (F16 || Q8) && VT;
     f32x4 r[RAW ? 1 : NG][VG / 4];  // fp32 keys (for RAW: the group being summed, slot 0)
     u32x2 h[F16 && VT ? NG : 1][VG / 4];  // raw f16 keys (VT) until used
@@ -1058,19 +1065,27 @@ struct VColumn {
     // SL, the keys' scales ls[0 .. pos]; both readable up to a multiple of VG).
     __device__ __forceinline__ float sum(const float* p, const float* ls = nullptr) {
         float acc = 0.0f;
+        float pb[PF ? 2 : 1][VG];
+        auto load_p = [&](float* dst, int t0) {
+#pragma unroll
+            for (int i4 = 0; i4 < VG / 4; i4++) {
+                const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
+                dst[4 * i4] = p4.x; dst[4 * i4 + 1] = p4.y; dst[4 * i4 + 2] = p4.z; dst[4 * i4 + 3] = p4.w;
+            }
+        };
+        if constexpr (PF) load_p(pb[0], 0);
         for (int g0 = 0; g0 * VG <= pos; g0 += NG) {
 #pragma unroll
             for (int gi = 0; gi < NG; gi++) {
                 const int t0 = (g0 + gi) * VG;
                 if (t0 <= pos) {
+                    if constexpr (PF) {
+                        if (t0 + VG <= pos) load_p(pb[(gi + 1) & 1], t0 + VG);
+                    }
                     widen(gi, t0);
                     const int ri = RAW ? 0 : gi;
-                    float pg[VG];
-#pragma unroll
-                    for (int i4 = 0; i4 < VG / 4; i4++) {
-                        const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + 4 * i4);
-                        pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
-                    }
+                    if constexpr (!PF) load_p(pb[0], t0);
+                    const float* pg = pb[PF ? (gi & 1) : 0];
                     float sg[SL ? VG : 1];
                     if constexpr (SL) {
 #pragma unroll
