@@ -513,7 +513,6 @@ static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
     constexpr int C16 = piece_bpl<T16, EPI == kEpiSiluMul ? 4 : 6>();
     constexpr bool L8 = BPR % 32 == 0 && BPR / 8 <= 8;  // whole 8-lane rows (u6 words: 4k blocks per lane)
     constexpr int T8 = BPR / 8;
-    constexpr int C8 = piece_bpl<T8, 4>();
     int rows = 0;
     for (int i = 0; i < p.nmat; i++) rows += p.mats[i].rows;
     const bool q32 = EPI == kEpiSiluMul && p.q_out;
@@ -522,7 +521,10 @@ static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
         // wide gate/up rows with the quantising SiLU epilogue: 32-row units of
         // four waves at 8 lanes per row, in pieces; two such workgroups fit a
         // CU, so the 4B/8B unit counts (304, 384) run in a single round
-        if (q32) return launch_lane_gemv<EPI, 8, C8, NB, 4, PRO, 2, T8>(p, stream);
+        // (pieces of up to 5 blocks per lane: the 4B rows in two pieces of 5
+        // measured 15.9 -> 15.3 us against three of 4, 4, 2; 16 lanes per row
+        // in eight-wave workgroups: 18.9 us)
+        if (q32) return launch_lane_gemv<EPI, 8, piece_bpl<T8, 5>(), NB, 4, PRO, 2, T8>(p, stream);
     }
     // (16-lane rows make 16-row units at four waves: the quantising SiLU
     // epilogue takes the eight-wave instance below)
