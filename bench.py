@@ -113,6 +113,27 @@ def copy_calibration(nbytes=256 << 20, reps=5):
     log(f"copy calibration: {reps} x {nbytes} B device-to-device copies")
 
 
+def measured_copy_gbs(nbytes=1 << 30, reps=10):
+    """HBM bandwidth a plain device-to-device copy reaches (bytes read + written per second):
+    the measured ceiling beside the 8 TB/s spec peak."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (s.elapsed_time(e) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    log(f"copy kernel: {gbs:.0f} GB/s ({nbytes} B read + written per copy)")
+    return gbs
+
+
 def prefill_microbench(seqs=(512, 2048, 8192), nh=16, kvh=8, hd=128, reps=20):
     """Config 3: causal GQA attention prefill (bf16 q / k / v N(0,1), seed 3, RoPE base 1e6) on MFMA,
     and the pre-attention RMSNorm over seq x 2048 rows (unit-mean gains); HIP events on the launch stream."""
@@ -375,6 +396,9 @@ def main():
                         frac=round(head["frac"], 4), traffic=traffic_from_profile(),
                         kernel="k4_gemv_lane_kernel<0,8,4,1,4,0,1,0> (W4A8 store, 8 lanes/row, 4-wave one-unit workgroups) 151936x1024 B=1",
                         avg_launch_us=round(head["avg_us"], 3), algo_bytes_per_launch=head["algo_bytes"])
+        copy = measured_copy_gbs()
+        roofline["measured_copy_gbs"] = round(copy, 1)
+        roofline["frac_of_measured_copy"] = round(head["gbs"] / copy, 4)
     cpu = None
     if not args.no_cpu:
         try:

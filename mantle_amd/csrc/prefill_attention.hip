@@ -254,40 +254,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             }
             // element i: key t0 + (i/4)*8 + 4*h2 + i%4 of query myq; the causal
             // mask only on tiles that reach past the wave's first query
-            float x[16];
+            // the raw scores' maximum (scale > 0), then p = 2^(s*scale*log2e - m)
+            // as one FMA per score
             float mt = -INFINITY;
             if (t0 + kPfKeys - 1 <= qw && t0 + kPfKeys <= a.seq) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    x[i] = sacc[i] * sl2;
-                    mt = fmaxf(mt, x[i]);
-                }
+                for (int i = 0; i < 16; i++) mt = fmaxf(mt, sacc[i]);
             } else {
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const int key = t0 + (i >> 2) * 8 + 4 * h2 + (i & 3);
-                    x[i] = key <= myq && key < a.seq ? sacc[i] * sl2 : -INFINITY;
-                    mt = fmaxf(mt, x[i]);
+                    sacc[i] = key <= myq && key < a.seq ? sacc[i] : -INFINITY;
+                    mt = fmaxf(mt, sacc[i]);
                 }
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            const float m_new = fmaxf(m_run, mt * sl2);
             float ls = 0.0f;
             f16x8 pb[2];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float pv = __builtin_amdgcn_exp2f(x[i] - m_new);
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2, -m_new));
                 ls += pv;
                 pb[i >> 3][i & 7] = (_Float16)pv;
             }
             ls += __shfl_xor(ls, 32, 64);
-            l_run = l_run * alpha + ls;
+            // rescale only when some query's running maximum moved (alpha = 1
+            // exactly otherwise: the 64 multiplies would change nothing)
+            if (__any(m_new != m_run)) {
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run = l_run * alpha;
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) o[t][i] *= alpha;
+            }
+            l_run = l_run + ls;
             m_run = m_new;
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) o[t][i] *= alpha;
             // O^T += V^T . P^T: k index 8*h2 + j of step s2 is key 16*s2 + (j/4)*8 + 4*h2 + j%4
 #pragma unroll
             for (int t = 0; t < 4; t++) {
