@@ -813,6 +813,12 @@ int attention_path() {
     return g_attn_path.load();
 }
 
+// MANTLE_HIP_PV_LDS=0 keeps the register-ring V sum for the f32 cache.
+static bool pv_lds_enabled() {
+    const char* e = getenv("MANTLE_HIP_PV_LDS");
+    return !(e && !strcmp(e, "0"));
+}
+
 static std::atomic<int> g_kv_type{0};
 int kv_cache_type() { return g_kv_type.load(); }
 bool set_kv_cache_type(int t) {
@@ -1239,6 +1245,113 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     PHASE(2);
 }
 
+// The V-sum launch with V staged in LDS (f32 transposed cache): waves 1-3
+// load the head's 32 columns in chunks of kPvChunk keys (two chunks of loads
+// in flight in registers, written to a double-buffered LDS slot), while wave
+// 0 runs the ordered V sum of each chunk from LDS, one chunk behind: the
+// chain wave's operands come from LDS instead of a register ring that only
+// reaches 160 keys ahead.  One barrier per chunk keeps the waves in step;
+// every wave runs the same number of them.
+static constexpr int kPvChunk = 256;
+static constexpr int kPvPitch = kPvChunk + 4;  // floats per staged column (16-byte rows, banks skewed)
+static constexpr int kPvItems = (32 * kPvChunk / 4 + 191) / 192;  // float4 per loader lane per chunk
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    constexpr int DB = 32;
+    const int nd = HD / DB;
+    const int h = blockIdx.x / nd, db = blockIdx.x % nd;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = h * a.kv_heads / a.n_head;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int pcap = (a.max_ctx + 31) / 32 * 32;
+    const float* sg = a.scores + (size_t)h * a.max_ctx;
+    float* p = lds;
+    float* red = lds + pcap;
+    float* vr = red + 32;  // [2][32 columns][kPvPitch]
+    const int nch = pos / kPvChunk + 1;
+    // loader lane lt of waves 1-3: item e = lt + 192 i is float4 k4 = e % 64 of column e / 64
+    const int lt = tid - 64;
+    const float* colbase = a.cache_v + (size_t)(kvh * HD + db * DB) * a.vt_stride;
+    f32x4 la[kPvItems], lb[kPvItems];
+    auto issue = [&](f32x4 (&dst)[kPvItems], int c) {
+#pragma unroll
+        for (int i = 0; i < kPvItems; i++) {
+            const int e = lt + 192 * i;
+            const int ee = e < 32 * kPvChunk / 4 ? e : 0;
+            int t = c * kPvChunk + 4 * (ee & 63);
+            t = t <= pos ? t : (pos & ~3);  // keys past pos are staged, never added
+            dst[i] = *reinterpret_cast<const f32x4*>(colbase + (size_t)(ee >> 6) * a.vt_stride + t);
+        }
+    };
+    auto store = [&](const f32x4 (&src)[kPvItems], int slot) {
+#pragma unroll
+        for (int i = 0; i < kPvItems; i++) {
+            const int e = lt + 192 * i;
+            if (e < 32 * kPvChunk / 4)
+                *reinterpret_cast<f32x4*>(vr + (slot * 32 + (e >> 6)) * kPvPitch + 4 * (e & 63)) = src[i];
+        }
+    };
+    if (wave != 0) {  // the first chunks' loads overlap the softmax
+        issue(la, 0);
+        if (nch > 1) issue(lb, 1);
+    }
+    head_softmax<false>(sg, p, red, pos);
+    if (wave != 0) {
+        store(la, 0);
+        if (nch > 2) issue(la, 2);
+    }
+    __syncthreads();
+    const int d = lane & 31;
+    float acc = 0.0f;
+    // wave 0: the ordered sum of chunk c from LDS slot `slot`
+    auto sum_chunk = [&](int slot, int c) {
+        const float* col = vr + (slot * 32 + d) * kPvPitch;
+        const int t0 = c * kPvChunk;
+        const int n = min(kPvChunk, pos + 1 - t0);
+        for (int k0 = 0; k0 < n; k0 += 32) {
+            float pg[32], vg[32];
+#pragma unroll
+            for (int i4 = 0; i4 < 8; i4++) {
+                const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + k0 + 4 * i4);
+                const f32x4 v4 = *reinterpret_cast<const f32x4*>(col + k0 + 4 * i4);
+                pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                vg[4 * i4] = v4.x; vg[4 * i4 + 1] = v4.y; vg[4 * i4 + 2] = v4.z; vg[4 * i4 + 3] = v4.w;
+            }
+            if (k0 + 32 <= n) {
+#pragma unroll
+                for (int k = 0; k < 32; k++) acc = acc + pg[k] * vg[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 32; k++) {
+                    const float nacc = acc + pg[k] * vg[k];
+                    acc = k0 + k < n ? nacc : acc;
+                }
+            }
+        }
+    };
+    for (int c = 0; c < nch; c += 2) {
+        if (wave == 0) {
+            sum_chunk(0, c);
+        } else {
+            if (c + 1 < nch) store(lb, 1);
+            if (c + 3 < nch) issue(lb, c + 3);
+        }
+        __syncthreads();
+        if (c + 1 >= nch) break;
+        if (wave == 0) {
+            sum_chunk(1, c + 1);
+        } else {
+            if (c + 2 < nch) store(la, 0);
+            if (c + 4 < nch) issue(la, c + 4);
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+    store_attn_out(a, h * HD + db * DB + d, acc, lane < 32);
+}
+
 // The library's zeroed arrival counters (one set per device, allocated on first
 // use, never freed), for callers that pass none.  Each launch leaves them at
 // zero again, so launches stream-ordered after one another may share them;
@@ -1336,6 +1449,11 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
              attention_scores_split<128, kKvQ8>}};
         auto pvk = pv[a.head_dim == 128][vt][kvt];
         size_t smem_pv = smem_b;
+        const size_t smem_lv = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 32 + 2 * 32 * kPvPitch);
+        if (vt && kvt == kKvF32 && smem_lv <= kMaxLds && pv_lds_enabled()) {  // V staged in LDS
+            pvk = a.head_dim == 128 ? attention_pv_lds<128> : attention_pv_lds<64>;
+            smem_pv = smem_lv;
+        }
         const size_t smem_sl = sizeof(float) * (2 * ((size_t)(a.max_ctx + 31) / 32 * 32) + 32);
         if (a.kv_q8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
             void (*const pvs[2][2])(AttnArgs) = {

@@ -118,6 +118,28 @@ def test_lane_q8_kv_cache_bitexact(hip, lane_path, path):
         _lib.call("mantleHipSetAttentionPath", 0)
 
 
+@pytest.mark.parametrize("pv_lds", ["1", "0"])
+def test_lane_f32_v_sum_staged_in_lds(hip, lane_path, pv_lds, monkeypatch):
+    """The f32 cache's V sum with V staged in LDS by loader waves, chunks of
+    256 keys (600 steps: three chunks, the last partial; 650 positions pad the
+    columns), and the register-ring form (MANTLE_HIP_PV_LDS=0): logits
+    bit-identical to the oracle."""
+    import mantle_amd
+    monkeypatch.setenv("MANTLE_HIP_PV_LDS", pv_lds)
+    rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=650)
+    om = models.oracle_model(lane_path, models.LANE, 650)
+    try:
+        toks = models.prompt(600, models.LANE["vocab"], 10)
+        for step, tok in enumerate(toks):
+            logits = rt.forward_token(tok)
+            _, want = om.forward_greedy(tok, want_logits=True)
+            if step % 50 == 49 or step in (0, 255, 256, 257, 511, 512, 599):
+                np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+    finally:
+        rt.close()
+        om.close()
+
+
 @pytest.mark.parametrize("path", ["fused", "split", "single", "general"])
 def test_lane_long_context_attention_paths(hip, lane_path, path):
     """140 fused steps (past two 64-key chunks, the step's own K/V row inside
