@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <type_traits>
 #include <mutex>
 
 #include "device_common.h"
@@ -1245,20 +1246,26 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     PHASE(2);
 }
 
-// The V-sum launch with V staged in LDS (f32 transposed cache): waves 1-3
-// load the head's 32 columns in chunks of kPvChunk keys (two chunks of loads
-// in flight in registers, written to a double-buffered LDS slot), while wave
-// 0 runs the ordered V sum of each chunk from LDS, one chunk behind: the
-// chain wave's operands come from LDS instead of a register ring that only
-// reaches 160 keys ahead.  One barrier per chunk keeps the waves in step;
-// every wave runs the same number of them.
+// The V-sum launch with V staged in LDS (transposed cache): waves 1-3 load
+// the head's 32 columns in chunks of kPvChunk keys (two chunks of loads in
+// flight in registers, widened to fp32 -- f16 through the flushing hardware
+// conversion, int8 exactly -- and written to a double-buffered LDS slot),
+// while wave 0 runs the ordered V sum of each chunk from LDS, one chunk
+// behind: the chain wave's operands come from LDS instead of a register ring
+// that only reaches 160-320 keys ahead, and it spends no instruction on
+// widening.  kKvQ8: the keys' scales are staged in LDS too (after the
+// probabilities) and the terms are (p * q) * s.  One barrier per chunk keeps
+// the waves in step; every wave runs the same number of them.
 static constexpr int kPvChunk = 256;
 static constexpr int kPvPitch = kPvChunk + 4;  // floats per staged column (16-byte rows, banks skewed)
 static constexpr int kPvItems = (32 * kPvChunk / 4 + 191) / 192;  // float4 per loader lane per chunk
 
-template <int HD>
+template <int HD, int KV>
 __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
+    constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
+    // raw loader registers: 4 keys of one column per item
+    typedef typename std::conditional<F16, u32x2, typename std::conditional<Q8, uint32_t, f32x4>::type>::type Raw;
     constexpr int DB = 32;
     const int nd = HD / DB;
     const int h = blockIdx.x / nd, db = blockIdx.x % nd;
@@ -1269,34 +1276,53 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     const float* sg = a.scores + (size_t)h * a.max_ctx;
     float* p = lds;
     float* red = lds + pcap;
-    float* vr = red + 32;  // [2][32 columns][kPvPitch]
+    float* ls = red + 32;              // Q8: the keys' scales [pcap]
+    float* vr = ls + (Q8 ? pcap : 0);  // [2][32 columns][kPvPitch]
     const int nch = pos / kPvChunk + 1;
-    // loader lane lt of waves 1-3: item e = lt + 192 i is float4 k4 = e % 64 of column e / 64
+    // loader lane lt of waves 1-3: item e = lt + 192 i is keys 4 (e % 64) .. +3 of column e / 64
     const int lt = tid - 64;
-    const float* colbase = a.cache_v + (size_t)(kvh * HD + db * DB) * a.vt_stride;
-    f32x4 la[kPvItems], lb[kPvItems];
-    auto issue = [&](f32x4 (&dst)[kPvItems], int c) {
+    const size_t colofs = (size_t)(kvh * HD + db * DB) * a.vt_stride;
+    const char* colbase = reinterpret_cast<const char*>(a.cache_v) + colofs * (F16 ? 2 : (Q8 ? 1 : 4));
+    constexpr int esz = F16 ? 2 : (Q8 ? 1 : 4);
+    Raw la[kPvItems], lb[kPvItems];
+    auto issue = [&](Raw (&dst)[kPvItems], int c) {
 #pragma unroll
         for (int i = 0; i < kPvItems; i++) {
             const int e = lt + 192 * i;
             const int ee = e < 32 * kPvChunk / 4 ? e : 0;
             int t = c * kPvChunk + 4 * (ee & 63);
             t = t <= pos ? t : (pos & ~3);  // keys past pos are staged, never added
-            dst[i] = *reinterpret_cast<const f32x4*>(colbase + (size_t)(ee >> 6) * a.vt_stride + t);
+            dst[i] = *reinterpret_cast<const Raw*>(colbase + ((size_t)(ee >> 6) * a.vt_stride + t) * esz);
         }
     };
-    auto store = [&](const f32x4 (&src)[kPvItems], int slot) {
+    auto store = [&](const Raw (&src)[kPvItems], int slot) {
 #pragma unroll
         for (int i = 0; i < kPvItems; i++) {
             const int e = lt + 192 * i;
+            f32x4 v;
+            if constexpr (F16) {
+                v.x = f16_cache_load((uint16_t)(src[i].x & 0xFFFFu));
+                v.y = f16_cache_load((uint16_t)(src[i].x >> 16));
+                v.z = f16_cache_load((uint16_t)(src[i].y & 0xFFFFu));
+                v.w = f16_cache_load((uint16_t)(src[i].y >> 16));
+            } else if constexpr (Q8) {
+                v.x = q8_byte_sdwa<0>(src[i]);
+                v.y = q8_byte_sdwa<1>(src[i]);
+                v.z = q8_byte_sdwa<2>(src[i]);
+                v.w = q8_byte_sdwa<3>(src[i]);
+            } else {
+                v = src[i];
+            }
             if (e < 32 * kPvChunk / 4)
-                *reinterpret_cast<f32x4*>(vr + (slot * 32 + (e >> 6)) * kPvPitch + 4 * (e & 63)) = src[i];
+                *reinterpret_cast<f32x4*>(vr + (slot * 32 + (e >> 6)) * kPvPitch + 4 * (e & 63)) = v;
         }
     };
     if (wave != 0) {  // the first chunks' loads overlap the softmax
         issue(la, 0);
         if (nch > 1) issue(lb, 1);
     }
+    if constexpr (Q8)
+        for (int t = tid; t <= pos; t += kThreads) ls[t] = a.v_scale[t];
     head_softmax<false>(sg, p, red, pos);
     if (wave != 0) {
         store(la, 0);
@@ -1311,21 +1337,29 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
         const int t0 = c * kPvChunk;
         const int n = min(kPvChunk, pos + 1 - t0);
         for (int k0 = 0; k0 < n; k0 += 32) {
-            float pg[32], vg[32];
+            float pg[32], vg[32], sgk[Q8 ? 32 : 1];
 #pragma unroll
             for (int i4 = 0; i4 < 8; i4++) {
                 const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + k0 + 4 * i4);
                 const f32x4 v4 = *reinterpret_cast<const f32x4*>(col + k0 + 4 * i4);
                 pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
                 vg[4 * i4] = v4.x; vg[4 * i4 + 1] = v4.y; vg[4 * i4 + 2] = v4.z; vg[4 * i4 + 3] = v4.w;
+                if constexpr (Q8) {
+                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(ls + t0 + k0 + 4 * i4);
+                    sgk[4 * i4] = s4.x; sgk[4 * i4 + 1] = s4.y; sgk[4 * i4 + 2] = s4.z; sgk[4 * i4 + 3] = s4.w;
+                }
             }
+            auto term = [&](int k) {
+                if constexpr (Q8) return (pg[k] * vg[k]) * sgk[k];
+                else return pg[k] * vg[k];
+            };
             if (k0 + 32 <= n) {
 #pragma unroll
-                for (int k = 0; k < 32; k++) acc = acc + pg[k] * vg[k];
+                for (int k = 0; k < 32; k++) acc = acc + term(k);
             } else {
 #pragma unroll
                 for (int k = 0; k < 32; k++) {
-                    const float nacc = acc + pg[k] * vg[k];
+                    const float nacc = acc + term(k);
                     acc = k0 + k < n ? nacc : acc;
                 }
             }
@@ -1449,13 +1483,18 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
              attention_scores_split<128, kKvQ8>}};
         auto pvk = pv[a.head_dim == 128][vt][kvt];
         size_t smem_pv = smem_b;
-        const size_t smem_lv = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 32 + 2 * 32 * kPvPitch);
-        if (vt && kvt == kKvF32 && smem_lv <= kMaxLds && pv_lds_enabled()) {  // V staged in LDS
-            pvk = a.head_dim == 128 ? attention_pv_lds<128> : attention_pv_lds<64>;
+        const size_t pcap = (size_t)(a.max_ctx + 31) / 32 * 32;
+        const size_t smem_lv = sizeof(float) * (pcap * (a.kv_q8 ? 2 : 1) + 32 + 2 * 32 * kPvPitch);
+        const bool lv_used = vt && smem_lv <= kMaxLds && pv_lds_enabled();
+        if (lv_used) {  // V staged in LDS
+            void (*const lv[2][3])(AttnArgs) = {
+                {attention_pv_lds<64, kKvF32>, attention_pv_lds<64, kKvF16>, attention_pv_lds<64, kKvQ8>},
+                {attention_pv_lds<128, kKvF32>, attention_pv_lds<128, kKvF16>, attention_pv_lds<128, kKvQ8>}};
+            pvk = lv[a.head_dim == 128][kvt];
             smem_pv = smem_lv;
         }
         const size_t smem_sl = sizeof(float) * (2 * ((size_t)(a.max_ctx + 31) / 32 * 32) + 32);
-        if (a.kv_q8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
+        if (!lv_used && a.kv_q8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
             void (*const pvs[2][2])(AttnArgs) = {
                 {attention_pv_split<64, false, kKvQ8, true>, attention_pv_split<64, true, kKvQ8, true>},
                 {attention_pv_split<128, false, kKvQ8, true>, attention_pv_split<128, true, kKvQ8, true>}};

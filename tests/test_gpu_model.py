@@ -118,16 +118,17 @@ def test_lane_q8_kv_cache_bitexact(hip, lane_path, path):
         _lib.call("mantleHipSetAttentionPath", 0)
 
 
-@pytest.mark.parametrize("pv_lds", ["1", "0"])
-def test_lane_f32_v_sum_staged_in_lds(hip, lane_path, pv_lds, monkeypatch):
-    """The f32 cache's V sum with V staged in LDS by loader waves, chunks of
-    256 keys (600 steps: three chunks, the last partial; 650 positions pad the
-    columns), and the register-ring form (MANTLE_HIP_PV_LDS=0): logits
-    bit-identical to the oracle."""
+@pytest.mark.parametrize("kv,pv_lds", [("f32", "1"), ("f32", "0"), ("f16", "1"), ("q8_0", "1")])
+def test_lane_v_sum_staged_in_lds(hip, lane_path, kv, pv_lds, monkeypatch):
+    """The V sum with V staged in LDS by loader waves (widened there: f16
+    through the flushing conversion, int8 exactly), chunks of 256 keys (600
+    steps: three chunks, the last partial; 650 positions pad the columns), and
+    the register-ring form (MANTLE_HIP_PV_LDS=0): logits bit-identical to the
+    oracle for each cache type."""
     import mantle_amd
     monkeypatch.setenv("MANTLE_HIP_PV_LDS", pv_lds)
-    rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=650)
-    om = models.oracle_model(lane_path, models.LANE, 650)
+    rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=650, kv_cache=kv)
+    om = models.oracle_model(lane_path, dict(models.LANE, kv_cache=kv), 650)
     try:
         toks = models.prompt(600, models.LANE["vocab"], 10)
         for step, tok in enumerate(toks):
