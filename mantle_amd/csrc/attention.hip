@@ -1257,6 +1257,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
 // probabilities) and the terms are (p * q) * s.  One barrier per chunk keeps
 // the waves in step; every wave runs the same number of them.
 static constexpr int kPvChunk = 256;
+static constexpr int kPvLdsMinCtx = 512;  // caches of more positions stage V in LDS
 static constexpr int kPvPitch = kPvChunk + 4;  // floats per staged column (16-byte rows, banks skewed)
 static constexpr int kPvItems = (32 * kPvChunk / 4 + 191) / 192;  // float4 per loader lane per chunk
 
@@ -1485,7 +1486,9 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         size_t smem_pv = smem_b;
         const size_t pcap = (size_t)(a.max_ctx + 31) / 32 * 32;
         const size_t smem_lv = sizeof(float) * (pcap * (a.kv_q8 ? 2 : 1) + 32 + 2 * 32 * kPvPitch);
-        const bool lv_used = vt && smem_lv <= kMaxLds && pv_lds_enabled();
+        // (short caches keep the register ring: at a few hundred keys the
+        // loader waves' barriers cost more than they save, 6.30 -> 6.55 us)
+        const bool lv_used = vt && a.max_ctx > kPvLdsMinCtx && smem_lv <= kMaxLds && pv_lds_enabled();
         if (lv_used) {  // V staged in LDS
             void (*const lv[2][3])(AttnArgs) = {
                 {attention_pv_lds<64, kKvF32>, attention_pv_lds<64, kKvF16>, attention_pv_lds<64, kKvQ8>},
