@@ -1253,8 +1253,8 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
 // while wave 0 runs the ordered V sum of each chunk from LDS, one chunk
 // behind: the chain wave's operands come from LDS instead of a register ring
 // that only reaches 160-320 keys ahead, and it spends no instruction on
-// widening.  kKvQ8: the keys' scales are staged in LDS too (after the
-// probabilities) and the terms are (p * q) * s.  One barrier per chunk keeps
+// widening.  kKvQ8: the loaders stage each chunk's key scales beside its
+// columns and the terms are (p * q) * s.  One barrier per chunk keeps
 // the waves in step; every wave runs the same number of them.
 static constexpr int kPvChunk = 256;
 static constexpr int kPvLdsMinCtx = 512;  // caches of more positions stage V in LDS
@@ -1277,8 +1277,8 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     const float* sg = a.scores + (size_t)h * a.max_ctx;
     float* p = lds;
     float* red = lds + pcap;
-    float* ls = red + 32;              // Q8: the keys' scales [pcap]
-    float* vr = ls + (Q8 ? pcap : 0);  // [2][32 columns][kPvPitch]
+    float* vr = red + 32;                  // [2][32 columns][kPvPitch]
+    float* vsc = vr + 2 * 32 * kPvPitch;  // Q8: [2][kPvChunk] key scales
     const int nch = pos / kPvChunk + 1;
     // loader lane lt of waves 1-3: item e = lt + 192 i is keys 4 (e % 64) .. +3 of column e / 64
     const int lt = tid - 64;
@@ -1286,6 +1286,24 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     const char* colbase = reinterpret_cast<const char*>(a.cache_v) + colofs * (F16 ? 2 : (Q8 ? 1 : 4));
     constexpr int esz = F16 ? 2 : (Q8 ? 1 : 4);
     Raw la[kPvItems], lb[kPvItems];
+    constexpr int NS = Q8 ? (kPvChunk + 191) / 192 : 1;  // scales per loader lane per chunk
+    float sa[NS], sb[NS];
+    auto issue_scales = [&](float (&dst)[NS], int c) {
+        if constexpr (Q8) {
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                const int t = c * kPvChunk + lt + 192 * i;
+                dst[i] = a.v_scale[t <= pos ? t : pos];
+            }
+        }
+    };
+    auto store_scales = [&](const float (&src)[NS], int slot) {
+        if constexpr (Q8) {
+#pragma unroll
+            for (int i = 0; i < NS; i++)
+                if (lt + 192 * i < kPvChunk) vsc[slot * kPvChunk + lt + 192 * i] = src[i];
+        }
+    };
     auto issue = [&](Raw (&dst)[kPvItems], int c) {
 #pragma unroll
         for (int i = 0; i < kPvItems; i++) {
@@ -1320,14 +1338,20 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     };
     if (wave != 0) {  // the first chunks' loads overlap the softmax
         issue(la, 0);
-        if (nch > 1) issue(lb, 1);
+        issue_scales(sa, 0);
+        if (nch > 1) {
+            issue(lb, 1);
+            issue_scales(sb, 1);
+        }
     }
-    if constexpr (Q8)
-        for (int t = tid; t <= pos; t += kThreads) ls[t] = a.v_scale[t];
     head_softmax<false>(sg, p, red, pos);
     if (wave != 0) {
         store(la, 0);
-        if (nch > 2) issue(la, 2);
+        store_scales(sa, 0);
+        if (nch > 2) {
+            issue(la, 2);
+            issue_scales(sa, 2);
+        }
     }
     __syncthreads();
     const int d = lane & 31;
@@ -1335,6 +1359,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     // wave 0: the ordered sum of chunk c from LDS slot `slot`
     auto sum_chunk = [&](int slot, int c) {
         const float* col = vr + (slot * 32 + d) * kPvPitch;
+        const float* cs = vsc + slot * kPvChunk;
         const int t0 = c * kPvChunk;
         const int n = min(kPvChunk, pos + 1 - t0);
         for (int k0 = 0; k0 < n; k0 += 32) {
@@ -1346,7 +1371,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
                 pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
                 vg[4 * i4] = v4.x; vg[4 * i4 + 1] = v4.y; vg[4 * i4 + 2] = v4.z; vg[4 * i4 + 3] = v4.w;
                 if constexpr (Q8) {
-                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(ls + t0 + k0 + 4 * i4);
+                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + k0 + 4 * i4);
                     sgk[4 * i4] = s4.x; sgk[4 * i4 + 1] = s4.y; sgk[4 * i4 + 2] = s4.z; sgk[4 * i4 + 3] = s4.w;
                 }
             }
@@ -1370,16 +1395,28 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
         if (wave == 0) {
             sum_chunk(0, c);
         } else {
-            if (c + 1 < nch) store(lb, 1);
-            if (c + 3 < nch) issue(lb, c + 3);
+            if (c + 1 < nch) {
+                store(lb, 1);
+                store_scales(sb, 1);
+            }
+            if (c + 3 < nch) {
+                issue(lb, c + 3);
+                issue_scales(sb, c + 3);
+            }
         }
         __syncthreads();
         if (c + 1 >= nch) break;
         if (wave == 0) {
             sum_chunk(1, c + 1);
         } else {
-            if (c + 2 < nch) store(la, 0);
-            if (c + 4 < nch) issue(la, c + 4);
+            if (c + 2 < nch) {
+                store(la, 0);
+                store_scales(sa, 0);
+            }
+            if (c + 4 < nch) {
+                issue(la, c + 4);
+                issue_scales(sa, c + 4);
+            }
         }
         __syncthreads();
     }
@@ -1485,7 +1522,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         auto pvk = pv[a.head_dim == 128][vt][kvt];
         size_t smem_pv = smem_b;
         const size_t pcap = (size_t)(a.max_ctx + 31) / 32 * 32;
-        const size_t smem_lv = sizeof(float) * (pcap * (a.kv_q8 ? 2 : 1) + 32 + 2 * 32 * kPvPitch);
+        const size_t smem_lv = sizeof(float) * (pcap + 32 + 2 * 32 * kPvPitch + (a.kv_q8 ? 2 * kPvChunk : 0));
         // (short caches keep the register ring: at a few hundred keys the
         // loader waves' barriers cost more than they save, 6.30 -> 6.55 us)
         const bool lv_used = vt && a.max_ctx > kPvLdsMinCtx && smem_lv <= kMaxLds && pv_lds_enabled();
