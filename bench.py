@@ -347,7 +347,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "single-GPU build: bench.py measures one MI355X; --gpus > 1 is not supported "
-                                   "(see DESIGN.md for how the path would shard)"}))
+                                   "(the path would shard the GEMV rows and the attention by kv head, one process per GPU)"}))
         sys.exit(2)
 
     import torch
