@@ -143,6 +143,17 @@ def test_host_validation_rejects_bad_arguments():
     assert L.mantleHipSoftmaxRowsF32(fake, 0, 4, None) == 1
     assert L.mantleHipArgMaxF32(fake, 0, fake, None) == 1
     assert L.mantleHipSetParityISA(7) == 1
+    # q8_0 cache: rows past 4096 values, a null row, a non-zero start, head_dim 96 (no split kernel)
+    assert L.mantleHipStoreKVQ8Row(fake, fake, fake, fake, fake, fake, 0, 5000, None) == 1
+    assert L.mantleHipStoreKVQ8Row(fake, fake, fake, fake, None, fake, 0, 1024, None) == 1
+    assert L.mantleHipStoreKVQ8Row(fake, fake, fake, fake, fake, fake, 0, 0, None) == 1
+    assert L.mantleHipAttentionInnerQ8CacheF32(fake, fake, fake, fake, fake, fake, fake, 5, 1, 1024, 128, 16, 8, 6,
+                                               C.c_float(1), None) == 1
+    assert L.mantleHipAttentionInnerQ8CacheF32(fake, fake, fake, fake, fake, fake, fake, 5, 0, 768, 96, 16, 8, 6,
+                                               C.c_float(1), None) == 1
+    assert L.mantleHipSetKVCacheType(3) == 1
+    assert L.mantleHipSetKVCacheType(2) == 0 and L.mantleHipGetKVCacheType() == 2
+    assert L.mantleHipSetKVCacheType(0) == 0
     assert L.mantleHipGetErrorString(1)
 
 
