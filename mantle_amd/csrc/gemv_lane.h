@@ -265,10 +265,16 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     PHASE(0);
     // Activation loads first: they must not queue behind the weight stream.
     // Every trip's loads are issued here, so the prologue waits for HBM once.
-    constexpr int HALVES = 2 * BPR;  // 16-value halves of one activation row
-    constexpr int TRIPS = (HALVES + NT - 1) / NT;
+    // The fp32 row is spread over the workgroup in pieces of VPT consecutive
+    // values (VPT = 16 / 8 / 4 / 2: every thread busy where the row allows),
+    // so a multi-wave workgroup shares the RMSNorm and quantisation work.
+    constexpr int NCOLS = BPR * 32;
+    constexpr int VPT0 = NCOLS / NT;
+    constexpr int VPT = VPT0 >= 16 ? 16 : (VPT0 >= 8 ? 8 : (VPT0 >= 4 ? 4 : 2));
+    constexpr int PIECES = NCOLS / VPT;
+    constexpr int TRIPS = (PIECES + NT - 1) / NT;
     constexpr int QV = (NB * BPR * 2 + NT - 1) / NT;  // 16-byte pieces of qx per lane
-    float pv[PRO == kProQx ? 1 : TRIPS][16], pg[PRO == kProNorm ? TRIPS : 1][16];
+    float pv[PRO == kProQx ? 1 : TRIPS][VPT], pg[PRO == kProNorm ? TRIPS : 1][VPT];
     constexpr int XV = (NB * BPR + NT - 1) / NT;  // block scales per lane
     u32x4 qpre[PRO == kProQx ? QV : 1];
     float xpre[PRO == kProQx ? XV : 1];
@@ -287,24 +293,10 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
     } else if constexpr (NB == 1) {
 #pragma unroll
         for (int t = 0; t < TRIPS; t++) {
-            // unconditional: lanes past the row re-read half 0 (not used)
-            const int hh = HALVES % NT == 0 || tid + t * NT < HALVES ? tid + t * NT : 0;
-            {
-                const float4* x4 = reinterpret_cast<const float4*>(p.x + hh * 16);
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float4 u = x4[k];
-                    pv[t][4 * k] = u.x; pv[t][4 * k + 1] = u.y; pv[t][4 * k + 2] = u.z; pv[t][4 * k + 3] = u.w;
-                }
-                if constexpr (PRO == kProNorm) {
-                    const float4* g4 = reinterpret_cast<const float4*>(p.norm_w + hh * 16);
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const float4 u = g4[k];
-                        pg[t][4 * k] = u.x; pg[t][4 * k + 1] = u.y; pg[t][4 * k + 2] = u.z; pg[t][4 * k + 3] = u.w;
-                    }
-                }
-            }
+            // unconditional: threads past the row re-read piece 0 (not used)
+            const int pc = PIECES % NT == 0 || tid + t * NT < PIECES ? tid + t * NT : 0;
+            load_piece<VPT>(p.x + pc * VPT, pv[t]);
+            if constexpr (PRO == kProNorm) load_piece<VPT>(p.norm_w + pc * VPT, pg[t]);
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead of the weight stream
@@ -329,25 +321,24 @@ __global__ __launch_bounds__(NW * 64) void k4_gemv_lane_kernel(GemvParams p) {
         PHASE_AFTER(2, pv[0][0]);
         float scale = 1.0f;
         if constexpr (PRO == kProNorm) {
-            constexpr int NCOL = BPR * 32;
 #pragma unroll
             for (int t = 0; t < TRIPS; t++) {
-                const int hh = tid + t * NT;
-                if (HALVES % NT == 0 || hh < HALVES) rms_stage_half(work, rms_stage_pitch(NCOL), hh, pv[t]);
+                const int pc = tid + t * NT;
+                if (PIECES % NT == 0 || pc < PIECES) rms_stage_piece<VPT>(work, rms_stage_pitch(NCOLS), pc, pv[t]);
             }
             __syncthreads();
-            scale = wg_rms_scale_t<NCOL, NW>(work, p.eps, p.isa, work + 16 * rms_stage_pitch(NCOL));
+            scale = wg_rms_scale_t<NCOLS, NW>(work, p.eps, p.isa, work + 16 * rms_stage_pitch(NCOLS));
             PHASE(6);
         }
 #pragma unroll
         for (int t = 0; t < TRIPS; t++) {
-            const int hh = tid + t * NT;
-            const bool live = HALVES % NT == 0 || hh < HALVES;
+            const int pc = tid + t * NT;
+            const bool live = PIECES % NT == 0 || pc < PIECES;
             if constexpr (PRO == kProNorm) {
 #pragma unroll
-                for (int k = 0; k < 16; k++) pv[t][k] = (pv[t][k] * scale) * pg[t][k];
+                for (int k = 0; k < VPT; k++) pv[t][k] = (pv[t][k] * scale) * pg[t][k];
             }
-            quantize_half16(pv[t], live, hh, sq, sxs);
+            quantize_piece<VPT>(pv[t], live, pc, sq, sxs);
         }
         __syncthreads();
     } else {
@@ -482,6 +473,25 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
     const int per = (units + slots - 1) / slots;
     const int grid = (units + per - 1) / per;
+    if (l2_plan_out) {  // record where each unit's weights will be read; no launch
+        L2Prefetch& f = *l2_plan_out;
+        f = L2Prefetch{};
+        for (int i = 0; i < p.nmat; i++) f.mats[i] = p.mats[i];
+        f.nmat = p.nmat;
+        f.nsub = EPI == kEpiSiluMul ? 2 : 1;
+        f.bpr = p.bpr;
+        f.rpu = RPU;
+        f.grid = grid;
+        f.units = units;
+        f.per = per;
+        for (int i = 0; i < 4; i++) f.wg_begin[i] = p.wg_begin[i];
+        f.nib_lines = RPU * p.bpr / 8;
+        f.lines = f.nib_lines + 2;
+        f.inv_lines = 1.0f / (float)f.lines;
+        return hipSuccess;
+    }
+    if (l2_next) p.pf = *l2_next;
+    else p.pf.nmat = 0;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), smem, stream, p);
     return hipGetLastError();
 }
@@ -535,7 +545,8 @@ static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
     }
     if constexpr (C16 == T16) {
         if (q32) return launch_lane_gemv<EPI, 16, T16, NB, 8, PRO>(p, stream);
-        return launch_lane_gemv<EPI, 16, T16, NB, 1, PRO>(p, stream);
+        // an in-kernel RMSNorm / quantisation prologue is shared by four waves
+        return launch_lane_gemv<EPI, 16, T16, NB, PRO == kProQx ? 1 : 4, PRO>(p, stream);
     } else {
         if (q32) return launch_lane_gemv<EPI, 16, C16, NB, 8, PRO, 2, T16>(p, stream);
         return launch_lane_gemv<EPI, 16, C16, NB, 1, PRO, 2, T16>(p, stream);

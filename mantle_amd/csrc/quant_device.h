@@ -340,6 +340,81 @@ __device__ __forceinline__ void quantize_half16(const float (&v)[16], bool live,
     if (half == 0) s_out[blk] = sc;
 }
 
+// VPT consecutive floats (16-byte aligned for VPT >= 4, 8-byte for 2).
+template <int VPT>
+__device__ __forceinline__ void load_piece(const float* __restrict__ src, float (&v)[VPT]) {
+    if constexpr (VPT >= 4) {
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+#pragma unroll
+        for (int k = 0; k < VPT / 4; k++) {
+            const float4 u = s4[k];
+            v[4 * k] = u.x; v[4 * k + 1] = u.y; v[4 * k + 2] = u.z; v[4 * k + 3] = u.w;
+        }
+    } else {
+        const float2 u = *reinterpret_cast<const float2*>(src);
+        v[0] = u.x; v[1] = u.y;
+    }
+}
+
+// quantize_half16 for a piece of VPT (2..16) consecutive values: piece pc
+// holds elements VPT*pc .. VPT*pc+VPT-1 of the row, the 32/VPT pieces of a
+// block sit in consecutive lanes of one wave (their max is an xor exchange
+// over those lanes; max is exact in any order), and every lane of the wave
+// calls it.  Same arithmetic and byte layout as quantize_half16.
+template <int VPT>
+__device__ __forceinline__ void quantize_piece(const float (&v)[VPT], bool live, int pc, int8_t* q_out,
+                                               float* s_out) {
+    static_assert(VPT == 2 || VPT == 4 || VPT == 8 || VPT == 16, "a block is 32 / VPT pieces");
+    float m = 0.0f;
+    if (live) {
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const float a = v[k] < 0 ? -v[k] : v[k];
+            m = a > m ? a : m;
+        }
+    }
+#pragma unroll
+    for (int off = 1; off < 32 / VPT; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (!live) return;
+    float sc;
+    const float inv = quant_block_inv(m, &sc);
+    const int e0 = (pc * VPT) & 31;  // first element of the piece within its block
+    int8_t* qb = q_out + (pc * VPT - e0);
+    if constexpr (VPT == 16) {
+        uint32_t we[2] = {0, 0}, wo[2] = {0, 0};
+        if (m != 0.0f) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const uint32_t byte = (uint32_t)(uint8_t)(int8_t)quant_value(v[k], inv);
+                const int dw = (k >> 3), sh = ((k >> 1) & 3) * 8;
+                if (k & 1) wo[dw] |= byte << sh; else we[dw] |= byte << sh;
+            }
+        }
+        uint2* q2 = reinterpret_cast<uint2*>(qb);
+        const int half = e0 >> 4;
+        q2[half] = make_uint2(we[0], we[1]);
+        q2[2 + half] = make_uint2(wo[0], wo[1]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const int8_t q = m != 0.0f ? (int8_t)quant_value(v[k], inv) : (int8_t)0;
+            qb[qx_perm(e0 + k)] = q;
+        }
+    }
+    if (e0 == 0) s_out[(pc * VPT) >> 5] = sc;
+}
+
+// rms_stage_half for a piece of VPT consecutive values: x[VPT*pc + k] goes to
+// tv[((VPT*pc + k) & 15) * pitch + ((VPT*pc + k) >> 4)].
+template <int VPT>
+__device__ __forceinline__ void rms_stage_piece(float* tv, int pitch, int pc, const float (&v)[VPT]) {
+#pragma unroll
+    for (int k = 0; k < VPT; k++) {
+        const int i = VPT * pc + k;
+        tv[(i & 15) * pitch + (i >> 4)] = v[k];
+    }
+}
+
 // Row pitch (floats) of the transposed staging of an N-value row: value
 // x[16m + l] sits at tv[l * pitch + m], so parity lane l's operands are one
 // contiguous run (read as float4); the +4 spreads the 16 runs over the banks.

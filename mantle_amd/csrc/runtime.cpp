@@ -198,13 +198,57 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
     float* q = m->qkv;
     float* k = m->qkv + m->q_dim;
     float* v = k + m->kv_dim;
-    TRY(launch_embed(m->embed, d, m->prompt, m->state, m->x, s));
-    for (int l = 0; l < c.n_layers; l++) {
+    const bool qattn = (c.head_dim & 31) == 0;  // whole int8 blocks per head
+    float* xo[1] = {m->x};
+    // The layer's four GEMVs.  runtime_decode.go:107 RMSNorm + attn.go:180-205
+    // one int8 activation for Q, K, V.
+    auto gemv_qkv = [&](int l) {
         const auto& L = m->layers[l];
-        // runtime_decode.go:107 RMSNorm + attn.go:180-205 one int8 activation for Q, K, V
         K4Mat qkv[3] = {L.wq, L.wk, L.wv};
         float* outs[3] = {q, k, v};
-        TRY(launch_k4_gemv_w4a8_fused(qkv, outs, 3, d, m->x, L.attn_norm, c.eps, m->isa, 1, kEpiStore, nullptr, s));
+        return launch_k4_gemv_w4a8_fused(qkv, outs, 3, d, m->x, L.attn_norm, c.eps, m->isa, 1, kEpiStore, nullptr, s);
+    };
+    // attn.go:417 Wo on the re-quantised attention output (quantised by the
+    // attention kernel), residual folded in
+    auto gemv_wo = [&](int l) {
+        const auto& L = m->layers[l];
+        if (qattn) return launch_k4_gemv_w4a8(&L.wo, xo, 1, m->q_dim, m->qx, m->xs, 1, kEpiResAdd, nullptr, s);
+        return launch_k4_gemv_w4a8_fused(&L.wo, xo, 1, m->q_dim, m->attn, nullptr, 0.0f, m->isa, 1, kEpiResAdd,
+                                         nullptr, s);
+    };
+    // ffn.go:18-91: RMSNorm, up/gate on one int8 activation, SiLU*up (also
+    // quantised for down), down + residual
+    auto gemv_gu = [&](int l) {
+        const auto& L = m->layers[l];
+        K4Mat gu[2] = {L.gate, L.up};
+        float* ao[2] = {m->act, m->act};
+        return launch_k4_gemv_w4a8_fused(gu, ao, 2, d, m->x, L.ffn_norm, c.eps, m->isa, 1, kEpiSiluMul, nullptr, s,
+                                         m->qx, m->xs);
+    };
+    auto gemv_down = [&](int l) {
+        return launch_k4_gemv_w4a8(&m->layers[l].down, xo, 1, c.ffn, m->qx, m->xs, 1, kEpiResAdd, nullptr, s);
+    };
+    // Each GEMV fetches the next one's weights into the L2s that will read
+    // them (QKV -> Wo -> gate/up -> down -> next layer's QKV).
+    const int nl = c.n_layers;
+    std::vector<L2Prefetch> plan((size_t)4 * nl + 1);  // [4l + i]: GEMV i of layer l; the last: none
+    if (l2_prefetch_enabled()) {
+        for (int l = 0; l < nl; l++) {
+            for (int i = 0; i < 4; i++) {
+                l2_plan_out = &plan[4 * l + i];
+                hipError_t pe = i == 0 ? gemv_qkv(l) : i == 1 ? gemv_wo(l) : i == 2 ? gemv_gu(l) : gemv_down(l);
+                l2_plan_out = nullptr;
+                if (pe != hipSuccess) return pe;
+            }
+        }
+    }
+    TRY(launch_embed(m->embed, d, m->prompt, m->state, m->x, s));
+    for (int l = 0; l < nl; l++) {
+        const auto& L = m->layers[l];
+        l2_next = &plan[4 * l + 1];
+        e = gemv_qkv(l);
+        l2_next = nullptr;
+        TRY(e);
         AttnArgs a{};
         a.q = q;
         a.k = k;
@@ -224,27 +268,19 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.scale = (float)(1.0 / sqrt((double)c.head_dim));  // attn.go:311-314
         a.fused = 1;
         a.isa = m->isa;
-        const bool qattn = (c.head_dim & 31) == 0;  // whole int8 blocks per head
         a.q_out = qattn ? m->qx : nullptr;
         a.q_scale = qattn ? m->xs : nullptr;
         a.counters = m->attn_counters;
         TRY(attention_cache(m, l, a, s));
         TRY(launch_attention_decode(a, s));
-        // attn.go:417 Wo on the re-quantised attention output (quantised by the
-        // attention kernel), residual folded in
-        float* xo[1] = {m->x};
-        if (qattn)
-            TRY(launch_k4_gemv_w4a8(&L.wo, xo, 1, m->q_dim, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
-        else
-            TRY(launch_k4_gemv_w4a8_fused(&L.wo, xo, 1, m->q_dim, m->attn, nullptr, 0.0f, m->isa, 1, kEpiResAdd,
-                                          nullptr, s));
-        // ffn.go:18-91: RMSNorm, up/gate on one int8 activation, SiLU*up (also
-        // quantised for down), down + residual
-        K4Mat gu[2] = {L.gate, L.up};
-        float* ao[2] = {m->act, m->act};
-        TRY(launch_k4_gemv_w4a8_fused(gu, ao, 2, d, m->x, L.ffn_norm, c.eps, m->isa, 1, kEpiSiluMul, nullptr, s,
-                                      m->qx, m->xs));
-        TRY(launch_k4_gemv_w4a8(&L.down, xo, 1, c.ffn, m->qx, m->xs, 1, kEpiResAdd, nullptr, s));
+        l2_next = &plan[4 * l + 2];
+        e = gemv_wo(l);
+        l2_next = &plan[4 * l + 3];
+        if (e == hipSuccess) e = gemv_gu(l);
+        l2_next = &plan[4 * l + 4];
+        if (e == hipSuccess) e = gemv_down(l);
+        l2_next = nullptr;
+        TRY(e);
     }
     // runtime_greedy.go:53-67: final RMSNorm, lm_head, argmax (first max wins)
     float* lo[1] = {m->logits};
