@@ -27,63 +27,8 @@ struct GemvParams {
     unsigned long long* key;
     int8_t* q_out;   // kEpiSiluMul: output also quantised (32-row units) ...
     float* q_scale;  // ... with these block scales
-    L2Prefetch pf;   // the next GEMV's weights (pf.nmat == 0: none)
 };
 
-// Issue this workgroup's share of the prefetch (at most PF loads per thread,
-// results in v, to be consumed at the kernel's end so the loads stay in
-// flight meanwhile).  The workgroups of XCD class c = b mod 8 fetch the
-// lines of the consumer units that run on workgroups of the same class.
-template <int PF, int NT>
-__device__ __forceinline__ void l2_prefetch_issue(const L2Prefetch& pf, uint32_t (&v)[PF]) {
-#pragma unroll
-    for (int s = 0; s < PF; s++) v[s] = 0;
-    if (pf.nmat == 0) return;
-    const int b = (int)blockIdx.x, G = (int)gridDim.x, c = b & 7;
-    if (c >= pf.grid) return;
-    const int nc = (G - c + 7) >> 3, k = b >> 3;
-    const int nwc = (pf.grid - c + 7) >> 3;  // consumer workgroups of class c
-    const float inv_nwc = 1.0f / (float)nwc;
-    const int total = nwc * pf.per * pf.nsub * pf.lines;
-    const int tid = (int)threadIdx.x;
-#pragma unroll
-    for (int s = 0; s < PF; s++) {
-        const int f0 = (k + s * nc) * NT;
-        if (f0 + (tid & ~63) >= total) break;  // wave-uniform
-        int f = f0 + tid;
-        bool ok = f < total;
-        f = ok ? f : 0;
-        int t = (int)((float)f * pf.inv_lines);
-        int l = f - t * pf.lines;
-        if (l < 0) { t--; l += pf.lines; } else if (l >= pf.lines) { t++; l -= pf.lines; }
-        const int m = pf.nsub == 2 ? (t & 1) : 0;
-        const int t2 = pf.nsub == 2 ? (t >> 1) : t;
-        int i = (int)((float)t2 * inv_nwc);
-        int w = t2 - i * nwc;
-        if (w < 0) { i--; w += nwc; } else if (w >= nwc) { i++; w -= nwc; }
-        const int u = c + 8 * w + i * pf.grid;
-        ok = ok && u < pf.units;
-        int ms = m, first = 0;
-        if (pf.nsub == 1) {
-            if (pf.nmat > 1 && u >= pf.wg_begin[1]) { ms = 1; first = pf.wg_begin[1]; }
-            if (pf.nmat > 2 && u >= pf.wg_begin[2]) { ms = 2; first = pf.wg_begin[2]; }
-        }
-        const K4Mat M = ms == 0 ? pf.mats[0] : (ms == 1 ? pf.mats[1] : pf.mats[2]);
-        const int row0 = (u - first) * pf.rpu;
-        const uint8_t* a;
-        if (l < pf.nib_lines) {
-            ok = ok && row0 + (l * 8) / pf.bpr < M.rows;
-            a = M.nib + ((size_t)row0 * pf.bpr * 16 + (size_t)l * 128);
-        } else if (l == pf.nib_lines) {
-            a = M.sub + (size_t)row0 * pf.bpr;
-        } else {
-            a = reinterpret_cast<const uint8_t*>(M.sup + (size_t)row0 * (pf.bpr / 8));
-        }
-        ok = ok && row0 < M.rows;
-        a = ok ? a : pf.mats[0].nib;
-        v[s] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(a) & ~(uintptr_t)3);
-    }
-}
 
 // kModeW4A8: activation already quantised (qx/xs); kModeW4A32: fp32 activation
 // used as is; kModeW4A8Fused: every workgroup quantises the fp32 activation

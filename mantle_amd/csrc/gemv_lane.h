@@ -473,25 +473,6 @@ static hipError_t launch_lane_gemv(GemvParams& p, hipStream_t stream) {
     if (gemv_max_wgs() > 0) slots = gemv_max_wgs();
     const int per = (units + slots - 1) / slots;
     const int grid = (units + per - 1) / per;
-    if (l2_plan_out) {  // record where each unit's weights will be read; no launch
-        L2Prefetch& f = *l2_plan_out;
-        f = L2Prefetch{};
-        for (int i = 0; i < p.nmat; i++) f.mats[i] = p.mats[i];
-        f.nmat = p.nmat;
-        f.nsub = EPI == kEpiSiluMul ? 2 : 1;
-        f.bpr = p.bpr;
-        f.rpu = RPU;
-        f.grid = grid;
-        f.units = units;
-        f.per = per;
-        for (int i = 0; i < 4; i++) f.wg_begin[i] = p.wg_begin[i];
-        f.nib_lines = RPU * p.bpr / 8;
-        f.lines = f.nib_lines + 2;
-        f.inv_lines = 1.0f / (float)f.lines;
-        return hipSuccess;
-    }
-    if (l2_next) p.pf = *l2_next;
-    else p.pf.nmat = 0;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), smem, stream, p);
     return hipGetLastError();
 }

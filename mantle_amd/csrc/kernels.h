@@ -21,34 +21,6 @@ struct K4Mat {
     int rows;
 };
 
-// The weights of the decode step's next GEMV, fetched by the current kernel
-// into the L2 of the XCD that will read them.  Workgroup b of every launch
-// runs on the XCD of b mod 8 (the dispatcher deals workgroups round-robin
-// over the 8 XCDs, starting afresh at each launch), and the L2 is not
-// flushed of clean lines between kernels, so the consumer's first weight
-// loads hit its own L2 (~0.8 us) instead of HBM (~1.8 us).  The consumer's
-// unit u (rpu consecutive rows) runs on workgroup u mod grid.
-struct L2Prefetch {
-    K4Mat mats[3];
-    int nmat;        // 0: nothing to fetch
-    int nsub;        // 2: every unit covers rows of mats[0] and mats[1] (gate and up)
-    int bpr, rpu, grid, units, per;  // per: units per consumer workgroup (at most)
-    int wg_begin[4];                 // first unit of each matrix (nsub == 1)
-    int nib_lines;                   // 128-byte nibble lines per unit per matrix
-    int lines;                       // nib_lines + 2 (one u6 line, one super line)
-    float inv_lines;
-};
-
-// Host side of the L2 prefetch (one decode step is enqueued by one thread):
-// while l2_plan_out is set, a lane-GEMV launch records its unit layout there
-// instead of launching; while l2_next is set, a lane-GEMV launch carries it.
-extern thread_local L2Prefetch* l2_plan_out;
-extern thread_local const L2Prefetch* l2_next;
-
-// MANTLE_HIP_L2_PREFETCH=1 turns the decode step's L2 prefetch on (off by
-// default: measured slower, the prefetch address work delays each kernel).
-bool l2_prefetch_enabled();
-
 // Region pointers of a k4 payload that starts at `payload`.
 K4Mat k4_mat_from_payload(const uint8_t* payload, int rows, int cols);
 int64_t k4_payload_size(int64_t rows, int64_t cols);

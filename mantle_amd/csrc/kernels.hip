@@ -346,16 +346,6 @@ static int choose_rpw(int total_rows, int bpr, int nsub, int batch, size_t fixed
     return rpw < rmax ? rpw : rmax;
 }
 
-thread_local L2Prefetch* l2_plan_out = nullptr;
-thread_local const L2Prefetch* l2_next = nullptr;
-bool l2_prefetch_enabled() {
-    static bool v = [] {
-        const char* e = getenv("MANTLE_HIP_L2_PREFETCH");
-        return e && atoi(e) != 0;
-    }();
-    return v;
-}
-
 template <int MODE, int EPI>
 static hipError_t launch_gemv_epi(GemvParams& p, hipStream_t stream) {
     constexpr int nsub = EPI == kEpiSiluMul ? 2 : 1;
@@ -462,7 +452,7 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
     p.key = argmax_key;
     bool used = false;
     hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
-    if (used || l2_plan_out) return e;  // planning: the tile kernel has no plan (none recorded)
+    if (used) return e;
     const int fit = tile_batch_fit(p.bpr, 17 * 4);
     if (batch > fit) {  // store epilogue only (batch > 1)
         for (int b0 = 0; b0 < batch; b0 += fit) {
@@ -508,7 +498,7 @@ hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int 
     p.q_scale = q_scale;
     bool used = false;
     hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
-    if (used || l2_plan_out) return e;  // planning: the tile kernel has no plan (none recorded)
+    if (used) return e;
     const int fit = tile_batch_fit(p.bpr, norm_w ? ((size_t)p.bpr * 32 + 17) * 4 : 17 * 4);
     if (batch > fit) {  // store epilogue only (batch > 1)
         for (int b0 = 0; b0 < batch; b0 += fit) {

@@ -228,27 +228,11 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
     auto gemv_down = [&](int l) {
         return launch_k4_gemv_w4a8(&m->layers[l].down, xo, 1, c.ffn, m->qx, m->xs, 1, kEpiResAdd, nullptr, s);
     };
-    // Each GEMV fetches the next one's weights into the L2s that will read
-    // them (QKV -> Wo -> gate/up -> down -> next layer's QKV).
     const int nl = c.n_layers;
-    std::vector<L2Prefetch> plan((size_t)4 * nl + 1);  // [4l + i]: GEMV i of layer l; the last: none
-    if (l2_prefetch_enabled()) {
-        for (int l = 0; l < nl; l++) {
-            for (int i = 0; i < 4; i++) {
-                l2_plan_out = &plan[4 * l + i];
-                hipError_t pe = i == 0 ? gemv_qkv(l) : i == 1 ? gemv_wo(l) : i == 2 ? gemv_gu(l) : gemv_down(l);
-                l2_plan_out = nullptr;
-                if (pe != hipSuccess) return pe;
-            }
-        }
-    }
     TRY(launch_embed(m->embed, d, m->prompt, m->state, m->x, s));
     for (int l = 0; l < nl; l++) {
         const auto& L = m->layers[l];
-        l2_next = &plan[4 * l + 1];
-        e = gemv_qkv(l);
-        l2_next = nullptr;
-        TRY(e);
+        TRY(gemv_qkv(l));
         AttnArgs a{};
         a.q = q;
         a.k = k;
@@ -273,14 +257,9 @@ static hipError_t enqueue_step(mantleHipModel* m, hipStream_t s) {
         a.counters = m->attn_counters;
         TRY(attention_cache(m, l, a, s));
         TRY(launch_attention_decode(a, s));
-        l2_next = &plan[4 * l + 2];
-        e = gemv_wo(l);
-        l2_next = &plan[4 * l + 3];
-        if (e == hipSuccess) e = gemv_gu(l);
-        l2_next = &plan[4 * l + 4];
-        if (e == hipSuccess) e = gemv_down(l);
-        l2_next = nullptr;
-        TRY(e);
+        TRY(gemv_wo(l));
+        TRY(gemv_gu(l));
+        TRY(gemv_down(l));
     }
     // runtime_greedy.go:53-67: final RMSNorm, lm_head, argmax (first max wins)
     float* lo[1] = {m->logits};
