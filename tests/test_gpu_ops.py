@@ -33,6 +33,21 @@ def test_rmsnorm_bitexact(hip, oracle, isa, n):
 
 
 @pytest.mark.parametrize("isa", ISAS)
+@pytest.mark.parametrize("n", [32, 64, 1024])
+def test_rmsnorm_lane_order_kat(hip, oracle, isa, n):
+    """x = [4096, 1, 1, ...]: 2^24 + 1 rounds back to 2^24, so each ISA order
+    gives a different sum of squares (tests/test_oracle.py pins the oracle on
+    it by hand-worked sums); the kernel must match the selected order."""
+    x = np.ones(n, dtype=np.float32)
+    x[0] = 4096.0
+    w = np.ones(n, dtype=np.float32)
+    g.call("mantleHipSetParityISA", isa)
+    out = g.empty(n)
+    g.call("mantleHipRMSNormF32", g.ptr(out), g.ptr(g.keep(x)), g.ptr(g.keep(w)), ctypes.c_float(0.0), n, g.stream())
+    g.assert_bitexact(g.host(out), oracle.rmsnorm(isa, x, w, 0.0), f"rmsnorm KAT isa={isa} n={n}")
+
+
+@pytest.mark.parametrize("isa", ISAS)
 def test_rmsnorm_batched_bitexact(hip, oracle, isa):
     hd, nh = 128, 16
     rng = np.random.default_rng(isa)

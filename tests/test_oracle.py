@@ -219,6 +219,63 @@ def test_rmsnorm_kat_and_float64(isa):
         np.testing.assert_allclose(o.rmsnorm(isa, x, w, 1e-6), want, rtol=2e-6, atol=2e-6)
 
 
+def test_rmsnorm_lane_order_kat():
+    """The three RMSNorm reduction orders give different bits (rmsNormAVX512,
+    ops_avx512.go:98-108: 16 FMA lanes over 16-wide steps, lanes added left to
+    right; rmsNormSIMD, ops_avx2.go:66-76: 8 lanes; rmsNormScalar, ops.go:73-76:
+    one running sum).  x = [4096, 1 x 31]: 4096^2 = 2^24, and 2^24 + 1 rounds
+    back to 2^24 (ties to even), so a 1 added straight onto 2^24 is lost while
+    ones summed in a lane first survive.  Hand-worked sums of squares:
+      scalar  2^24 + 1 + ... + 1, every 1 lost            -> 16777216
+      AVX2    lane 0: 2^24 (+1 lost x3); lanes 1-7 hold 4 -> 2^24 + 28
+      AVX-512 lane 0: 2^24 (+1 lost);    lanes 1-15 hold 2 -> 2^24 + 30"""
+    x = np.ones(32, dtype=np.float32)
+    x[0] = 4096.0
+    w = np.ones(32, dtype=np.float32)
+    sums = {0: 16777216.0, 1: 16777216.0 + 28, 2: 16777216.0 + 30}
+    outs = {}
+    for isa, ssq in sums.items():
+        mean = np.float32(ssq) / np.float32(32)
+        scale = np.float32(1.0) / np.float32(math.sqrt(float(np.float32(mean + np.float32(0.0)))))
+        want = (x * scale).astype(np.float32) * w
+        outs[isa] = o.rmsnorm(isa, x, w, 0.0)
+        np.testing.assert_array_equal(outs[isa], want)
+    # the orders are distinguishable through the output bits
+    assert outs[0][1] != outs[1][1] != outs[2][1] != outs[0][1]
+
+
+def test_fast_exp_range_reduction_kat():
+    """fastExp (ops.go:108-150) takes k = int32(x*ln2Inv + 0.5) (x*ln2Inv - 0.5
+    for x < 0, truncated toward zero), fastExpVec (ops_avx2.go:98-128)
+    RoundToEven(x*ln2Inv).  At x = 1.7328680 (float32), x*ln2Inv is exactly
+    2.5: fastExp takes k = 3 (r = x - 3 ln2 < 0), fastExpVec k = 2 (r > 0),
+    and the two approximations differ.  Same at -x with k = -3 / -2.  At
+    x*ln2Inv = 3.5 both give k = 4."""
+    f = np.float32
+    ln2, ln2inv = f(0.693147180559945309417), f(1.44269504088896340736)
+    x = f(1.732867956161499)
+    assert f(x * ln2inv) == f(2.5)
+
+    def with_k(xv, k, vec):
+        r = f(xv - f(f(k) * ln2))
+        r2 = f(r * r); r3 = f(r2 * r); r4 = f(r2 * r2); r5 = f(r4 * r)
+        poly = f(f(f(f(f(f(1.0) + r) + f(r2 * f(0.5))) + f(r3 * f(0.16666667))) + f(r4 * f(0.041666667)))
+                 + f(r5 * f(0.008333333)))
+        return float(f(poly * f(2.0 ** k)))
+
+    for sgn in (1, -1):
+        xv = f(sgn * x)
+        k_trunc, k_even = 3 * sgn, 2 * sgn
+        assert o.fast_exp(float(xv)) == with_k(xv, k_trunc, False)
+        assert o.fast_exp_vec(float(xv)) == with_k(xv, k_even, True)
+        assert o.fast_exp(float(xv)) != o.fast_exp_vec(float(xv))
+    x35 = f(3.5 / 1.44269504088896340736)
+    while f(x35 * ln2inv) != f(3.5):
+        x35 = np.nextafter(x35, f(10), dtype=np.float32)
+    assert o.fast_exp(float(x35)) == with_k(x35, 4, False)
+    assert o.fast_exp_vec(float(x35)) == with_k(x35, 4, True)
+
+
 # -------------------------------------------------- exp / softmax / silu ----
 def test_fast_exp_kat_and_accuracy():
     assert o.fast_exp(0.0) == 1.0
