@@ -140,9 +140,10 @@ int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, cons
  * with scale max|x|/127 over all kvStride values (kvStride <= 4096). */
 int mantleHipStoreKVQ8Row(int8_t* cacheK, int8_t* cacheV, float* kScales, float* vScales, const float* k,
                           const float* v, int cachePos, int kvStride, mantleHipStream_t stream);
-/* KV cache element type of models loaded afterwards (LoadModelOptions.CacheTypeK/V,
- * internal/backend/core/load_options.go:7-8): MANTLE_HIP_KV_F32, MANTLE_HIP_KV_F16 or
- * MANTLE_HIP_KV_Q8_0 (K and V of one type). */
+/* KV cache element type of models loaded afterwards by the entry points without options
+ * (LoadModelOptions.CacheTypeK/V, internal/backend/core/load_options.go:7-8):
+ * MANTLE_HIP_KV_F32, MANTLE_HIP_KV_F16 or MANTLE_HIP_KV_Q8_0, K and V of one type.
+ * Process-wide: prefer mantleHipModelLoadMCFWithOptions, which also takes mixed types. */
 #define MANTLE_HIP_KV_F32 0
 #define MANTLE_HIP_KV_F16 1
 #define MANTLE_HIP_KV_Q8_0 2
@@ -216,6 +217,24 @@ int mantleHipMCFSection(const mantleHipMCF* f, uint32_t type, const uint8_t** da
  * internal/backend/core/interfaces.go:4-18) for the k4 decode path. */
 typedef struct mantleHipModel mantleHipModel;
 int mantleHipModelLoadMCF(const char* path, int maxContext, mantleHipModel** out);
+/* Backend.LoadModel's core.LoadModelOptions (internal/backend/core/load_options.go:5-13),
+ * per model instead of process-wide: cacheTypeK / cacheTypeV (--cache-type-k / --cache-type-v,
+ * cmd/mantle/run.go:183-195, independent: MANTLE_HIP_KV_*), parityIsa (the host ISA whose
+ * reduction order Mantle's CPU path would use, tensor_cpu.go:18-24: 0 scalar, 1 AVX2,
+ * 2 AVX-512; HostCaps stands in for it) and useGraph (UseGraph: replay the captured decode
+ * step).  The entry points without options take mantleHipSetParityISA /
+ * mantleHipSetKVCacheType's current values and useGraph 1. */
+typedef struct mantleHipLoadOptions {
+    int cache_type_k;
+    int cache_type_v;
+    int parity_isa;
+    int use_graph;
+    int reserved[4];
+} mantleHipLoadOptions;
+int mantleHipModelLoadMCFWithOptions(const char* path, int maxContext, const mantleHipLoadOptions* opts,
+                                     mantleHipModel** out);
+int mantleHipModelLoadMCFImageWithOptions(const uint8_t* data, uint64_t size, int maxContext,
+                                          const mantleHipLoadOptions* opts, mantleHipModel** out);
 /* Same, from an MCF image the caller already holds in memory (Mantle keeps the file mmapped:
  * pkg/mcf/reader.go:21-69); the image is only read during the call. */
 int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, int maxContext, mantleHipModel** out);

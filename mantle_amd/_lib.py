@@ -30,6 +30,11 @@ class Qwen3Config(C.Structure):
 
 
 # name -> (restype, argtypes)
+class LoadOptions(C.Structure):
+    """mantleHipLoadOptions: core.LoadModelOptions (internal/backend/core/load_options.go:5-13)."""
+    _fields_ = [("cache_type_k", I), ("cache_type_v", I), ("parity_isa", I), ("use_graph", I), ("reserved", I * 4)]
+
+
 _SIGS = {
     "mantleHipGetErrorString": (C.c_char_p, [I]),
     "mantleHipGetDeviceCount": (I, [C.POINTER(I)]),
@@ -75,6 +80,8 @@ _SIGS = {
     "mantleHipMCFSection": (I, [P, C.c_uint32, C.POINTER(P), C.POINTER(U64)]),
     "mantleHipModelLoadMCF": (I, [C.c_char_p, I, C.POINTER(P)]),
     "mantleHipModelLoadMCFImage": (I, [P, U64, I, C.POINTER(P)]),
+    "mantleHipModelLoadMCFWithOptions": (I, [C.c_char_p, I, C.POINTER(LoadOptions), C.POINTER(P)]),
+    "mantleHipModelLoadMCFImageWithOptions": (I, [P, U64, I, C.POINTER(LoadOptions), C.POINTER(P)]),
     "mantleHipModelClose": (None, [P]),
     "mantleHipModelConfig": (I, [P, C.POINTER(Qwen3Config)]),
     "mantleHipModelReset": (I, [P]),

@@ -12,7 +12,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import I, P, Qwen3Config, call, lib
+from ._lib import I, LoadOptions, P, Qwen3Config, call, lib
 
 ISA = {"scalar": 0, "avx2": 1, "avx512": 2}
 
@@ -30,25 +30,38 @@ class Backend:
         return "hip"
 
     def load_model(self, path: str, max_context: int = 4096, parity_isa: str = "avx512",
-                   kv_cache: str = "f32") -> "Runtime":
-        """kv_cache: "f32" (Mantle's loader default), "f16" (`mantle run`'s
-        --cache-type-k/v default, cmd/mantle/run.go:183-195) or "q8_0"."""
-        call("mantleHipSetParityISA", ISA[parity_isa])
-        call("mantleHipSetKVCacheType", {"f32": 0, "f16": 1, "q8_0": 2}[kv_cache])
+                   kv_cache: str = "f32", kv_cache_k: str | None = None, kv_cache_v: str | None = None,
+                   use_graph: bool = True) -> "Runtime":
+        """LoadModel with core.LoadModelOptions (internal/backend/core/load_options.go:5-13),
+        per model: kv_cache "f32" (Mantle's loader default), "f16" (`mantle run`'s
+        --cache-type-k/v default, cmd/mantle/run.go:183-195) or "q8_0" for both
+        caches, or kv_cache_k / kv_cache_v separately."""
+        opts = _options(parity_isa, kv_cache_k or kv_cache, kv_cache_v or kv_cache, use_graph)
         h = P()
-        try:
-            call("mantleHipModelLoadMCF", path.encode(), int(max_context), C.byref(h))
-        finally:
-            call("mantleHipSetKVCacheType", 0)
+        call("mantleHipModelLoadMCFWithOptions", path.encode(), int(max_context), C.byref(opts), C.byref(h))
         return Runtime(h, max_context)
 
-    def load_model_image(self, image, max_context: int = 4096, parity_isa: str = "avx512") -> "Runtime":
+    def load_model_image(self, image, max_context: int = 4096, parity_isa: str = "avx512",
+                         kv_cache: str = "f32", kv_cache_k: str | None = None, kv_cache_v: str | None = None,
+                         use_graph: bool = True) -> "Runtime":
         """LoadModel from an MCF image already in memory (bytes / numpy uint8)."""
-        call("mantleHipSetParityISA", ISA[parity_isa])
+        opts = _options(parity_isa, kv_cache_k or kv_cache, kv_cache_v or kv_cache, use_graph)
         buf = np.frombuffer(image, dtype=np.uint8) if not isinstance(image, np.ndarray) else image
         h = P()
-        call("mantleHipModelLoadMCFImage", buf.ctypes.data, C.c_uint64(buf.nbytes), int(max_context), C.byref(h))
+        call("mantleHipModelLoadMCFImageWithOptions", buf.ctypes.data, C.c_uint64(buf.nbytes), int(max_context),
+             C.byref(opts), C.byref(h))
         return Runtime(h, max_context)
+
+
+KV = {"f32": 0, "f16": 1, "q8_0": 2}
+
+
+def _options(isa: str, k: str, v: str, use_graph: bool) -> LoadOptions:
+    if isa not in ISA or k not in KV or v not in KV:
+        raise ValueError(f"bad load options isa={isa!r} kv_cache_k={k!r} kv_cache_v={v!r}")
+    o = LoadOptions()
+    o.cache_type_k, o.cache_type_v, o.parity_isa, o.use_graph = KV[k], KV[v], ISA[isa], int(bool(use_graph))
+    return o
 
 
 class Runtime:

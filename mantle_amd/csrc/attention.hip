@@ -563,7 +563,8 @@ __device__ __forceinline__ void prep_finish(const AttnArgs& a, PrepRegs r, int k
     if (wave >= 3) return;
     float x0 = r.x0, x1 = r.x1;
     prep_pair<HD>(x0, x1, r.g0, r.g1, r.cs, r.sn, r.has_norm, r.rope && wave < 2, a.eps, a.isa, wbuf + wave * 128);
-    if (a.kv_f16 && wave > 0) {  // the f16 cache holds (and the step reads back) the rounded row
+    const int ctype = wave == 1 ? a.k_type : a.v_type;  // this wave's cache (waves 1 and 2)
+    if (wave > 0 && ctype == kKvF16) {  // the f16 cache holds (and the step reads back) the rounded row
         x0 = f16_cache_round(x0);
         x1 = f16_cache_round(x1);
     }
@@ -571,8 +572,8 @@ __device__ __forceinline__ void prep_finish(const AttnArgs& a, PrepRegs r, int k
         float* dst = wave == 0 ? sq : (wave == 1 ? sk : sv);
         dst[lane] = x0;
         dst[lane + half] = x1;
-        if (a.fused && wave > 0 && append) {
-            if (a.kv_f16) {
+        if (a.fused && wave > 0 && append && ctype != kKvQ8) {  // (q8_0 rows: launch_kv_append_q8)
+            if (ctype == kKvF16) {
                 uint16_t* c16 = reinterpret_cast<uint16_t*>(wave == 1 ? a.cache_k : a.cache_v);
                 const uint16_t h0 = mantle_f32_to_f16_trunc(x0), h1 = mantle_f32_to_f16_trunc(x1);
                 if (wave == 2 && a.vt_stride > 0) {
@@ -882,7 +883,7 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
         else chunk_issue_t<HD>(ck, kbase, a.kv_stride, c * kc, nk, HD, kp, skip);
     };
     issue(sidx);
-    prep_finish<HD>(a, pr, kvh, pos, a.fused && !Q8 && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
+    prep_finish<HD>(a, pr, kvh, pos, a.fused && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
     __syncthreads();
     for (int c = sidx; c < nchunks; c += S) {
         const int t0 = c * kc;
@@ -1467,17 +1468,20 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     const bool split_ok = fast_hd && a.scores && (mode == kAttnPathSplit || mode == kAttnPathFused);
     if (vt && (!split_ok || (a.vt_stride & 3) || a.vt_stride < (a.max_ctx + 3) / 4 * 4))
         return hipErrorInvalidValue;  // the transposed V cache is read by the split kernels only
-    if (a.kv_f16 && !split_ok) return hipErrorInvalidValue;  // the f16 cache is read by the split kernels only
-    if (a.kv_q8) {
-        // the q8_0 cache: the two-launch split form only, 16-byte int8 rows
-        // and (transposed V) 16-key groups of a column
-        if (!split_ok || a.kv_f16 || a.max_ctx > kSplitMaxCtx || !a.k_scale || !a.v_scale || (a.kv_stride & 15) ||
-            (a.head_stride & 15) || (vt && ((a.vt_stride & 15) || a.vt_stride < (a.max_ctx + 15) / 16 * 16)))
-            return hipErrorInvalidValue;
-    }
-    const bool f16 = a.kv_f16 != 0;
-    const int kvt = a.kv_q8 ? kKvQ8 : (f16 ? kKvF16 : kKvF32);
-    if (split_ok && !a.kv_q8 && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
+    const int kt = a.k_type, vtt = a.v_type;  // cache element types of K and V
+    if (kt < kKvF32 || kt > kKvQ8 || vtt < kKvF32 || vtt > kKvQ8) return hipErrorInvalidValue;
+    if ((kt != kKvF32 || vtt != kKvF32) && !split_ok)
+        return hipErrorInvalidValue;  // f16 / q8_0 caches are read by the split kernels only
+    const bool any_q8 = kt == kKvQ8 || vtt == kKvQ8;
+    if (kt == kKvQ8 && (!a.k_scale || (a.kv_stride & 15) || (a.head_stride & 15))) return hipErrorInvalidValue;
+    if (vtt == kKvQ8 && (!a.v_scale || (!vt && ((a.kv_stride & 15) || (a.head_stride & 15))) ||
+                         (vt && ((a.vt_stride & 15) || a.vt_stride < (a.max_ctx + 15) / 16 * 16))))
+        return hipErrorInvalidValue;  // 16-byte int8 rows, (transposed V) 16-key groups of a column
+    // q8_0 and mixed caches: the two-launch split form only
+    if ((any_q8 || kt != vtt) && a.max_ctx > kSplitMaxCtx) return hipErrorInvalidValue;
+    const bool f16 = kt == kKvF16;
+    const int kvt = kt;
+    if (split_ok && !any_q8 && kt == vtt && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
         AttnArgs f = a;
         if (!f.counters) f.counters = library_counters(a.n_head);
         if (!f.counters) return hipErrorInvalidValue;
@@ -1519,10 +1523,10 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
             {attention_scores_split<64, kKvF32>, attention_scores_split<64, kKvF16>, attention_scores_split<64, kKvQ8>},
             {attention_scores_split<128, kKvF32>, attention_scores_split<128, kKvF16>,
              attention_scores_split<128, kKvQ8>}};
-        auto pvk = pv[a.head_dim == 128][vt][kvt];
+        auto pvk = pv[a.head_dim == 128][vt][vtt];
         size_t smem_pv = smem_b;
         const size_t pcap = (size_t)(a.max_ctx + 31) / 32 * 32;
-        const size_t smem_lv = sizeof(float) * (pcap + 32 + 2 * 32 * kPvPitch + (a.kv_q8 ? 2 * kPvChunk : 0));
+        const size_t smem_lv = sizeof(float) * (pcap + 32 + 2 * 32 * kPvPitch + (vtt == kKvQ8 ? 2 * kPvChunk : 0));
         // (short caches keep the register ring: at a few hundred keys the
         // loader waves' barriers cost more than they save, 6.30 -> 6.55 us)
         const bool lv_used = vt && a.max_ctx > kPvLdsMinCtx && smem_lv <= kMaxLds && pv_lds_enabled();
@@ -1530,11 +1534,11 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
             void (*const lv[2][3])(AttnArgs) = {
                 {attention_pv_lds<64, kKvF32>, attention_pv_lds<64, kKvF16>, attention_pv_lds<64, kKvQ8>},
                 {attention_pv_lds<128, kKvF32>, attention_pv_lds<128, kKvF16>, attention_pv_lds<128, kKvQ8>}};
-            pvk = lv[a.head_dim == 128][kvt];
+            pvk = lv[a.head_dim == 128][vtt];
             smem_pv = smem_lv;
         }
         const size_t smem_sl = sizeof(float) * (2 * ((size_t)(a.max_ctx + 31) / 32 * 32) + 32);
-        if (!lv_used && a.kv_q8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
+        if (!lv_used && vtt == kKvQ8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
             void (*const pvs[2][2])(AttnArgs) = {
                 {attention_pv_split<64, false, kKvQ8, true>, attention_pv_split<64, true, kKvQ8, true>},
                 {attention_pv_split<128, false, kKvQ8, true>, attention_pv_split<128, true, kKvQ8, true>}};
@@ -1632,19 +1636,22 @@ __global__ __launch_bounds__(kThreads) void kv_append_q8_kernel(KvQ8Args a) {
     for (int i = tid; i < n; i += kThreads) {
         const int g = i / a.head_dim, d = i - g * a.head_dim;
         const size_t row = (size_t)g * a.head_stride + (size_t)pos * a.row_stride + d;
-        a.cache_k[row] = max_k == 0.0f ? (int8_t)0 : q8_store_value(sk[i], inv_k);
-        const int8_t qv = max_v == 0.0f ? (int8_t)0 : q8_store_value(sv[i], inv_v);
-        if (a.vt_stride > 0) a.cache_v[(size_t)i * a.vt_stride + pos] = qv;
-        else a.cache_v[row] = qv;
+        if (!a.skip_k) a.cache_k[row] = max_k == 0.0f ? (int8_t)0 : q8_store_value(sk[i], inv_k);
+        if (!a.skip_v) {
+            const int8_t qv = max_v == 0.0f ? (int8_t)0 : q8_store_value(sv[i], inv_v);
+            if (a.vt_stride > 0) a.cache_v[(size_t)i * a.vt_stride + pos] = qv;
+            else a.cache_v[row] = qv;
+        }
     }
     if (tid == 0) {
-        a.k_scale[pos] = max_k / 127.0f;
-        a.v_scale[pos] = max_v / 127.0f;
+        if (!a.skip_k) a.k_scale[pos] = max_k / 127.0f;
+        if (!a.skip_v) a.v_scale[pos] = max_v / 127.0f;
     }
 }
 
 hipError_t launch_kv_append_q8(const KvQ8Args& a, hipStream_t stream) {
-    if (!a.k || !a.v || !a.cache_k || !a.cache_v || !a.k_scale || !a.v_scale || a.kv_heads <= 0 || a.head_dim <= 0 ||
+    if ((a.skip_k && a.skip_v) || !a.k || !a.v || (!a.skip_k && (!a.cache_k || !a.k_scale)) ||
+        (!a.skip_v && (!a.cache_v || !a.v_scale)) || a.kv_heads <= 0 || a.head_dim <= 0 ||
         a.kv_heads * a.head_dim > kKvQ8MaxRow || a.head_stride < 0 || a.row_stride < 0 || a.vt_stride < 0)
         return hipErrorInvalidValue;
     if (!a.pos_dev && a.pos_host < 0) return hipErrorInvalidValue;

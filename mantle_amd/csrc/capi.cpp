@@ -166,9 +166,9 @@ int mantleHipAttentionInnerF16CacheF32(const float* q, const uint16_t* cacheK, c
         return hipErrorInvalidValue;
     AttnArgs a{};
     a.q = q;
-    a.cache_k = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheK));  // f16 values (kv_f16)
+    a.cache_k = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheK));  // f16 values
     a.cache_v = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheV));
-    a.kv_f16 = 1;
+    a.k_type = a.v_type = kKvF16;
     a.scores = scoresScratch;
     a.out = out;
     a.pos_host = pos;
@@ -196,9 +196,9 @@ int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, cons
         return hipErrorInvalidValue;
     AttnArgs a{};
     a.q = q;
-    a.cache_k = reinterpret_cast<float*>(const_cast<int8_t*>(cacheK));  // int8 values (kv_q8)
+    a.cache_k = reinterpret_cast<float*>(const_cast<int8_t*>(cacheK));  // int8 values
     a.cache_v = reinterpret_cast<float*>(const_cast<int8_t*>(cacheV));
-    a.kv_q8 = 1;
+    a.k_type = a.v_type = kKvQ8;
     a.k_scale = kScales;
     a.v_scale = vScales;
     a.scores = scoresScratch;

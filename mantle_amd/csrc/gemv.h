@@ -47,8 +47,16 @@ enum GemvMode : int { kModeW4A8 = 0, kModeW4A32 = 1, kModeW4A8Fused = 2 };
 // kernel, or RMSNorm then quantised in the kernel.
 enum LanePro : int { kProQx = 0, kProQuant = 1, kProNorm = 2 };
 
+// 64-bit key whose maximum over (v, idx) pairs is argmaxHost's answer
+// (runtime_greedy.go:70-82: best = x[0], then x[i] > best): order-preserving
+// value bits, then -idx so the first maximum wins.  Strict '>' also makes -0
+// equal to +0 (mapped to +0 here) and never lets a NaN win: a NaN at index 0
+// is kept forever (the largest key), any other NaN takes key 0, below every
+// number (the smallest numeric key, -inf, is 0x007FFFFF...).
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
     uint32_t u = __float_as_uint(v);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return idx == 0 ? ~0ull : 0ull;
+    if (u == 0x80000000u) u = 0u;
     uint32_t s = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)s << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
 }

@@ -111,16 +111,17 @@ struct AttnArgs {
     int isa;
     int8_t* q_out;         // optional: out also as Mantle's int8 blocks (permuted layout) ...
     float* q_scale;        // ... and their scales, for the next W4A8 GEMV (head_dim % 32 == 0)
-    int kv_f16;            // cache_k / cache_v hold Mantle's truncating f16 (uint16) values
-                           // (--cache-type-k/v f16, split paths only)
+    int k_type, v_type;    // KvCacheType of cache_k / cache_v (--cache-type-k / --cache-type-v,
+                           // cmd/mantle/run.go:183-195; independent).  f16: Mantle's truncating f16
+                           // (uint16) values, split paths only.  q8_0: see k_scale below.
     int vt_stride;         // > 0: V is stored transposed, element (t, d) of kv head g at
                            // cache_v + (g*head_dim + d)*vt_stride + t (split paths only)
     unsigned* counters;    // [n_head] zeroed arrival counters of the one-launch split path (null: the
                            // library's own, for callers that serialise their launches on one stream)
-    int kv_q8;             // cache_k / cache_v hold int8 rows with one scale per position in
-    const float* k_scale;  // k_scale / v_scale [max_ctx] (--cache-type-k/v q8_0; two-launch split
-    const float* v_scale;  // path only).  The step's own rows must already be in the cache (fused:
-                           // q alone is prepared here, launch_kv_append_q8 prepares and appends K / V)
+    const float* k_scale;  // a q8_0 cache holds int8 rows with one scale per position in k_scale /
+    const float* v_scale;  // v_scale [max_ctx] (two-launch split path only).  Its step rows must
+                           // already be in the cache (fused: launch_kv_append_q8 prepares and
+                           // appends the q8_0 rows; this launch prepares q and the other rows)
 };
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
 // Decode-attention kernel variant for head_dim 64 / 128 (other sizes always
@@ -181,6 +182,7 @@ struct KvQ8Args {
     int vt_stride;  // > 0: V transposed, (g*head_dim + d)*vt_stride + t
     float *k_scale, *v_scale;  // [max_ctx]
     int prep;
+    int skip_k, skip_v;  // 1: that row is not a q8_0 cache (mixed cache types): left alone
 };
 static constexpr int kKvQ8MaxRow = 4096;  // kv_heads*head_dim: both rows staged in LDS
 hipError_t launch_kv_append_q8(const KvQ8Args& a, hipStream_t stream);

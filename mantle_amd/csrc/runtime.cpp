@@ -62,8 +62,9 @@ struct mantleHipModel {
     // keys contiguous, so the V sum loads four keys per 16 bytes.
     int vt_stride = 0;
     int v_rows = 0;  // per layer and kv column: max_ctx or vt_stride
-    int kv_f16 = 0;  // caches hold Mantle's truncating f16 (--cache-type-k/v f16)
-    int kv_q8 = 0;   // caches hold int8 rows, one scale per position (--cache-type-k/v q8_0)
+    int k_type = kKvF32, v_type = kKvF32;  // KvCacheType of the K / V caches (--cache-type-k / -v):
+                                           // f32, Mantle's truncating f16, or q8_0 int8 rows with
+                                           // one scale per position
     float *k_scale = nullptr, *v_scale = nullptr;  // q8_0: [layer][max_ctx]
     float *rope_cos = nullptr, *rope_sin = nullptr;
     DecodeState* state = nullptr;
@@ -75,9 +76,10 @@ struct mantleHipModel {
 };
 
 // Layer l's base in a KV cache of `rows` keys per kv column (f32, f16 or int8 elements).
-static float* layer_cache(const mantleHipModel* m, float* base, int l, int rows) {
+static size_t kv_elem_bytes(int type) { return type == kKvQ8 ? 1 : (type == kKvF16 ? 2 : 4); }
+static float* layer_cache(const mantleHipModel* m, float* base, int l, int rows, int type) {
     const size_t elems = (size_t)l * rows * m->kv_dim;
-    const size_t elem = m->kv_q8 ? 1 : (m->kv_f16 ? 2 : 4);
+    const size_t elem = kv_elem_bytes(type);
     return reinterpret_cast<float*>(reinterpret_cast<char*>(base) + elems * elem);
 }
 
@@ -86,16 +88,16 @@ static float* layer_cache(const mantleHipModel* m, float* base, int l, int rows)
 // then prepares q only and reads the step's rows from the cache).
 static hipError_t attention_cache(const mantleHipModel* m, int l, AttnArgs& a, hipStream_t s) {
     const mantleHipQwen3Config& c = m->cfg;
-    a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx);
-    a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows);
-    a.kv_f16 = m->kv_f16;
+    a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx, m->k_type);
+    a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows, m->v_type);
+    a.k_type = m->k_type;
+    a.v_type = m->v_type;
     a.vt_stride = m->vt_stride;
     a.kv_stride = c.head_dim;                 // head-major cache:
     a.head_stride = m->max_ctx * c.head_dim;  // [layer][kv_head][max_ctx][head_dim]
-    if (!m->kv_q8) return hipSuccess;
-    a.kv_q8 = 1;
-    a.k_scale = m->k_scale + (size_t)l * m->max_ctx;
-    a.v_scale = m->v_scale + (size_t)l * m->max_ctx;
+    if (m->k_type != kKvQ8 && m->v_type != kKvQ8) return hipSuccess;
+    if (m->k_type == kKvQ8) a.k_scale = m->k_scale + (size_t)l * m->max_ctx;
+    if (m->v_type == kKvQ8) a.v_scale = m->v_scale + (size_t)l * m->max_ctx;
     KvQ8Args q{};
     q.k = a.k;
     q.v = a.v;
@@ -115,6 +117,8 @@ static hipError_t attention_cache(const mantleHipModel* m, int l, AttnArgs& a, h
     q.k_scale = const_cast<float*>(a.k_scale);
     q.v_scale = const_cast<float*>(a.v_scale);
     q.prep = 1;
+    q.skip_k = m->k_type != kKvQ8;
+    q.skip_v = m->v_type != kKvQ8;
     return launch_kv_append_q8(q, s);
 }
 
@@ -336,10 +340,37 @@ extern "C" void mantleHipModelClose(mantleHipModel* m) {
 
 // LoadModelMCF (internal/backend/simd/loader.go:51-80 + internal/backend/cuda/cuda.go:39-73,
 // internal/backend/cuda/ops.go:5214-5313 weight residency).
-static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const char* path);
+static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions& o, mantleHipModel** out,
+                      const char* path);
+
+// The process-wide settings (mantleHipSetParityISA / mantleHipSetKVCacheType)
+// as load options, for the entry points that take none.
+static mantleHipLoadOptions default_options() {
+    mantleHipLoadOptions o{};
+    o.parity_isa = mantleHipGetParityISA();
+    o.cache_type_k = o.cache_type_v = kv_cache_type();
+    o.use_graph = 1;
+    return o;
+}
+
+static bool options_valid(const mantleHipLoadOptions* o) {
+    return o && o->parity_isa >= kIsaScalar && o->parity_isa <= kIsaAvx512 && o->cache_type_k >= kKvF32 &&
+           o->cache_type_k <= kKvQ8 && o->cache_type_v >= kKvF32 && o->cache_type_v <= kKvQ8;
+}
 
 extern "C" int mantleHipModelLoadMCF(const char* path, int max_ctx, mantleHipModel** out) {
+    return mantleHipModelLoadMCFWithOptions(path, max_ctx, nullptr, out);
+}
+
+extern "C" int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, int max_ctx, mantleHipModel** out) {
+    return mantleHipModelLoadMCFImageWithOptions(data, size, max_ctx, nullptr, out);
+}
+
+extern "C" int mantleHipModelLoadMCFWithOptions(const char* path, int max_ctx, const mantleHipLoadOptions* opts,
+                                                mantleHipModel** out) {
     if (!path || !out || max_ctx <= 0) return hipErrorInvalidValue;
+    const mantleHipLoadOptions o = opts ? *opts : default_options();
+    if (!options_valid(&o)) return hipErrorInvalidValue;
     *out = nullptr;
     McfFile f;
     std::string err;
@@ -347,11 +378,14 @@ extern "C" int mantleHipModelLoadMCF(const char* path, int max_ctx, mantleHipMod
         fprintf(stderr, "mantle_hip: %s: %s\n", path, err.c_str());
         return hipErrorInvalidValue;
     }
-    return load_model(f, max_ctx, out, path);
+    return load_model(f, max_ctx, o, out, path);
 }
 
-extern "C" int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, int max_ctx, mantleHipModel** out) {
+extern "C" int mantleHipModelLoadMCFImageWithOptions(const uint8_t* data, uint64_t size, int max_ctx,
+                                                     const mantleHipLoadOptions* opts, mantleHipModel** out) {
     if (!data || !out || max_ctx <= 0) return hipErrorInvalidValue;
+    const mantleHipLoadOptions o = opts ? *opts : default_options();
+    if (!options_valid(&o)) return hipErrorInvalidValue;
     *out = nullptr;
     McfFile f;
     std::string err;
@@ -359,10 +393,11 @@ extern "C" int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, in
         fprintf(stderr, "mantle_hip: MCF image: %s\n", err.c_str());
         return hipErrorInvalidValue;
     }
-    return load_model(f, max_ctx, out, "MCF image");
+    return load_model(f, max_ctx, o, out, "MCF image");
 }
 
-static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const char* path) {
+static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions& o, mantleHipModel** out,
+                      const char* path) {
     const McfSection* cs = f.section(kSecHFConfigJSON);
     if (!cs) {
         fprintf(stderr, "mantle_hip: %s: missing config.json section\n", path);
@@ -398,7 +433,8 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     c.eps = json_number(js, "rms_norm_eps", &v) ? (float)v : 1e-6f;
     c.tie_embeddings = f.find("lm_head.weight") < 0;
     m->max_ctx = max_ctx;
-    m->isa = mantleHipGetParityISA();
+    m->isa = o.parity_isa;
+    m->use_graph = o.use_graph != 0;
     m->q_dim = c.n_heads * c.head_dim;
     m->kv_dim = c.n_kv_heads * c.head_dim;
     if (c.head_dim > 256 || (c.head_dim & 1) || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads) {
@@ -538,31 +574,33 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     const size_t kv_elems = (size_t)c.n_layers * max_ctx * m->kv_dim;
     const int apath = attention_path();
     const bool split = (c.head_dim == 64 || c.head_dim == 128) && (apath == kAttnPathSplit || apath == kAttnPathFused);
-    m->kv_f16 = kv_cache_type() == kKvF16;
-    m->kv_q8 = kv_cache_type() == kKvQ8;
-    if ((m->kv_f16 || m->kv_q8) && !split) {
+    m->k_type = o.cache_type_k;
+    m->v_type = o.cache_type_v;
+    const bool any_q8 = m->k_type == kKvQ8 || m->v_type == kKvQ8;
+    if ((m->k_type != kKvF32 || m->v_type != kKvF32) && !split) {
         fprintf(stderr, "mantle_hip: the f16 / q8_0 KV cache needs head_dim 64/128 and a split attention path\n");
         free_model(m);
         return hipErrorInvalidValue;
     }
-    if (m->kv_q8 && (max_ctx > 32768 || m->kv_dim > kKvQ8MaxRow)) {
-        fprintf(stderr, "mantle_hip: the q8_0 KV cache supports up to 32768 positions and %d values per row\n",
+    if ((any_q8 || m->k_type != m->v_type) && (max_ctx > 32768 || (any_q8 && m->kv_dim > kKvQ8MaxRow))) {
+        fprintf(stderr, "mantle_hip: q8_0 and mixed KV caches support up to 32768 positions (q8_0: %d values per row)\n",
                 kKvQ8MaxRow);
         free_model(m);
         return hipErrorInvalidValue;
     }
     // transposed V: a column's keys padded to 16 bytes (4 fp32, 8 f16, 16 int8 keys)
-    const int vt_pad = m->kv_q8 ? 16 : 4;
+    const int vt_pad = m->v_type == kKvQ8 ? 16 : 4;
     m->vt_stride = split ? (max_ctx + vt_pad - 1) / vt_pad * vt_pad : 0;
     m->v_rows = split ? m->vt_stride : max_ctx;
     const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
-    const size_t kv_elem = m->kv_q8 ? 1 : (m->kv_f16 ? 2 : 4);
-    CHECK(hipMalloc((void**)&m->cache_k, kv_elem * kv_elems));
-    CHECK(hipMalloc((void**)&m->cache_v, kv_elem * v_elems));
-    if (m->kv_q8) {
+    CHECK(hipMalloc((void**)&m->cache_k, kv_elem_bytes(m->k_type) * kv_elems));
+    CHECK(hipMalloc((void**)&m->cache_v, kv_elem_bytes(m->v_type) * v_elems));
+    if (m->k_type == kKvQ8) {
         CHECK(hipMalloc((void**)&m->k_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
-        CHECK(hipMalloc((void**)&m->v_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
         CHECK(hipMemset(m->k_scale, 0, sizeof(float) * (size_t)c.n_layers * max_ctx));
+    }
+    if (m->v_type == kKvQ8) {
+        CHECK(hipMalloc((void**)&m->v_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
         CHECK(hipMemset(m->v_scale, 0, sizeof(float) * (size_t)c.n_layers * max_ctx));
     }
     CHECK(hipMalloc((void**)&m->state, sizeof(DecodeState)));
@@ -586,8 +624,8 @@ static int load_model(const McfFile& f, int max_ctx, mantleHipModel** out, const
     CHECK(hipMemset(m->state, 0, sizeof(DecodeState)));
     CHECK(hipMemset(m->prompt, 0, sizeof(int) * max_ctx));
     CHECK(hipMemset(m->out_tokens, 0, sizeof(int) * max_ctx));
-    CHECK(hipMemset(m->cache_k, 0, kv_elem * kv_elems));
-    CHECK(hipMemset(m->cache_v, 0, kv_elem * v_elems));
+    CHECK(hipMemset(m->cache_k, 0, kv_elem_bytes(m->k_type) * kv_elems));
+    CHECK(hipMemset(m->cache_v, 0, kv_elem_bytes(m->v_type) * v_elems));
     CHECK(hipDeviceSynchronize());
 #undef CHECK
     *out = m;

@@ -661,6 +661,58 @@ void mo_attn_heads_q8(const float* q, const int8_t* ck, const int8_t* cv, const 
     }
 }
 
+/* internal/backend/simd/attnpool.go:77-153 (RunAttnHeads), every cache-type
+ * pair and the ring / window placement: useRing = 0 < cacheLen < pos + 1,
+ * cachePos = t % cacheLen; scores by Dot (f32, ISA order), DotF16 (f16,
+ * scalar) or DotQ8 (q8_0: scalar sum * scale_t, ops.go:240-246) times
+ * scale; Softmax; the V sum in key order with p * v, p * f16(v) or
+ * (p * q) * s_t. */
+void mo_attn_heads_mixed(int isa, const float* q, int k_type, const void* ck, const float* ks, int v_type,
+                         const void* cv, const float* vs, float* out, int pos, int start, int cache_len,
+                         int kv_stride, int head_dim, int n_head, int kv_heads, float scale) {
+    int win = pos - start + 1;
+    int ring = cache_len > 0 && cache_len < pos + 1;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int h = 0; h < n_head; h++) {
+        float* scores = (float*)malloc(sizeof(float) * (size_t)win);
+        int kvh = h * kv_heads / n_head;
+        const float* qh = q + (int64_t)h * head_dim;
+        for (int t = start; t <= pos; t++) {
+            int cp = ring ? t % cache_len : t;
+            int64_t off = (int64_t)cp * kv_stride + (int64_t)kvh * head_dim;
+            float sc;
+            if (k_type == MO_KV_Q8) {
+                const int8_t* kt = (const int8_t*)ck + off;
+                float sum = 0.0f;
+                for (int i = 0; i < head_dim; i++) sum += qh[i] * (float)kt[i];
+                sc = sum * ks[cp];
+            } else if (k_type == MO_KV_F16) {
+                const uint16_t* kt = (const uint16_t*)ck + off;
+                float sum = 0.0f;
+                for (int i = 0; i < head_dim; i++) sum += qh[i] * mo_f16_to_f32(kt[i]);
+                sc = sum;
+            } else {
+                sc = mo_dot(isa, qh, (const float*)ck + off, head_dim);
+            }
+            scores[t - start] = sc * scale;
+        }
+        mo_softmax(scores, win);
+        for (int d = 0; d < head_dim; d++) {
+            float sum = 0.0f;
+            for (int t = start; t <= pos; t++) {
+                int cp = ring ? t % cache_len : t;
+                int64_t off = (int64_t)cp * kv_stride + (int64_t)kvh * head_dim + d;
+                float p = scores[t - start];
+                if (v_type == MO_KV_Q8) sum += (p * (float)((const int8_t*)cv)[off]) * vs[cp];
+                else if (v_type == MO_KV_F16) sum += p * mo_f16_to_f32(((const uint16_t*)cv)[off]);
+                else sum += p * ((const float*)cv)[off];
+            }
+            out[(int64_t)h * head_dim + d] = sum;
+        }
+        free(scores);
+    }
+}
+
 /* internal/backend/simd/runtime_greedy.go:70-82 (argmaxHost: strict '>'). */
 int64_t mo_argmax(const float* x, int64_t n) {
     if (n <= 0) return -1;
@@ -794,7 +846,7 @@ mo_model* mo_model_create(const mo_config* cfg, const mo_weights* w, int max_ctx
     m->act = calloc((size_t)f, 4);
     m->down = calloc((size_t)d, 4);
     m->logits = calloc((size_t)cfg->vocab, 4);
-    /* f32 cache, or (kv_f16) uint16 f16 values in the same [L][max_ctx][kv_dim] slots */
+    /* f32 cache, or uint16 f16 / int8 values in the same [L][max_ctx][kv_dim] slots */
     m->cache_k = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx * m->kv_dim), 4);
     m->cache_v = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx * m->kv_dim), 4);
     m->kscale = calloc((size_t)(cfg->n_layers * (int64_t)max_ctx), 4);
@@ -872,30 +924,30 @@ int64_t mo_model_forward_greedy(mo_model* m, int64_t tok, float* logits_out) {
         /* ops_runtime.go:40-131 StoreKV + RunAttnHeads */
         float* ck = m->cache_k + (int64_t)l * m->max_ctx * m->kv_dim;
         float* cv = m->cache_v + (int64_t)l * m->max_ctx * m->kv_dim;
-        if (c->kv_q8) {  /* loader.go:645-663 --cache-type-k/v q8_0; ops_runtime.go:112-131 */
-            int8_t* ck8 = (int8_t*)ck;
-            int8_t* cv8 = (int8_t*)cv;
-            float* ks = m->kscale + (int64_t)l * m->max_ctx;
-            float* vs = m->vscale + (int64_t)l * m->max_ctx;
-            mo_store_q8(m->k, ck8 + (int64_t)pos * m->kv_dim, ks + pos, m->kv_dim);
-            mo_store_q8(m->v, cv8 + (int64_t)pos * m->kv_dim, vs + pos, m->kv_dim);
-            mo_attn_heads_q8(m->q, ck8, cv8, ks, vs, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads,
-                             c->n_kv_heads, scale);
-        } else if (c->kv_f16) {  /* loader.go:645-663 --cache-type-k/v f16 */
-            uint16_t* ck16 = (uint16_t*)ck;
-            uint16_t* cv16 = (uint16_t*)cv;
-            for (int64_t i = 0; i < m->kv_dim; i++) {
-                ck16[(int64_t)pos * m->kv_dim + i] = mo_f32_to_f16(m->k[i]);
-                cv16[(int64_t)pos * m->kv_dim + i] = mo_f32_to_f16(m->v[i]);
-            }
-            mo_attn_heads_f16(m->q, ck16, cv16, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads, c->n_kv_heads,
-                              scale);
-        } else {
-            memcpy(ck + (int64_t)pos * m->kv_dim, m->k, sizeof(float) * (size_t)m->kv_dim);
-            memcpy(cv + (int64_t)pos * m->kv_dim, m->v, sizeof(float) * (size_t)m->kv_dim);
+        float* ks = m->kscale + (int64_t)l * m->max_ctx;
+        float* vs = m->vscale + (int64_t)l * m->max_ctx;
+        /* ops_runtime.go:112-131 StoreKV: each row in its cache's type (loader.go:640-668) */
+        int64_t row = (int64_t)pos * m->kv_dim;
+        if (c->kv_k == MO_KV_Q8) mo_store_q8(m->k, (int8_t*)ck + row, ks + pos, m->kv_dim);
+        else if (c->kv_k == MO_KV_F16)
+            for (int64_t i = 0; i < m->kv_dim; i++) ((uint16_t*)ck)[row + i] = mo_f32_to_f16(m->k[i]);
+        else memcpy(ck + row, m->k, sizeof(float) * (size_t)m->kv_dim);
+        if (c->kv_v == MO_KV_Q8) mo_store_q8(m->v, (int8_t*)cv + row, vs + pos, m->kv_dim);
+        else if (c->kv_v == MO_KV_F16)
+            for (int64_t i = 0; i < m->kv_dim; i++) ((uint16_t*)cv)[row + i] = mo_f32_to_f16(m->v[i]);
+        else memcpy(cv + row, m->v, sizeof(float) * (size_t)m->kv_dim);
+        if (c->kv_k == c->kv_v && c->kv_k == MO_KV_Q8)
+            mo_attn_heads_q8(m->q, (int8_t*)ck, (int8_t*)cv, ks, vs, m->attn, pos, 0, (int)m->kv_dim, (int)hd,
+                             c->n_heads, c->n_kv_heads, scale);
+        else if (c->kv_k == c->kv_v && c->kv_k == MO_KV_F16)
+            mo_attn_heads_f16(m->q, (uint16_t*)ck, (uint16_t*)cv, m->attn, pos, 0, (int)m->kv_dim, (int)hd,
+                              c->n_heads, c->n_kv_heads, scale);
+        else if (c->kv_k == c->kv_v)
             mo_attn_heads(c->isa, m->q, ck, cv, m->attn, pos, 0, (int)m->kv_dim, (int)hd, c->n_heads, c->n_kv_heads,
                           scale);
-        }
+        else
+            mo_attn_heads_mixed(c->isa, m->q, c->kv_k, ck, ks, c->kv_v, cv, vs, m->attn, pos, 0, 0, (int)m->kv_dim,
+                                (int)hd, c->n_heads, c->n_kv_heads, scale);
         /* attn.go:417 Wo (re-quantises attnOut) */
         quant_then_matvec(m, m->w.wo[l], d, m->q_dim, m->attn, m->proj);
         /* runtime.go:278-289 addResidual */

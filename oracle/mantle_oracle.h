@@ -88,6 +88,14 @@ void mo_attn_heads_q8(const float* q, const int8_t* cache_k, const int8_t* cache
                       const float* v_scale, float* out, int pos, int start, int kv_stride, int head_dim, int n_head,
                       int kv_heads, float scale);
 int64_t mo_argmax(const float* x, int64_t n);
+/* RunAttnHeads in general (internal/backend/simd/attnpool.go:77-153): K and V
+ * caches of independent types (MO_KV_F32: float, MO_KV_F16: uint16 f16,
+ * MO_KV_Q8: int8 with per-position scales ks / vs), keys t = start..pos, each
+ * at cache slot t % cache_len when 0 < cache_len < pos + 1 (the ring), else t. */
+enum { MO_KV_F32 = 0, MO_KV_F16 = 1, MO_KV_Q8 = 2 };
+void mo_attn_heads_mixed(int isa, const float* q, int k_type, const void* cache_k, const float* ks, int v_type,
+                         const void* cache_v, const float* vs, float* out, int pos, int start, int cache_len,
+                         int kv_stride, int head_dim, int n_head, int kv_heads, float scale);
 
 /* ---- Qwen3-shaped decoder (k4 weights, f32 KV cache) ---- */
 typedef struct {
@@ -96,8 +104,8 @@ typedef struct {
     float eps;
     int isa;
     int wdtype; /* MO_W_K4: the matrix pointers below are k4 payloads; MO_W_BF16: bf16 [rows][cols] */
-    int kv_f16; /* KV cache in Mantle's f16 (--cache-type-k/v f16) instead of f32 */
-    int kv_q8;  /* KV cache in Mantle's q8_0 (--cache-type-k/v q8_0) instead of f32 */
+    int kv_k;   /* K cache type (--cache-type-k): MO_KV_F32, MO_KV_F16 (Mantle's truncating f16), MO_KV_Q8 */
+    int kv_v;   /* V cache type (--cache-type-v), independent of kv_k */
 } mo_config;
 enum { MO_W_K4 = 0, MO_W_BF16 = 1 };
 

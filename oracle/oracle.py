@@ -24,8 +24,8 @@ F = C.c_float
 
 class Config(C.Structure):
     _fields_ = [("n_layers", I), ("d_model", I), ("n_heads", I), ("n_kv_heads", I), ("head_dim", I), ("ffn", I),
-                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I), ("kv_f16", I),
-                ("kv_q8", I)]
+                ("vocab", I), ("rope_base", C.c_double), ("eps", F), ("isa", I), ("wdtype", I), ("kv_k", I),
+                ("kv_v", I)]
 
 
 class Weights(C.Structure):
@@ -60,6 +60,7 @@ _SIGS = {
     "mo_store_q8": (None, [P, P, P, C.c_int64]),
     "mo_attn_heads_q8": (None, [P, P, P, P, P, P, I, I, I, I, I, I, F]),
     "mo_argmax": (I64, [P, I64]),
+    "mo_attn_heads_mixed": (None, [I, P, I, P, P, I, P, P, P, I, I, I, I, I, I, I, F]),
     "mo_model_create": (P, [C.POINTER(Config), C.POINTER(Weights), I]),
     "mo_model_free": (None, [P]),
     "mo_model_reset": (None, [P]),
@@ -276,6 +277,27 @@ def attn_heads_q8(q, cache_k8, cache_v8, k_scale, v_scale, pos: int, kv_stride: 
     return out
 
 
+KV_TYPES = {"f32": 0, "f16": 1, "q8_0": 2}
+
+
+def attn_heads_mixed(isa, q, k_type, cache_k, k_scale, v_type, cache_v, v_scale, pos, start, cache_len, kv_stride,
+                     head_dim, n_head, kv_heads, scale):
+    """RunAttnHeads over K / V caches of independent types ("f32" / "f16" /
+    "q8_0"; f16 caches as uint16, q8_0 as int8 with per-position scales) with
+    the ring placement (cache_len) and window start."""
+    q = _f32(q)
+    dt = {"f32": np.float32, "f16": np.uint16, "q8_0": np.int8}
+    ck = np.ascontiguousarray(cache_k, dtype=dt[k_type])
+    cv = np.ascontiguousarray(cache_v, dtype=dt[v_type])
+    ks = _f32(k_scale if k_scale is not None else np.zeros(1))
+    vs = _f32(v_scale if v_scale is not None else np.zeros(1))
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    lib().mo_attn_heads_mixed(int(isa), _ptr(q), KV_TYPES[k_type], ck.ctypes.data, _ptr(ks), KV_TYPES[v_type],
+                              cv.ctypes.data, _ptr(vs), _ptr(out), int(pos), int(start), int(cache_len),
+                              int(kv_stride), int(head_dim), int(n_head), int(kv_heads), float(scale))
+    return out
+
+
 def argmax(x) -> int:
     x = _f32(x)
     return int(lib().mo_argmax(_ptr(x), len(x)))
@@ -284,7 +306,8 @@ def argmax(x) -> int:
 class Model:
     """Qwen3-shaped decoder on the CPU (the greedy-token oracle), k4 weights or,
     with cfg["weights"] == "bf16", bf16 ones; cfg["kv_cache"] == "f16" stores the
-    KV cache in Mantle's truncating f16, "q8_0" as int8 rows with one scale each.
+    KV cache in Mantle's truncating f16, "q8_0" as int8 rows with one scale each
+    (cfg["kv_cache_k"] / cfg["kv_cache_v"] set the two caches separately).
 
     `tensors(name) -> np.uint8 payload / np.float32 gains` supplies the weights
     (e.g. views into an MCF file); they must outlive the model.
@@ -319,7 +342,8 @@ class Model:
             setattr(w, field, arr([lname(l, suffix) for l in range(L)]))
         c = Config(cfg["n_layers"], cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"],
                    cfg["vocab"], cfg["rope_base"], cfg["eps"], isa, 1 if cfg.get("weights") == "bf16" else 0,
-                   1 if cfg.get("kv_cache") == "f16" else 0, 1 if cfg.get("kv_cache") == "q8_0" else 0)
+                   KV_TYPES[cfg.get("kv_cache_k", cfg.get("kv_cache", "f32"))],
+                   KV_TYPES[cfg.get("kv_cache_v", cfg.get("kv_cache", "f32"))])
         self._keep = keep
         self._w = w
         self._c = c

@@ -238,3 +238,28 @@ def test_qwen3_0_6b_first_64_tokens(hip, tmp_models, kv_cache):
     finally:
         om.close()
     assert got == want
+
+
+@pytest.mark.parametrize("kt,vt", [("f32", "f16"), ("f16", "f32"), ("f32", "q8_0"), ("q8_0", "f32"),
+                                   ("f16", "q8_0"), ("q8_0", "f16")])
+@pytest.mark.parametrize("ctx", [200, 650])
+def test_lane_mixed_kv_cache_types(hip, lane_path, kt, vt, ctx):
+    """--cache-type-k and --cache-type-v chosen independently
+    (cmd/mantle/run.go:183-195; StoreKV / RunAttnHeads handle each cache by
+    its own type, ops_runtime.go:112-131, attnpool.go:100-135): logits
+    bit-identical to the oracle with the same pair, on the register-ring V
+    sum (200 positions) and the LDS-staged one (650)."""
+    import mantle_amd
+    rt = mantle_amd.new_backend("hip").load_model(lane_path, max_context=ctx, kv_cache_k=kt, kv_cache_v=vt)
+    om = models.oracle_model(lane_path, dict(models.LANE, kv_cache_k=kt, kv_cache_v=vt), ctx)
+    try:
+        n = 150 if ctx == 200 else 300
+        toks = models.prompt(n, models.LANE["vocab"], 11)
+        for step, tok in enumerate(toks):
+            logits = rt.forward_token(tok)
+            _, want = om.forward_greedy(tok, want_logits=True)
+            if step % 25 == 24 or step in (0, 63, 64, 65, n - 1):
+                np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32), err_msg=f"step {step}")
+    finally:
+        rt.close()
+        om.close()

@@ -116,6 +116,38 @@ def test_argmax_first_max_wins(hip):
     assert int(g.host(out)[0]) == int(np.argmax(x))
 
 
+@pytest.mark.parametrize("case", ["nan_later", "nan_first", "signed_zero", "neg_zero_first", "all_nan_tail"])
+def test_argmax_nan_and_signed_zero(hip, oracle, case):
+    """argmaxHost's strict '>' (runtime_greedy.go:70-82): a NaN never wins
+    unless it is x[0] (then nothing beats it), and -0 equals +0 (first wins)."""
+    n = 70000
+    x = np.full(n, -5.0, dtype=np.float32)
+    if case == "nan_later":
+        x[[10, 500]] = np.nan
+        x[700] = 1.0
+    elif case == "nan_first":
+        x[0] = np.nan
+        x[900] = 100.0
+    elif case == "signed_zero":
+        x[30] = np.float32(-0.0)
+        x[40] = np.float32(0.0)
+    elif case == "neg_zero_first":
+        x[3] = np.float32(0.0)
+        x[2] = np.float32(-0.0)
+    else:
+        x[1:] = np.nan
+    want = oracle.argmax(x) if hasattr(oracle, "argmax") else None
+    ref = 0
+    for i in range(1, n):  # argmaxHost, literally
+        if x[i] > x[ref]:
+            ref = i
+    if want is not None:
+        assert want == ref
+    out = g.empty(1, torch.int32)
+    g.call("mantleHipArgMaxF32", g.ptr(g.keep(x)), n, g.ptr(out), g.stream())
+    assert int(g.host(out)[0]) == ref, case
+
+
 def test_add_vectors(hip):
     a = np.arange(1000, dtype=np.float32)
     b = np.full(1000, 0.5, dtype=np.float32)

@@ -586,3 +586,88 @@ def test_attn_q8_vs_float64():
         p /= p.sum()
         want[h * hd:(h + 1) * hd] = p @ vf[:, g]
     np.testing.assert_allclose(got, want, atol=1e-5, rtol=1e-5)
+
+
+def test_argmax_strict_greater_kat():
+    """argmaxHost (runtime_greedy.go:70-82): best = x[0], replaced only by a
+    strictly greater value, so ties keep the first index, -0 ties +0, a later
+    NaN never wins and a NaN at index 0 is never replaced."""
+    f = np.float32
+    assert o.argmax(np.array([1, 3, 3, 2], dtype=f)) == 1
+    assert o.argmax(np.array([f(-0.0), f(0.0)], dtype=f)) == 0
+    assert o.argmax(np.array([-1, np.nan, 0.5, np.nan], dtype=f)) == 2
+    assert o.argmax(np.array([np.nan, 1, 2], dtype=f)) == 0
+
+
+# ------------------------------------------- mixed K / V caches, ring / window ----
+def _mixed_caches(rng, rows, kv):
+    kf = (rng.standard_normal(rows * kv) * 2).astype(np.float32)
+    vf = rng.standard_normal(rows * kv).astype(np.float32)
+    caches = {"f32": (kf, vf, None, None), "f16": (_f16_bits(kf), _f16_bits(vf), None, None)}
+    k8 = np.empty(rows * kv, np.int8); v8 = np.empty(rows * kv, np.int8)
+    ks = np.empty(rows, np.float32); vs = np.empty(rows, np.float32)
+    for t in range(rows):
+        k8[t * kv:(t + 1) * kv], ks[t] = o.store_q8(kf[t * kv:(t + 1) * kv])
+        v8[t * kv:(t + 1) * kv], vs[t] = o.store_q8(vf[t * kv:(t + 1) * kv])
+    caches["q8_0"] = (k8, v8, ks, vs)
+    return caches
+
+
+def _decoded(kind, c, which, kv):
+    if kind == "f32":
+        return c[0 if which == "k" else 1]
+    if kind == "f16":
+        return np.array([o.f16_to_f32(int(b)) for b in c[0 if which == "k" else 1]], np.float32)
+    raw, sc = (c[0], c[2]) if which == "k" else (c[1], c[3])
+    return (raw.astype(np.float64).reshape(-1, kv) * sc[:, None]).reshape(-1)
+
+
+@pytest.mark.parametrize("kt", ["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("vt", ["f32", "f16", "q8_0"])
+def test_attn_mixed_matches_single_type_and_float64(kt, vt):
+    """RunAttnHeads with K and V caches of independent types (attnpool.go:100-135):
+    equal types give exactly the single-type restatements; every pair agrees
+    with float64 attention over the decoded caches within 1e-5
+    (TestRunAttnHeadsMatchesReference's tolerance, attn_test.go:10-86)."""
+    rng = np.random.default_rng(21)
+    nh, kvh, hd, pos = 4, 2, 64, 90
+    kv = kvh * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    cs = _mixed_caches(rng, pos + 1, kv)
+    ck, cv = cs[kt], cs[vt]
+    got = o.attn_heads_mixed(2, q, kt, ck[0], ck[2], vt, cv[1], cv[3], pos, 0, 0, kv, hd, nh, kvh, 0.125)
+    if kt == vt == "f32":
+        np.testing.assert_array_equal(got, o.attn_heads(2, q, ck[0], cv[1], pos, kv, hd, nh, kvh, 0.125))
+    elif kt == vt == "f16":
+        np.testing.assert_array_equal(got, o.attn_heads_f16(q, ck[0], cv[1], pos, kv, hd, nh, kvh, 0.125))
+    elif kt == vt == "q8_0":
+        np.testing.assert_array_equal(got, o.attn_heads_q8(q, ck[0], cv[1], ck[2], cv[3], pos, kv, hd, nh, kvh, 0.125))
+    kd = _decoded(kt, ck, "k", kv).astype(np.float64).reshape(pos + 1, kvh, hd)
+    vd = _decoded(vt, cv, "v", kv).astype(np.float64).reshape(pos + 1, kvh, hd)
+    want = np.empty((nh, hd))
+    for h in range(nh):
+        g = h * kvh // nh
+        s = kd[:, g, :] @ q[h * hd:(h + 1) * hd].astype(np.float64) * 0.125
+        p = np.exp(s - s.max()); p /= p.sum()
+        want[h] = p @ vd[:, g, :]
+    np.testing.assert_allclose(got, want.reshape(-1), atol=1e-5, rtol=1e-5)
+
+
+def test_attn_ring_and_window_placement():
+    """RunAttnHeads' ring (attnpool.go:88-99: 0 < cacheLen < pos + 1 puts key t at
+    slot t % cacheLen) and window start: a window of the last W keys read from a
+    ring of W slots equals the same window read from a linear cache."""
+    rng = np.random.default_rng(5)
+    nh, kvh, hd, W, pos = 2, 1, 64, 16, 40
+    kv = kvh * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    lin_k = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+    lin_v = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+    ring_k = np.zeros(W * kv, np.float32); ring_v = np.zeros(W * kv, np.float32)
+    for t in range(pos + 1):  # StoreKV at cachePos = t % cacheLen (ops_runtime.go:51-55)
+        ring_k[(t % W) * kv:(t % W + 1) * kv] = lin_k[t * kv:(t + 1) * kv]
+        ring_v[(t % W) * kv:(t % W + 1) * kv] = lin_v[t * kv:(t + 1) * kv]
+    start = pos - W + 1
+    a = o.attn_heads_mixed(2, q, "f32", ring_k, None, "f32", ring_v, None, pos, start, W, kv, hd, nh, kvh, 0.125)
+    b = o.attn_heads(2, q, lin_k, lin_v, pos, kv, hd, nh, kvh, 0.125, start=start)
+    np.testing.assert_array_equal(a, b)
