@@ -95,31 +95,50 @@ int mantleHipQuantizeVecBlocksF32(const float* x, int n, int8_t* qx, float* scal
 int mantleHipRMSNormF32(float* out, const float* x, const float* weight, float eps, int n, mantleHipStream_t stream);
 int mantleHipRMSNormBatchedF32(float* out, const float* x, const float* weight, float eps, int headDim, int nHeads,
                                mantleHipStream_t stream);
-/* Replaces mantleCudaApplyRoPEInplaceF32 (internal/backend/cuda/native/attn_fused.cu:51-75); takes
- * Mantle's float64 inverse frequencies (internal/backend/simd/loader.go:1604-1612). */
-int mantleHipApplyRoPEInplaceF32(float* x, const double* invFreq, int pos, float attnScale, int headDim, int half,
+/* Replaces mantleCudaApplyRoPEInplaceF32 with its argument list (internal/backend/cuda/native/
+ * attn_fused.cu:51-75: float32 invFreq table, attnScale 0 taken as 1).  The angle
+ * pos * invFreq[i] and its cos / sin are evaluated in float64 and the pairs updated as the CPU
+ * path does (y0 = x0*c - x1*s, y1 = fma(x0, s, x1*c), internal/backend/simd/ops_avx512.go:146-190). */
+int mantleHipApplyRoPEInplaceF32(float* x, const float* invFreq, int pos, float attnScale, int headDim, int half,
                                  int nHeads, mantleHipStream_t stream);
+/* The same with Mantle's CPU float64 inverse frequencies (internal/backend/simd/loader.go:1604-1612),
+ * which the CPU path's RoPE reads (no reference C counterpart). */
+int mantleHipApplyRoPEInplaceF64FreqF32(float* x, const double* invFreq, int pos, float attnScale, int headDim,
+                                        int half, int nHeads, mantleHipStream_t stream);
 /* RoPE from precomputed float32 cos/sin rows (what the decode runtime uses). */
 int mantleHipApplyRoPEInplaceTableF32(float* x, const float* cosv, const float* sinv, int headDim, int half,
                                       int nHeads, mantleHipStream_t stream);
 /* f32 KV append; the f32 twin of mantleCudaStoreKVF16Row (internal/backend/cuda/native/attn_fused.cu:91-107). */
 int mantleHipStoreKVF32Row(float* cache, const float* src, int cachePos, int kvStride, mantleHipStream_t stream);
-/* Decode attention over an f32 cache; f32 twin of mantleCudaAttentionInnerF16CacheF32
- * (internal/backend/cuda/native/softmax.h:70-83), CPU-parity with RunAttnHeads
- * (internal/backend/simd/attnpool.go:77-153).  scoresScratch: nHead*(pos+1) floats. */
+/* Decode attention over row-major caches ([cachePos][kvStride], kvHead's vector at
+ * + kvHead*headDim), CPU-parity with RunAttnHeads (internal/backend/simd/attnpool.go:77-153):
+ * keys start..pos, key t read from row t % cacheLen when 0 < cacheLen < pos + 1 (the
+ * ring; else row t).  headDim 64 / 128 on the split attention paths.
+ * f32 cache: the f32 twin of mantleCudaAttentionInnerF16CacheF32 (no reference counterpart:
+ * Mantle's CUDA backend keeps f16 caches); scoresScratch: nHead*(pos-start+1) floats. */
 int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const float* cacheV, float* out,
                                     float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
                                     int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
-/* Decode attention over Mantle's f16 KV cache (--cache-type-k/v f16, the CLI
- * default: cmd/mantle/run.go:183-195); replaces mantleCudaAttentionInnerF16CacheF32
+/* Over Mantle's f16 KV cache (--cache-type-k/v f16, the CLI default: cmd/mantle/run.go:183-195).
+ * Replaces mantleCudaAttentionInnerF16CacheF32 with its exact argument list
  * (internal/backend/cuda/native/softmax.h:70-83), with the CPU arithmetic of
- * internal/backend/simd/attnpool.go:103-106, :127-135 (DotF16 in the scalar
- * order, p_t * f16(v) summed in key order).  Layout [pos][kvStride] uint16;
- * scoresScratch as in mantleHipAttentionInnerF32Cache.  Split attention
- * paths only (MANTLE_HIP_ATTN_SPLIT / _FUSED). */
+ * internal/backend/simd/attnpool.go:103-106, :127-135 (DotF16 in the scalar order,
+ * p_t * f16(v) summed in key order).  The scores live in a library-owned buffer per device
+ * (grown on demand): calls on one device must be serialised on one stream. */
 int mantleHipAttentionInnerF16CacheF32(const float* q, const uint16_t* cacheK, const uint16_t* cacheV, float* out,
-                                       float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
-                                       int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
+                                       int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
+                                       int cacheLen, float scale, mantleHipStream_t stream);
+/* K and V caches each f16 or q8_0 (useQ8K / useQ8V; --cache-type-k / -v chosen independently).
+ * Replaces mantleCudaAttentionInnerMixedCacheF32 with its exact argument list
+ * (internal/backend/cuda/native/softmax.h:84-104); the CPU arithmetic of
+ * attnpool.go:100-135 (DotQ8 / DotF16 scalar orders; q8_0 V terms (p_t * q) * s_t).  The
+ * q8_0 side needs kvStride a multiple of 16 and 16-byte aligned rows, positions up to
+ * 32768.  Scores as in mantleHipAttentionInnerF16CacheF32. */
+int mantleHipAttentionInnerMixedCacheF32(const float* q, const uint16_t* cacheKF16, const uint16_t* cacheVF16,
+                                         const int8_t* cacheKQ8, const int8_t* cacheVQ8, const float* cacheKScales,
+                                         const float* cacheVScales, float* out, int useQ8K, int useQ8V, int pos,
+                                         int start, int kvStride, int headDim, int nHead, int kvHeads, int cacheLen,
+                                         float scale, mantleHipStream_t stream);
 /* StoreKV into an f16 cache row; replaces mantleCudaStoreKVF16Row
  * (internal/backend/cuda/native/attn_fused.cu:91-107) but converts as the CPU
  * does (Float32ToFloat16: truncating, flush to zero, internal/backend/simd/float16.go:7-46). */
@@ -129,8 +148,8 @@ int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int 
  * internal/backend/simd/attnpool.go:100-102, :122-130: score = DotQ8(q, k_t, kScales[t]) * scale
  * (ops.go:240-246, the scalar order), out_d = sum_t (p_t * v_t,d) * vScales[t] in key order.
  * Layout [pos][kvStride] int8 (kvStride a multiple of 16, 16-byte aligned rows), one scale
- * per position; scoresScratch as in mantleHipAttentionInnerF32Cache; positions up to 32768.
- * Split attention paths only (MANTLE_HIP_ATTN_SPLIT / _FUSED, both take the two-launch form). */
+ * per position; scoresScratch, start and cacheLen as in mantleHipAttentionInnerF32Cache;
+ * positions up to 32768.  Split attention paths only (both take the two-launch form). */
 int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, const int8_t* cacheV,
                                       const float* kScales, const float* vScales, float* out, float* scoresScratch,
                                       int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
@@ -238,6 +257,21 @@ int mantleHipModelLoadMCFImageWithOptions(const uint8_t* data, uint64_t size, in
 /* Same, from an MCF image the caller already holds in memory (Mantle keeps the file mmapped:
  * pkg/mcf/reader.go:21-69); the image is only read during the call. */
 int mantleHipModelLoadMCFImage(const uint8_t* data, uint64_t size, int maxContext, mantleHipModel** out);
+/* Build the model from tensors the caller already holds, for a Go LoadModel that walks
+ * mcfstore.File (internal/mcfstore/file.go:28-194: Tensor / ReadTensorRaw for each payload,
+ * SectionData for the HF config.json): configJSON is that section's text, each view one
+ * tensor's MCF payload with its MCF dtype code (1 f32, 3 bf16, 0x31 k4) and shape.  The views
+ * are only read during the call (copied into HBM). */
+typedef struct mantleHipTensorView {
+    const char* name;
+    int dtype;
+    int rank;
+    int64_t shape[4];
+    const uint8_t* data;
+    uint64_t size;
+} mantleHipTensorView;
+int mantleHipModelLoadTensors(const char* configJSON, uint64_t configSize, const mantleHipTensorView* tensors,
+                              int nTensors, int maxContext, const mantleHipLoadOptions* opts, mantleHipModel** out);
 void mantleHipModelClose(mantleHipModel* m);
 int mantleHipModelConfig(const mantleHipModel* m, mantleHipQwen3Config* out);
 /* Reset(): Pos = 0 (internal/backend/simd/runtime.go:293-333). */
@@ -250,6 +284,16 @@ int mantleHipModelForwardTokenGreedy(mantleHipModel* m, int tok, int* next);
 /* PrefillTokens (internal/backend/simd/runtime_prefill.go:11-30): token-by-token,
  * as Mantle runs k4 prefill; *next receives the greedy token after the last one. */
 int mantleHipModelPrefillTokens(mantleHipModel* m, const int* toks, int n, int* next);
+/* prefillForwarder.PrefillTokens([]int) ([]float32, error) (internal/inference/engine.go:28-30):
+ * the prompt, then the logits of its last position copied to logitsHost (vocab floats). */
+int mantleHipModelPrefillTokensLogits(mantleHipModel* m, const int* toks, int n, float* logitsHost);
+/* SetEffectiveContextLength (internal/backend/core/instance.go:325-339): reallocate the KV cache
+ * and the other context-sized buffers for ctxLen positions (0 or more than the load-time
+ * maxContext: that maxContext).  Only at position 0 (before the first token or after Reset). */
+int mantleHipModelSetEffectiveContextLength(mantleHipModel* m, int ctxLen);
+/* core.Runtime.UpdateRoPE (internal/backend/core/interfaces.go:14-18): recompute the RoPE tables,
+ * with a new RoPE base when ropeBase > 0. */
+int mantleHipModelUpdateRoPE(mantleHipModel* m, double ropeBase);
 /* Greedy generation kept on the device: prompt then nGen tokens, one replay
  * of the captured decode-step graph per position, no host round trip between
  * steps.  outTokens receives the nGen generated ids. */

@@ -35,6 +35,11 @@ class LoadOptions(C.Structure):
     _fields_ = [("cache_type_k", I), ("cache_type_v", I), ("parity_isa", I), ("use_graph", I), ("reserved", I * 4)]
 
 
+class TensorView(C.Structure):
+    """mantleHipTensorView: one MCF tensor payload held by the caller."""
+    _fields_ = [("name", C.c_char_p), ("dtype", I), ("rank", I), ("shape", I64 * 4), ("data", P), ("size", U64)]
+
+
 _SIGS = {
     "mantleHipGetErrorString": (C.c_char_p, [I]),
     "mantleHipGetDeviceCount": (I, [C.POINTER(I)]),
@@ -43,7 +48,8 @@ _SIGS = {
     "mantleHipGetAttentionPath": (I, []),
     "mantleHipGetParityISA": (I, []),
     "mantleHipMatVecBF16F32": (I, [P, P, P, I, I, P]),
-    "mantleHipAttentionInnerF16CacheF32": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "mantleHipAttentionInnerF16CacheF32": (I, [P, P, P, P, I, I, I, I, I, I, I, F, P]),
+    "mantleHipAttentionInnerMixedCacheF32": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, P]),
     "mantleHipStoreKVF16Row": (I, [P, P, I, I, P]),
     "mantleHipAttentionInnerQ8CacheF32": (I, [P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "mantleHipStoreKVQ8Row": (I, [P, P, P, P, P, P, I, I, P]),
@@ -58,6 +64,7 @@ _SIGS = {
     "mantleHipRMSNormF32": (I, [P, P, P, F, I, P]),
     "mantleHipRMSNormBatchedF32": (I, [P, P, P, F, I, I, P]),
     "mantleHipApplyRoPEInplaceF32": (I, [P, P, I, F, I, I, I, P]),
+    "mantleHipApplyRoPEInplaceF64FreqF32": (I, [P, P, I, F, I, I, I, P]),
     "mantleHipApplyRoPEInplaceTableF32": (I, [P, P, P, I, I, I, P]),
     "mantleHipStoreKVF32Row": (I, [P, P, I, I, P]),
     "mantleHipAttentionInnerF32Cache": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
@@ -89,6 +96,11 @@ _SIGS = {
     "mantleHipModelForwardToken": (I, [P, I, P]),
     "mantleHipModelForwardTokenGreedy": (I, [P, I, C.POINTER(I)]),
     "mantleHipModelPrefillTokens": (I, [P, P, I, C.POINTER(I)]),
+    "mantleHipModelPrefillTokensLogits": (I, [P, P, I, P]),
+    "mantleHipModelSetEffectiveContextLength": (I, [P, I]),
+    "mantleHipModelUpdateRoPE": (I, [P, C.c_double]),
+    "mantleHipModelLoadTensors": (I, [C.c_char_p, U64, C.POINTER(TensorView), I, I, C.POINTER(LoadOptions),
+                                      C.POINTER(P)]),
     "mantleHipModelGenerateGreedy": (I, [P, P, I, I, P]),
     "mantleHipModelDecodeSteps": (I, [P, I]),
     "mantleHipModelSynchronize": (I, [P]),

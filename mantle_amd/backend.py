@@ -12,7 +12,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import I, LoadOptions, P, Qwen3Config, call, lib
+from ._lib import I, LoadOptions, P, Qwen3Config, TensorView, call, lib
 
 ISA = {"scalar": 0, "avx2": 1, "avx512": 2}
 
@@ -53,6 +53,31 @@ class Backend:
         return Runtime(h, max_context)
 
 
+    def load_model_tensors(self, config_json: bytes, tensors, max_context: int = 4096, parity_isa: str = "avx512",
+                           kv_cache: str = "f32", kv_cache_k: str | None = None, kv_cache_v: str | None = None,
+                           use_graph: bool = True) -> "Runtime":
+        """LoadModel from tensors the caller holds, as a Go backend walking
+        mcfstore.File would (internal/mcfstore/file.go:28-194: SectionData for
+        config.json, ReadTensorRaw per tensor): `tensors` yields (name, MCF dtype
+        code, shape, uint8 payload)."""
+        opts = _options(parity_isa, kv_cache_k or kv_cache, kv_cache_v or kv_cache, use_graph)
+        items = list(tensors)
+        views = (TensorView * len(items))()
+        keep = []
+        for v, (name, dtype, shape, payload) in zip(views, items):
+            buf = np.ascontiguousarray(payload).view(np.uint8)
+            nm = name.encode()
+            keep += [buf, nm]
+            v.name, v.dtype, v.rank = nm, int(dtype), len(shape)
+            for i, d in enumerate(shape):
+                v.shape[i] = int(d)
+            v.data, v.size = buf.ctypes.data, buf.nbytes
+        h = P()
+        call("mantleHipModelLoadTensors", config_json, len(config_json), views, len(items), int(max_context),
+             C.byref(opts), C.byref(h))
+        return Runtime(h, max_context)
+
+
 KV = {"f32": 0, "f16": 1, "q8_0": 2}
 
 
@@ -68,6 +93,7 @@ class Runtime:
     def __init__(self, handle: P, max_context: int):
         self._h = handle
         self.max_context = max_context
+        self._load_context = max_context
         cfg = Qwen3Config()
         call("mantleHipModelConfig", handle, C.byref(cfg))
         self.config = cfg.as_dict()
@@ -101,6 +127,26 @@ class Runtime:
         nxt = I()
         call("mantleHipModelPrefillTokens", self._handle(), arr.ctypes.data, len(arr), C.byref(nxt))
         return nxt.value
+
+    def prefill_tokens_logits(self, toks) -> np.ndarray:
+        """prefillForwarder.PrefillTokens: the logits after the last prompt token."""
+        arr = np.ascontiguousarray(toks, dtype=np.int32)
+        logits = np.empty(self.config["vocab"], dtype=np.float32)
+        call("mantleHipModelPrefillTokensLogits", self._handle(), arr.ctypes.data, len(arr), logits.ctypes.data)
+        return logits
+
+    def set_effective_context_length(self, n: int) -> None:
+        call("mantleHipModelSetEffectiveContextLength", self._handle(), int(n))
+        self.max_context = int(n) if 0 < n < self._load_context else self._load_context
+
+    def update_rope(self, rope_base: float = 0.0) -> None:
+        call("mantleHipModelUpdateRoPE", self._handle(), float(rope_base))
+
+    def model_config(self) -> dict:
+        """core.Runtime.ModelConfig."""
+        cfg = Qwen3Config()
+        call("mantleHipModelConfig", self._handle(), C.byref(cfg))
+        return cfg.as_dict()
 
     def generate_greedy(self, prompt, n_gen: int) -> list[int]:
         arr = np.ascontiguousarray(prompt, dtype=np.int32)

@@ -50,6 +50,17 @@ struct ChunkRegs {
     int off[8];  // LDS offset (row * pitch + col), -1: nothing to store
 };
 
+// Cache row of window key t (RunAttnHeads, attnpool.go:88-99): keys are
+// numbered from the window start `base`; a ring of `ring` rows (0: none) puts
+// key position p at row p % ring.
+struct KeyMap {
+    int base = 0, ring = 0;
+};
+__device__ __forceinline__ int krow(const KeyMap& km, int t) {
+    const int p = km.base + t;
+    return km.ring ? p % km.ring : p;
+}
+
 __device__ __forceinline__ void chunk_issue(ChunkRegs& c, const float* __restrict__ base, int stride, int t0, int nk,
                                             int hd, int kp, int skip) {
     // Loads are unconditional (lanes past the chunk re-read row t0, column 0) so
@@ -74,7 +85,7 @@ __device__ __forceinline__ void chunk_issue(ChunkRegs& c, const float* __restric
 // chunk_issue with the head size known at compile time (no integer division).
 template <int HD>
 __device__ __forceinline__ void chunk_issue_t(ChunkRegs& c, const float* __restrict__ base, int stride, int t0, int nk,
-                                              int hd, int kp, int skip) {
+                                              int hd, int kp, int skip, KeyMap km = KeyMap()) {
     constexpr int hd4 = HD / 4;
     const int total4 = nk * hd4;
 #pragma unroll
@@ -86,7 +97,7 @@ __device__ __forceinline__ void chunk_issue_t(ChunkRegs& c, const float* __restr
         const int i4 = ee - tl * hd4;
         const int t = t0 + tl;
         const int o = tl * kp + 4 * i4;
-        c.r[j] = *reinterpret_cast<const f32x4*>(base + (size_t)t * stride + 4 * i4);
+        c.r[j] = *reinterpret_cast<const f32x4*>(base + (size_t)krow(km, t) * stride + 4 * i4);
         c.off[j] = (!live || t == skip) ? -1 : o;
     }
 }
@@ -379,7 +390,7 @@ struct ChunkRegs16 {
 
 template <int HD>
 __device__ __forceinline__ void chunk_issue16_t(ChunkRegs16& c, const uint16_t* __restrict__ base, int stride, int t0,
-                                                int nk, int kp, int skip) {
+                                                int nk, int kp, int skip, KeyMap km = KeyMap()) {
     constexpr int hd4 = HD / 4;
     const int total4 = nk * hd4;
 #pragma unroll
@@ -390,7 +401,7 @@ __device__ __forceinline__ void chunk_issue16_t(ChunkRegs16& c, const uint16_t* 
         const int tl = ee / hd4;
         const int i4 = ee - tl * hd4;
         const int t = t0 + tl;
-        c.r[j] = *reinterpret_cast<const u32x2*>(base + (size_t)t * stride + 4 * i4);
+        c.r[j] = *reinterpret_cast<const u32x2*>(base + (size_t)krow(km, t) * stride + 4 * i4);
         c.off[j] = (!live || t == skip) ? -1 : tl * kp + 4 * i4;
     }
 }
@@ -440,7 +451,7 @@ __device__ __forceinline__ float q8_byte_sdwa(uint32_t w) {
 
 template <int HD>
 __device__ __forceinline__ void chunk_issue8_t(ChunkRegs8& c, const int8_t* __restrict__ base, int stride, int t0,
-                                               int nk, int kp) {
+                                               int nk, int kp, KeyMap km = KeyMap()) {
     constexpr int hd16 = HD / 16;
     const int total = nk * hd16;
 #pragma unroll
@@ -450,7 +461,7 @@ __device__ __forceinline__ void chunk_issue8_t(ChunkRegs8& c, const int8_t* __re
         const int ee = live ? e : 0;
         const int tl = ee / hd16;
         const int i16 = ee - tl * hd16;
-        c.r[j] = *reinterpret_cast<const u32x4*>(base + (size_t)(t0 + tl) * stride + 16 * i16);
+        c.r[j] = *reinterpret_cast<const u32x4*>(base + (size_t)krow(km, t0 + tl) * stride + 16 * i16);
         c.off[j] = live ? tl * kp + 16 * i16 : -1;
     }
 }
@@ -871,6 +882,9 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
     const int8_t* kbase8 = reinterpret_cast<const int8_t*>(a.cache_k) + (size_t)kvh * a.head_stride;
     const int skip = a.fused && !Q8 ? pos : -1;
     float* sg = a.scores + (size_t)h * a.max_ctx;
+    KeyMap km;
+    km.base = a.key_base;
+    km.ring = a.key_ring;
     const PrepRegs pr = prep_load<HD>(a, h, kvh, pos);
     __builtin_amdgcn_sched_barrier(0);
     ChunkRegs ck;
@@ -878,9 +892,9 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
     ChunkRegs8 ck8;
     auto issue = [&](int c) {
         const int nk = min(kc, pos + 1 - c * kc);
-        if constexpr (Q8) chunk_issue8_t<HD>(ck8, kbase8, a.kv_stride, c * kc, nk, kp);
-        else if constexpr (F16) chunk_issue16_t<HD>(ck16, kbase16, a.kv_stride, c * kc, nk, kp, skip);
-        else chunk_issue_t<HD>(ck, kbase, a.kv_stride, c * kc, nk, HD, kp, skip);
+        if constexpr (Q8) chunk_issue8_t<HD>(ck8, kbase8, a.kv_stride, c * kc, nk, kp, km);
+        else if constexpr (F16) chunk_issue16_t<HD>(ck16, kbase16, a.kv_stride, c * kc, nk, kp, skip, km);
+        else chunk_issue_t<HD>(ck, kbase, a.kv_stride, c * kc, nk, HD, kp, skip, km);
     };
     issue(sidx);
     prep_finish<HD>(a, pr, kvh, pos, a.fused && sidx == 0 && first_of_group(a, h, kvh), sq, sk, sv, wbuf);
@@ -897,7 +911,7 @@ __device__ __forceinline__ void scores_split_chunks(const AttnArgs& a, float* ld
         if (tid < nk) {
             const float4* qv = reinterpret_cast<const float4*>(sq);
             const float4* kv = reinterpret_cast<const float4*>(kt + tid * kp);
-            if constexpr (Q8) sg[t0 + tid] = (dot_parity_v4<HD, kIsaScalar>(qv, kv) * a.k_scale[t0 + tid]) * a.scale;
+            if constexpr (Q8) sg[t0 + tid] = (dot_parity_v4<HD, kIsaScalar>(qv, kv) * a.k_scale[krow(km, t0 + tid)]) * a.scale;
             else sg[t0 + tid] = (F16 ? dot_parity_v4<HD, kIsaScalar>(qv, kv) : dot_v4_isa<HD>(qv, kv, a.isa)) * a.scale;
         }
         __syncthreads();
@@ -951,10 +965,13 @@ struct VColumn {
     size_t step;
     float own;
     int skip, pos;
+    KeyMap km;  // window / ring rows (row-major caches only)
 
     __device__ __forceinline__ void init(const AttnArgs& a, int kvh, int hd, int d, int pos_) {
         pos = pos_;
         skip = a.fused && !Q8 ? pos : -1;
+        km.base = a.key_base;
+        km.ring = a.key_ring;
         const uint16_t* c16 = reinterpret_cast<const uint16_t*>(a.cache_v);
         const int8_t* c8 = reinterpret_cast<const int8_t*>(a.cache_v);
         vscale = a.v_scale;
@@ -984,7 +1001,7 @@ struct VColumn {
     __device__ __forceinline__ void issue(int g, int t0) {
         if constexpr (Q8 && !SL) {
             const int tk = t0 + (int)(threadIdx.x & 31);
-            sr[g] = vscale[tk <= pos ? tk : pos];
+            sr[g] = vscale[krow(km, tk <= pos ? tk : pos)];
         }
         if (VT && t0 + VG <= pos) {
             // the whole group lies below pos: no clamp and no own row, so the
@@ -1018,8 +1035,9 @@ struct VColumn {
 #pragma unroll
             for (int k = 0; k < VG; k++) {
                 const int t = t0 + k <= pos ? t0 + k : pos;
-                const float v = Q8 ? (float)col8[(size_t)t * step]
-                                   : (F16 ? f16_cache_load(col16[(size_t)t * step]) : col[(size_t)t * step]);
+                const size_t row = (size_t)krow(km, t);
+                const float v = Q8 ? (float)col8[row * step]
+                                   : (F16 ? f16_cache_load(col16[row * step]) : col[row * step]);
                 r[g][k >> 2][k & 3] = t == skip ? own : v;
             }
         }
@@ -1239,7 +1257,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     if (wave == 0) vc.prime();
     float* ls = lds + pcap + 32;
     if constexpr (SL)
-        for (int t = tid; t <= pos; t += kThreads) ls[t] = a.v_scale[t];
+        for (int t = tid; t <= pos; t += kThreads) ls[t] = a.v_scale[krow(KeyMap{a.key_base, a.key_ring}, t)];
     head_softmax<false>(sg, lds, lds + pcap, pos);
     PHASE(1);
     if (wave != 0) return;
@@ -1468,6 +1486,8 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     const bool split_ok = fast_hd && a.scores && (mode == kAttnPathSplit || mode == kAttnPathFused);
     if (vt && (!split_ok || (a.vt_stride & 3) || a.vt_stride < (a.max_ctx + 3) / 4 * 4))
         return hipErrorInvalidValue;  // the transposed V cache is read by the split kernels only
+    if ((a.key_base || a.key_ring) && (!split_ok || a.fused || vt || a.key_base < 0 || a.key_ring < 0))
+        return hipErrorInvalidValue;  // window / ring rows: row-major caches on the split kernels
     const int kt = a.k_type, vtt = a.v_type;  // cache element types of K and V
     if (kt < kKvF32 || kt > kKvQ8 || vtt < kKvF32 || vtt > kKvQ8) return hipErrorInvalidValue;
     if ((kt != kKvF32 || vtt != kKvF32) && !split_ok)

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -119,8 +120,13 @@ int mantleHipRMSNormBatchedF32(float* out, const float* x, const float* weight, 
     return launch_rmsnorm(out, x, weight, eps, headDim, nHeads, g_isa.load(), S(stream));
 }
 
-int mantleHipApplyRoPEInplaceF32(float* x, const double* invFreq, int pos, float attnScale, int headDim, int half,
+int mantleHipApplyRoPEInplaceF32(float* x, const float* invFreq, int pos, float attnScale, int headDim, int half,
                                  int nHeads, mantleHipStream_t stream) {
+    return launch_rope_f32(x, invFreq, pos, attnScale, headDim, half, nHeads, S(stream));
+}
+
+int mantleHipApplyRoPEInplaceF64FreqF32(float* x, const double* invFreq, int pos, float attnScale, int headDim,
+                                        int half, int nHeads, mantleHipStream_t stream) {
     return launch_rope_f64(x, invFreq, pos, attnScale, headDim, half, nHeads, S(stream));
 }
 
@@ -133,55 +139,96 @@ int mantleHipStoreKVF32Row(float* cache, const float* src, int cachePos, int kvS
     return launch_store_kv_row(cache, src, cachePos, kvStride, S(stream));
 }
 
+// RunAttnHeads over row-major caches ([cachePos][kvStride]) of any K / V
+// types: keys start..pos, key t at row t % cacheLen when 0 < cacheLen < pos + 1
+// (attnpool.go:77-153).  scores: nHead * (pos - start + 1) floats.
+static int attention_rows(const float* q, const void* cacheK, const void* cacheV, int kt, int vt, const float* kScales,
+                          const float* vScales, float* out, float* scores, int pos, int start, int kvStride,
+                          int headDim, int nHead, int kvHeads, int cacheLen, float scale, hipStream_t stream) {
+    if (pos < 0 || start < 0 || start > pos || kvHeads <= 0 || nHead % kvHeads || cacheLen < 0)
+        return hipErrorInvalidValue;
+    const bool ring = cacheLen > 0 && cacheLen < pos + 1;
+    AttnArgs a{};
+    a.q = q;
+    a.cache_k = reinterpret_cast<float*>(const_cast<void*>(cacheK));  // element type k_type
+    a.cache_v = reinterpret_cast<float*>(const_cast<void*>(cacheV));  // element type v_type
+    a.k_type = kt;
+    a.v_type = vt;
+    a.k_scale = kScales;
+    a.v_scale = vScales;
+    a.scores = scores;
+    a.out = out;
+    a.pos_host = pos - start;  // the window's last key
+    a.key_base = start;
+    a.key_ring = ring ? cacheLen : 0;
+    a.n_head = nHead;
+    a.kv_heads = kvHeads;
+    a.head_dim = headDim;
+    a.kv_stride = kvStride;
+    a.head_stride = headDim;  // Mantle's cache: row = cachePos * kvStride + kvHead * headDim
+    a.max_ctx = pos - start + 1;
+    a.scale = scale;
+    a.fused = 0;
+    a.isa = g_isa.load();
+    return launch_attention_decode(a, stream);
+}
+
+// The library's per-device scores buffer for the entry points that take no
+// scratch argument (the reference signatures): grown on demand, shared by
+// every such call on the device, so such calls must be serialised on one
+// stream per device.
+static float* library_scores(size_t floats) {
+    static std::mutex mu;
+    static float* buf[64] = {};
+    static size_t cap[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < floats) {
+        if (buf[dev]) {
+            // earlier launches may still read it
+            if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+            (void)hipFree(buf[dev]);
+            buf[dev] = nullptr;
+            cap[dev] = 0;
+        }
+        size_t n = floats < 65536 ? 65536 : floats;
+        if (hipMalloc((void**)&buf[dev], sizeof(float) * n) != hipSuccess) return nullptr;
+        cap[dev] = n;
+    }
+    return buf[dev];
+}
+
 int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const float* cacheV, float* out,
                                     float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
                                     int kvHeads, int cacheLen, float scale, mantleHipStream_t stream) {
-    // Sliding windows (start > 0) and ring caches (cacheLen <= pos) are not on
-    // the Qwen3 path; they are rejected rather than silently mis-computed.
-    if (start != 0 || (cacheLen > 0 && cacheLen <= pos) || pos < 0 || kvHeads <= 0 || nHead % kvHeads)
-        return hipErrorInvalidValue;
-    AttnArgs a{};
-    a.q = q;
-    a.cache_k = const_cast<float*>(cacheK);
-    a.cache_v = const_cast<float*>(cacheV);
-    a.scores = scoresScratch;
-    a.out = out;
-    a.pos_host = pos;
-    a.n_head = nHead;
-    a.kv_heads = kvHeads;
-    a.head_dim = headDim;
-    a.kv_stride = kvStride;
-    a.head_stride = headDim;  // Mantle's cache: row = pos * kvStride + kvHead * headDim
-    a.max_ctx = pos + 1;
-    a.scale = scale;
-    a.fused = 0;
-    a.isa = g_isa.load();
-    return launch_attention_decode(a, S(stream));
+    return attention_rows(q, cacheK, cacheV, kKvF32, kKvF32, nullptr, nullptr, out, scoresScratch, pos, start,
+                          kvStride, headDim, nHead, kvHeads, cacheLen, scale, S(stream));
 }
 
 int mantleHipAttentionInnerF16CacheF32(const float* q, const uint16_t* cacheK, const uint16_t* cacheV, float* out,
-                                       float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
-                                       int kvHeads, int cacheLen, float scale, mantleHipStream_t stream) {
-    if (start != 0 || (cacheLen > 0 && cacheLen <= pos) || pos < 0 || kvHeads <= 0 || nHead % kvHeads)
-        return hipErrorInvalidValue;
-    AttnArgs a{};
-    a.q = q;
-    a.cache_k = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheK));  // f16 values
-    a.cache_v = reinterpret_cast<float*>(const_cast<uint16_t*>(cacheV));
-    a.k_type = a.v_type = kKvF16;
-    a.scores = scoresScratch;
-    a.out = out;
-    a.pos_host = pos;
-    a.n_head = nHead;
-    a.kv_heads = kvHeads;
-    a.head_dim = headDim;
-    a.kv_stride = kvStride;
-    a.head_stride = headDim;
-    a.max_ctx = pos + 1;
-    a.scale = scale;
-    a.fused = 0;
-    a.isa = g_isa.load();
-    return launch_attention_decode(a, S(stream));
+                                       int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
+                                       int cacheLen, float scale, mantleHipStream_t stream) {
+    if (pos < 0 || start < 0 || start > pos || nHead <= 0) return hipErrorInvalidValue;
+    float* scores = library_scores((size_t)nHead * (size_t)(pos - start + 1));
+    if (!scores) return hipErrorOutOfMemory;
+    return attention_rows(q, cacheK, cacheV, kKvF16, kKvF16, nullptr, nullptr, out, scores, pos, start, kvStride,
+                          headDim, nHead, kvHeads, cacheLen, scale, S(stream));
+}
+
+int mantleHipAttentionInnerMixedCacheF32(const float* q, const uint16_t* cacheKF16, const uint16_t* cacheVF16,
+                                         const int8_t* cacheKQ8, const int8_t* cacheVQ8, const float* cacheKScales,
+                                         const float* cacheVScales, float* out, int useQ8K, int useQ8V, int pos,
+                                         int start, int kvStride, int headDim, int nHead, int kvHeads, int cacheLen,
+                                         float scale, mantleHipStream_t stream) {
+    if (pos < 0 || start < 0 || start > pos || nHead <= 0) return hipErrorInvalidValue;
+    const void* ck = useQ8K ? static_cast<const void*>(cacheKQ8) : static_cast<const void*>(cacheKF16);
+    const void* cv = useQ8V ? static_cast<const void*>(cacheVQ8) : static_cast<const void*>(cacheVF16);
+    if ((useQ8K && !cacheKScales) || (useQ8V && !cacheVScales)) return hipErrorInvalidValue;
+    float* scores = library_scores((size_t)nHead * (size_t)(pos - start + 1));
+    if (!scores) return hipErrorOutOfMemory;
+    return attention_rows(q, ck, cv, useQ8K ? kKvQ8 : kKvF16, useQ8V ? kKvQ8 : kKvF16, cacheKScales, cacheVScales,
+                          out, scores, pos, start, kvStride, headDim, nHead, kvHeads, cacheLen, scale, S(stream));
 }
 
 int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int kvStride, mantleHipStream_t stream) {
@@ -192,28 +239,9 @@ int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, cons
                                       const float* kScales, const float* vScales, float* out, float* scoresScratch,
                                       int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
                                       int cacheLen, float scale, mantleHipStream_t stream) {
-    if (start != 0 || (cacheLen > 0 && cacheLen <= pos) || pos < 0 || kvHeads <= 0 || nHead % kvHeads)
-        return hipErrorInvalidValue;
-    AttnArgs a{};
-    a.q = q;
-    a.cache_k = reinterpret_cast<float*>(const_cast<int8_t*>(cacheK));  // int8 values
-    a.cache_v = reinterpret_cast<float*>(const_cast<int8_t*>(cacheV));
-    a.k_type = a.v_type = kKvQ8;
-    a.k_scale = kScales;
-    a.v_scale = vScales;
-    a.scores = scoresScratch;
-    a.out = out;
-    a.pos_host = pos;
-    a.n_head = nHead;
-    a.kv_heads = kvHeads;
-    a.head_dim = headDim;
-    a.kv_stride = kvStride;
-    a.head_stride = headDim;
-    a.max_ctx = pos + 1;
-    a.scale = scale;
-    a.fused = 0;
-    a.isa = g_isa.load();
-    return launch_attention_decode(a, S(stream));
+    if (!kScales || !vScales) return hipErrorInvalidValue;
+    return attention_rows(q, cacheK, cacheV, kKvQ8, kKvQ8, kScales, vScales, out, scoresScratch, pos, start, kvStride,
+                          headDim, nHead, kvHeads, cacheLen, scale, S(stream));
 }
 
 int mantleHipStoreKVQ8Row(int8_t* cacheK, int8_t* cacheV, float* kScales, float* vScales, const float* k,

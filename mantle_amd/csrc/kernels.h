@@ -118,6 +118,10 @@ struct AttnArgs {
                            // cache_v + (g*head_dim + d)*vt_stride + t (split paths only)
     unsigned* counters;    // [n_head] zeroed arrival counters of the one-launch split path (null: the
                            // library's own, for callers that serialise their launches on one stream)
+    int key_base, key_ring;  // row-major caches only (fused 0, vt_stride 0), split path: the
+                             // window's key t (0..pos) is cache row (key_base + t), taken
+                             // mod key_ring when key_ring > 0 (RunAttnHeads' window start
+                             // and ring, attnpool.go:88-99)
     const float* k_scale;  // a q8_0 cache holds int8 rows with one scale per position in k_scale /
     const float* v_scale;  // v_scale [max_ctx] (two-launch split path only).  Its step rows must
                            // already be in the cache (fused: launch_kv_append_q8 prepares and
@@ -158,6 +162,8 @@ hipError_t launch_softmax_rows(float* data, int rows, int cols, hipStream_t stre
 hipError_t launch_rope_table(float* x, const float* cosv, const float* sinv, int head_dim, int half, int n_heads,
                              hipStream_t stream);
 hipError_t launch_rope_f64(float* x, const double* inv_freq, int pos, float attn_scale, int head_dim, int half,
+                           int n_heads, hipStream_t stream);
+hipError_t launch_rope_f32(float* x, const float* inv_freq, int pos, float attn_scale, int head_dim, int half,
                            int n_heads, hipStream_t stream);
 hipError_t launch_store_kv_row(float* cache, const float* src, int cache_pos, int kv_stride, hipStream_t stream);
 hipError_t launch_store_kv_row_f16(uint16_t* cache, const float* src, int cache_pos, int kv_stride,

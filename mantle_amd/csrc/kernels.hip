@@ -732,13 +732,17 @@ hipError_t launch_rope_table(float* x, const float* cosv, const float* sinv, int
     return hipGetLastError();
 }
 
-// RoPE from float64 inverse frequencies (Mantle keeps invFreq as []float64,
-// internal/backend/simd/loader.go:1604-1612); cos/sin evaluated in f64.
-__global__ void rope_f64_kernel(float* x, const double* inv_freq, int pos, float attn_scale, int head_dim, int half) {
+// RoPE from inverse frequencies: float64 (Mantle's CPU invFreq []float64,
+// internal/backend/simd/loader.go:1604-1612) or float32 (the CUDA backend's
+// pre-uploaded table, internal/backend/cuda/native/attn_fused.cu:51-58);
+// either way the angle pos * invFreq[i] and its cos / sin are evaluated in
+// f64 as applyRoPE does (ops_avx512.go:146-160), then the CPU's pair update.
+template <typename F>
+__global__ void rope_freq_kernel(float* x, const F* inv_freq, int pos, float attn_scale, int head_dim, int half) {
     float* lo = x + (size_t)blockIdx.x * head_dim;
     float* hi = lo + half;
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const double ang = (double)pos * inv_freq[i];
+        const double ang = (double)pos * (double)inv_freq[i];
         float c = (float)cos(ang), s = (float)sin(ang);
         if (attn_scale != 1.0f) {
             c = c * attn_scale;
@@ -750,13 +754,25 @@ __global__ void rope_f64_kernel(float* x, const double* inv_freq, int pos, float
     }
 }
 
-hipError_t launch_rope_f64(float* x, const double* inv_freq, int pos, float attn_scale, int head_dim, int half,
-                           int n_heads, hipStream_t stream) {
+template <typename F>
+static hipError_t launch_rope_freq(float* x, const F* inv_freq, int pos, float attn_scale, int head_dim, int half,
+                                   int n_heads, hipStream_t stream) {
     if (!x || !inv_freq || head_dim <= 0 || half <= 0 || half * 2 > head_dim || n_heads <= 0 || pos < 0)
         return hipErrorInvalidValue;
     if (attn_scale == 0.0f) attn_scale = 1.0f;
-    hipLaunchKernelGGL(rope_f64_kernel, dim3(n_heads), dim3(128), 0, stream, x, inv_freq, pos, attn_scale, head_dim, half);
+    hipLaunchKernelGGL(rope_freq_kernel<F>, dim3(n_heads), dim3(128), 0, stream, x, inv_freq, pos, attn_scale,
+                       head_dim, half);
     return hipGetLastError();
+}
+
+hipError_t launch_rope_f64(float* x, const double* inv_freq, int pos, float attn_scale, int head_dim, int half,
+                           int n_heads, hipStream_t stream) {
+    return launch_rope_freq(x, inv_freq, pos, attn_scale, head_dim, half, n_heads, stream);
+}
+
+hipError_t launch_rope_f32(float* x, const float* inv_freq, int pos, float attn_scale, int head_dim, int half,
+                           int n_heads, hipStream_t stream) {
+    return launch_rope_freq(x, inv_freq, pos, attn_scale, head_dim, half, n_heads, stream);
 }
 
 __global__ void store_kv_row_kernel(float* cache, const float* src, int cache_pos, int kv_stride) {

@@ -72,6 +72,8 @@ struct mantleHipModel {
     int* out_tokens = nullptr;
     int pos = 0;  // host mirror of state->pos
     bool use_graph = true;
+    bool split = false;  // split attention kernels (transposed V cache)
+    int load_ctx = 0;    // maxContext given at load (SetEffectiveContextLength(0) restores it)
     hipGraphExec_t graph = nullptr;
 };
 
@@ -338,9 +340,124 @@ extern "C" void mantleHipModelClose(mantleHipModel* m) {
     free_model(m);
 }
 
+// Everything sized by the context length: scores, KV caches (+ q8_0
+// scales), prompt / output tokens and the RoPE tables
+// (internal/backend/simd/loader.go:1604-1612, ops_avx512.go:146-160: cos / sin
+// of pos * invFreq in f64 on the host).  Frees what was there first.
+static void free_context(mantleHipModel* m) {
+    void* bufs[] = {m->scores, m->cache_k, m->cache_v, m->k_scale, m->v_scale, m->prompt, m->out_tokens, m->rope_cos, m->rope_sin};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    m->scores = nullptr;
+    m->cache_k = m->cache_v = m->k_scale = m->v_scale = m->rope_cos = m->rope_sin = nullptr;
+    m->prompt = m->out_tokens = nullptr;
+}
+
+static hipError_t rope_tables(mantleHipModel* m) {
+    const mantleHipQwen3Config& c = m->cfg;
+    const int half = c.head_dim / 2, ctx = m->max_ctx;
+    std::vector<float> cs_tab((size_t)ctx * half), sn_tab((size_t)ctx * half);
+    std::vector<double> inv(half);
+    for (int i = 0; i < half; i++)
+        inv[i] = 1.0 / pow(c.rope_base > 0 ? c.rope_base : 10000.0, (double)(2 * i) / (double)c.head_dim);
+    for (int p = 0; p < ctx; p++)
+        for (int i = 0; i < half; i++) {
+            double ang = (double)p * inv[i];
+            cs_tab[(size_t)p * half + i] = (float)cos(ang);
+            sn_tab[(size_t)p * half + i] = (float)sin(ang);
+        }
+    hipError_t e = hipMemcpy(m->rope_cos, cs_tab.data(), sizeof(float) * cs_tab.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(m->rope_sin, sn_tab.data(), sizeof(float) * sn_tab.size(), hipMemcpyHostToDevice);
+    return e;
+}
+
+static hipError_t alloc_context(mantleHipModel* m, int ctx) {
+    const mantleHipQwen3Config& c = m->cfg;
+    const bool any_q8 = m->k_type == kKvQ8 || m->v_type == kKvQ8;
+    if ((any_q8 || m->k_type != m->v_type) && (ctx > 32768 || (any_q8 && m->kv_dim > kKvQ8MaxRow))) {
+        fprintf(stderr, "mantle_hip: q8_0 and mixed KV caches support up to 32768 positions (q8_0: %d values per row)\n",
+                kKvQ8MaxRow);
+        return hipErrorInvalidValue;
+    }
+    free_context(m);
+    m->max_ctx = ctx;
+    hipError_t e;
+#define TRYA(x)                        \
+    do {                               \
+        if ((e = (x)) != hipSuccess) { \
+            free_context(m);           \
+            return e;                  \
+        }                              \
+    } while (0)
+    TRYA(hipMalloc((void**)&m->scores, sizeof(float) * (size_t)c.n_heads * ctx));
+    const size_t kv_elems = (size_t)c.n_layers * ctx * m->kv_dim;
+    // transposed V: a column's keys padded to 16 bytes (4 fp32, 8 f16, 16 int8 keys)
+    const int vt_pad = m->v_type == kKvQ8 ? 16 : 4;
+    m->vt_stride = m->split ? (ctx + vt_pad - 1) / vt_pad * vt_pad : 0;
+    m->v_rows = m->split ? m->vt_stride : ctx;
+    const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
+    TRYA(hipMalloc((void**)&m->cache_k, kv_elem_bytes(m->k_type) * kv_elems));
+    TRYA(hipMalloc((void**)&m->cache_v, kv_elem_bytes(m->v_type) * v_elems));
+    TRYA(hipMemset(m->cache_k, 0, kv_elem_bytes(m->k_type) * kv_elems));
+    TRYA(hipMemset(m->cache_v, 0, kv_elem_bytes(m->v_type) * v_elems));
+    if (m->k_type == kKvQ8) {
+        TRYA(hipMalloc((void**)&m->k_scale, sizeof(float) * (size_t)c.n_layers * ctx));
+        TRYA(hipMemset(m->k_scale, 0, sizeof(float) * (size_t)c.n_layers * ctx));
+    }
+    if (m->v_type == kKvQ8) {
+        TRYA(hipMalloc((void**)&m->v_scale, sizeof(float) * (size_t)c.n_layers * ctx));
+        TRYA(hipMemset(m->v_scale, 0, sizeof(float) * (size_t)c.n_layers * ctx));
+    }
+    TRYA(hipMalloc((void**)&m->prompt, sizeof(int) * ctx));
+    TRYA(hipMalloc((void**)&m->out_tokens, sizeof(int) * ctx));
+    TRYA(hipMemset(m->prompt, 0, sizeof(int) * ctx));
+    TRYA(hipMemset(m->out_tokens, 0, sizeof(int) * ctx));
+    TRYA(hipMalloc((void**)&m->rope_cos, sizeof(float) * (size_t)ctx * (c.head_dim / 2)));
+    TRYA(hipMalloc((void**)&m->rope_sin, sizeof(float) * (size_t)ctx * (c.head_dim / 2)));
+    TRYA(rope_tables(m));
+#undef TRYA
+    // the captured step holds the old buffers
+    if (m->graph) {
+        (void)hipGraphExecDestroy(m->graph);
+        m->graph = nullptr;
+    }
+    return hipSuccess;
+}
+
+// What a model is built from: the HF config.json text and the named tensor
+// payloads (an MCF file's, or views the caller holds, e.g. Go's
+// mcfstore.File.ReadTensorRaw results).
+struct SrcTensor {
+    std::string name;
+    uint16_t dtype;
+    std::vector<uint64_t> shape;
+    const uint8_t* data;
+    uint64_t size;
+};
+struct ModelSource {
+    std::string config_json;
+    std::vector<SrcTensor> tensors;
+    int find(const std::string& n) const {
+        for (size_t i = 0; i < tensors.size(); i++)
+            if (tensors[i].name == n) return (int)i;
+        return -1;
+    }
+};
+
+static bool source_from_mcf(const McfFile& f, ModelSource* src, const char* path) {
+    const McfSection* cs = f.section(kSecHFConfigJSON);
+    if (!cs) {
+        fprintf(stderr, "mantle_hip: %s: missing config.json section\n", path);
+        return false;
+    }
+    src->config_json.assign((const char*)f.data() + cs->off, cs->size);
+    for (const McfTensor& t : f.tensors()) src->tensors.push_back({t.name, t.dtype, t.shape, f.data() + t.off, t.size});
+    return true;
+}
+
 // LoadModelMCF (internal/backend/simd/loader.go:51-80 + internal/backend/cuda/cuda.go:39-73,
 // internal/backend/cuda/ops.go:5214-5313 weight residency).
-static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions& o, mantleHipModel** out,
+static int load_model(const ModelSource& f, int max_ctx, const mantleHipLoadOptions& o, mantleHipModel** out,
                       const char* path);
 
 // The process-wide settings (mantleHipSetParityISA / mantleHipSetKVCacheType)
@@ -378,7 +495,9 @@ extern "C" int mantleHipModelLoadMCFWithOptions(const char* path, int max_ctx, c
         fprintf(stderr, "mantle_hip: %s: %s\n", path, err.c_str());
         return hipErrorInvalidValue;
     }
-    return load_model(f, max_ctx, o, out, path);
+    ModelSource src;
+    if (!source_from_mcf(f, &src, path)) return hipErrorInvalidValue;
+    return load_model(src, max_ctx, o, out, path);
 }
 
 extern "C" int mantleHipModelLoadMCFImageWithOptions(const uint8_t* data, uint64_t size, int max_ctx,
@@ -393,17 +512,37 @@ extern "C" int mantleHipModelLoadMCFImageWithOptions(const uint8_t* data, uint64
         fprintf(stderr, "mantle_hip: MCF image: %s\n", err.c_str());
         return hipErrorInvalidValue;
     }
-    return load_model(f, max_ctx, o, out, "MCF image");
+    ModelSource src;
+    if (!source_from_mcf(f, &src, "MCF image")) return hipErrorInvalidValue;
+    return load_model(src, max_ctx, o, out, "MCF image");
 }
 
-static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions& o, mantleHipModel** out,
-                      const char* path) {
-    const McfSection* cs = f.section(kSecHFConfigJSON);
-    if (!cs) {
-        fprintf(stderr, "mantle_hip: %s: missing config.json section\n", path);
-        return hipErrorInvalidValue;
+extern "C" int mantleHipModelLoadTensors(const char* configJSON, uint64_t configSize, const mantleHipTensorView* tensors,
+                                         int nTensors, int max_ctx, const mantleHipLoadOptions* opts,
+                                         mantleHipModel** out) {
+    if (!configJSON || !tensors || nTensors <= 0 || !out || max_ctx <= 0) return hipErrorInvalidValue;
+    *out = nullptr;
+    const mantleHipLoadOptions o = opts ? *opts : default_options();
+    if (!options_valid(&o)) return hipErrorInvalidValue;
+    ModelSource src;
+    src.config_json.assign(configJSON, configSize);
+    for (int i = 0; i < nTensors; i++) {
+        const mantleHipTensorView& t = tensors[i];
+        if (!t.name || t.rank < 1 || t.rank > 4) return hipErrorInvalidValue;
+        std::vector<uint64_t> shape;
+        for (int d = 0; d < t.rank; d++) {
+            if (t.shape[d] <= 0) return hipErrorInvalidValue;
+            shape.push_back((uint64_t)t.shape[d]);
+        }
+        src.tensors.push_back({t.name, (uint16_t)t.dtype, shape, t.data, t.size});
     }
-    std::string js((const char*)f.data() + cs->off, cs->size);
+    return load_model(src, max_ctx, o, out, "tensor views");
+}
+
+static int load_model(const ModelSource& f, int max_ctx, const mantleHipLoadOptions& o, mantleHipModel** out,
+                      const char* path) {
+    (void)path;
+    const std::string& js = f.config_json;
     mantleHipModel* m = new mantleHipModel();
     mantleHipQwen3Config& c = m->cfg;
     double v;
@@ -433,6 +572,7 @@ static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions&
     c.eps = json_number(js, "rms_norm_eps", &v) ? (float)v : 1e-6f;
     c.tie_embeddings = f.find("lm_head.weight") < 0;
     m->max_ctx = max_ctx;
+    m->load_ctx = max_ctx;
     m->isa = o.parity_isa;
     m->use_graph = o.use_graph != 0;
     m->q_dim = c.n_heads * c.head_dim;
@@ -446,7 +586,7 @@ static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions&
     // Rank-2 weights are all k4 or all raw bf16 (the embedding's dtype decides).
     {
         const int ei = f.find("model.embed_tokens.weight");
-        m->bf16 = ei >= 0 && f.tensors()[ei].dtype == kDTypeBF16;
+        m->bf16 = ei >= 0 && f.tensors[ei].dtype == kDTypeBF16;
     }
     c.weight_dtype = m->bf16 ? kDTypeBF16 : kDTypeK4;
     const uint16_t wdt = m->bf16 ? (uint16_t)kDTypeBF16 : (uint16_t)kDTypeK4;
@@ -489,10 +629,14 @@ static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions&
             free_model(m);
             return hipErrorInvalidValue;
         }
-        const McfTensor& t = f.tensors()[i];
+        const SrcTensor& t = f.tensors[i];
         bool shape_ok = w.dtype != kDTypeF32
                             ? (t.shape.size() == 2 && (int64_t)t.shape[0] == w.rows && (int64_t)t.shape[1] == w.cols)
                             : (t.shape.size() == 1 && (int64_t)t.shape[0] == w.rows);
+        const int64_t elems = w.dtype == kDTypeF32 ? w.rows : w.rows * w.cols;
+        const uint64_t want_size = w.dtype == kDTypeK4 ? (uint64_t)k4_payload_bytes(w.rows, w.cols)
+                                                       : (uint64_t)elems * (w.dtype == kDTypeF32 ? 4 : 2);
+        if (shape_ok && (t.size != want_size || !t.data)) shape_ok = false;
         if (t.dtype != w.dtype || !shape_ok) {
             fprintf(stderr, "mantle_hip: tensor %s has unexpected dtype/shape\n", w.name.c_str());
             free_model(m);
@@ -514,8 +658,8 @@ static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions&
     CHECK(hipMalloc((void**)&m->arena, total));
     m->arena_bytes = total;
     for (size_t j = 0; j < wants.size(); j++) {
-        const McfTensor& t = f.tensors()[tidx[j]];
-        CHECK(hipMemcpy(m->arena + wants[j].arena_off, f.data() + t.off, t.size, hipMemcpyHostToDevice));
+        const SrcTensor& t = f.tensors[tidx[j]];
+        CHECK(hipMemcpy(m->arena + wants[j].arena_off, t.data, t.size, hipMemcpyHostToDevice));
     }
     size_t wi = 0;
     auto nextk = [&](int rows, int cols) { return k4_mat_from_payload(m->arena + wants[wi++].arena_off, rows, cols); };
@@ -566,66 +710,23 @@ static int load_model(const McfFile& f, int max_ctx, const mantleHipLoadOptions&
         CHECK(hipMalloc((void**)&m->up, sizeof(float) * c.ffn));
     }
     CHECK(hipMalloc((void**)&m->logits, sizeof(float) * c.vocab));
-    CHECK(hipMalloc((void**)&m->scores, sizeof(float) * (size_t)c.n_heads * max_ctx));
     CHECK(hipMalloc((void**)&m->attn_counters, sizeof(unsigned) * c.n_heads));
     CHECK(hipMemset(m->attn_counters, 0, sizeof(unsigned) * c.n_heads));
     CHECK(hipMalloc((void**)&m->qx, (size_t)big_blocks * 32));
     CHECK(hipMalloc((void**)&m->xs, sizeof(float) * big_blocks));
-    const size_t kv_elems = (size_t)c.n_layers * max_ctx * m->kv_dim;
     const int apath = attention_path();
     const bool split = (c.head_dim == 64 || c.head_dim == 128) && (apath == kAttnPathSplit || apath == kAttnPathFused);
     m->k_type = o.cache_type_k;
     m->v_type = o.cache_type_v;
-    const bool any_q8 = m->k_type == kKvQ8 || m->v_type == kKvQ8;
     if ((m->k_type != kKvF32 || m->v_type != kKvF32) && !split) {
         fprintf(stderr, "mantle_hip: the f16 / q8_0 KV cache needs head_dim 64/128 and a split attention path\n");
         free_model(m);
         return hipErrorInvalidValue;
     }
-    if ((any_q8 || m->k_type != m->v_type) && (max_ctx > 32768 || (any_q8 && m->kv_dim > kKvQ8MaxRow))) {
-        fprintf(stderr, "mantle_hip: q8_0 and mixed KV caches support up to 32768 positions (q8_0: %d values per row)\n",
-                kKvQ8MaxRow);
-        free_model(m);
-        return hipErrorInvalidValue;
-    }
-    // transposed V: a column's keys padded to 16 bytes (4 fp32, 8 f16, 16 int8 keys)
-    const int vt_pad = m->v_type == kKvQ8 ? 16 : 4;
-    m->vt_stride = split ? (max_ctx + vt_pad - 1) / vt_pad * vt_pad : 0;
-    m->v_rows = split ? m->vt_stride : max_ctx;
-    const size_t v_elems = (size_t)c.n_layers * m->v_rows * m->kv_dim;
-    CHECK(hipMalloc((void**)&m->cache_k, kv_elem_bytes(m->k_type) * kv_elems));
-    CHECK(hipMalloc((void**)&m->cache_v, kv_elem_bytes(m->v_type) * v_elems));
-    if (m->k_type == kKvQ8) {
-        CHECK(hipMalloc((void**)&m->k_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
-        CHECK(hipMemset(m->k_scale, 0, sizeof(float) * (size_t)c.n_layers * max_ctx));
-    }
-    if (m->v_type == kKvQ8) {
-        CHECK(hipMalloc((void**)&m->v_scale, sizeof(float) * (size_t)c.n_layers * max_ctx));
-        CHECK(hipMemset(m->v_scale, 0, sizeof(float) * (size_t)c.n_layers * max_ctx));
-    }
+    m->split = split;
     CHECK(hipMalloc((void**)&m->state, sizeof(DecodeState)));
-    CHECK(hipMalloc((void**)&m->prompt, sizeof(int) * max_ctx));
-    CHECK(hipMalloc((void**)&m->out_tokens, sizeof(int) * max_ctx));
-    // RoPE tables (internal/backend/simd/loader.go:1604-1612, ops_avx512.go:146-160), host f64.
-    const int half = c.head_dim / 2;
-    std::vector<float> cs_tab((size_t)max_ctx * half), sn_tab((size_t)max_ctx * half);
-    std::vector<double> inv(half);
-    for (int i = 0; i < half; i++) inv[i] = 1.0 / pow(c.rope_base > 0 ? c.rope_base : 10000.0, (double)(2 * i) / (double)c.head_dim);
-    for (int p = 0; p < max_ctx; p++)
-        for (int i = 0; i < half; i++) {
-            double ang = (double)p * inv[i];
-            cs_tab[(size_t)p * half + i] = (float)cos(ang);
-            sn_tab[(size_t)p * half + i] = (float)sin(ang);
-        }
-    CHECK(hipMalloc((void**)&m->rope_cos, sizeof(float) * cs_tab.size()));
-    CHECK(hipMalloc((void**)&m->rope_sin, sizeof(float) * sn_tab.size()));
-    CHECK(hipMemcpy(m->rope_cos, cs_tab.data(), sizeof(float) * cs_tab.size(), hipMemcpyHostToDevice));
-    CHECK(hipMemcpy(m->rope_sin, sn_tab.data(), sizeof(float) * sn_tab.size(), hipMemcpyHostToDevice));
     CHECK(hipMemset(m->state, 0, sizeof(DecodeState)));
-    CHECK(hipMemset(m->prompt, 0, sizeof(int) * max_ctx));
-    CHECK(hipMemset(m->out_tokens, 0, sizeof(int) * max_ctx));
-    CHECK(hipMemset(m->cache_k, 0, kv_elem_bytes(m->k_type) * kv_elems));
-    CHECK(hipMemset(m->cache_v, 0, kv_elem_bytes(m->v_type) * v_elems));
+    CHECK(alloc_context(m, max_ctx));
     CHECK(hipDeviceSynchronize());
 #undef CHECK
     *out = m;
@@ -699,6 +800,44 @@ extern "C" int mantleHipModelPrefillTokens(mantleHipModel* m, const int* toks, i
             return e;
     }
     return hipStreamSynchronize(m->stream);
+}
+
+// prefillForwarder.PrefillTokens (internal/inference/engine.go:28-30): the
+// prompt, then the logits of its last position (vocab floats, host).
+extern "C" int mantleHipModelPrefillTokensLogits(mantleHipModel* m, const int* toks, int n, float* logits) {
+    if (!m || !toks || n <= 0 || !logits) return hipErrorInvalidValue;
+    hipError_t e = (hipError_t)mantleHipModelPrefillTokens(m, toks, n, nullptr);
+    if (e != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(logits, m->logits, sizeof(float) * m->cfg.vocab, hipMemcpyDeviceToHost, m->stream)) !=
+        hipSuccess)
+        return e;
+    return hipStreamSynchronize(m->stream);
+}
+
+// SetEffectiveContextLength (internal/backend/core/instance.go:325-339,
+// internal/backend/cuda/cuda.go:237-250): size the KV cache and the other
+// context-sized buffers for ctxLen positions (0: the maxContext given at
+// load, which is also the upper bound).  Only before the first token (or
+// after Reset): the caches are reallocated, not copied.
+extern "C" int mantleHipModelSetEffectiveContextLength(mantleHipModel* m, int ctxLen) {
+    if (!m || ctxLen < 0) return hipErrorInvalidValue;
+    const int want = ctxLen == 0 || ctxLen > m->load_ctx ? m->load_ctx : ctxLen;
+    if (m->pos != 0) return hipErrorInvalidValue;
+    if (want == m->max_ctx) return hipSuccess;
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) return e;
+    return alloc_context(m, want);
+}
+
+// core.Runtime.UpdateRoPE (internal/backend/core/interfaces.go:14-18): the RoPE
+// tables recomputed after the caller changed the RoPE base (ropeBase > 0;
+// 0 keeps the current one).
+extern "C" int mantleHipModelUpdateRoPE(mantleHipModel* m, double ropeBase) {
+    if (!m || ropeBase < 0) return hipErrorInvalidValue;
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) return e;
+    if (ropeBase > 0) m->cfg.rope_base = ropeBase;
+    return rope_tables(m);
 }
 
 extern "C" int mantleHipModelGenerateGreedy(mantleHipModel* m, const int* prompt, int n_prompt, int n_gen,

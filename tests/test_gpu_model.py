@@ -263,3 +263,82 @@ def test_lane_mixed_kv_cache_types(hip, lane_path, kt, vt, ctx):
     finally:
         rt.close()
         om.close()
+
+
+def test_load_from_tensor_views_matches_mcf_load(hip, lane_path):
+    """mantleHipModelLoadTensors (a Go LoadModel feeding mcfstore.File's
+    ReadTensorRaw payloads and the config.json section) builds the same model
+    as loading the MCF file: identical logits per step."""
+    import mantle_amd
+    from mantle_amd.mcf import MCFFile
+    f = MCFFile(lane_path)
+    items = [(n, t["dtype"], t["shape"], f.raw(n).copy()) for n, t in f.tensors.items()]
+    cfg_json = f.section(0x0100)
+    a = mantle_amd.new_backend().load_model(lane_path, max_context=48)
+    b = mantle_amd.new_backend().load_model_tensors(cfg_json, reversed(items), max_context=48)
+    try:
+        tok = 5
+        for _ in range(8):
+            la, lb = a.forward_token(tok), b.forward_token(tok)
+            np.testing.assert_array_equal(la.view(np.uint32), lb.view(np.uint32))
+            tok = int(np.argmax(la))
+    finally:
+        a.close()
+        b.close()
+        f.close()
+
+
+def test_prefill_tokens_logits_and_effective_context(hip, lane_path):
+    """PrefillTokens([]int) ([]float32, error) (internal/inference/engine.go:28-30):
+    the last prompt position's logits equal the oracle's; SetEffectiveContextLength
+    (internal/backend/core/instance.go:325-339) shrinks the caches before the first
+    token without changing a result, and is refused mid-sequence."""
+    import mantle_amd
+    from mantle_amd import _lib
+    prompt = models.prompt(40, models.LANE["vocab"], 12)
+    rt = mantle_amd.new_backend().load_model(lane_path, max_context=400)
+    om = models.oracle_model(lane_path, models.LANE, 400)
+    try:
+        rt.set_effective_context_length(64)
+        assert rt.max_context == 64
+        logits = rt.prefill_tokens_logits(prompt)
+        want = None
+        for t in prompt:
+            _, want = om.forward_greedy(t, want_logits=True)
+        np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32))
+        assert _lib.lib().mantleHipModelSetEffectiveContextLength(rt._handle(), 128) == 1  # pos != 0
+        tok = int(np.argmax(logits))
+        for _ in range(20):  # up to position 60 of the 64
+            lg = rt.forward_token(tok)
+            nxt, w = om.forward_greedy(tok, want_logits=True)
+            np.testing.assert_array_equal(lg.view(np.uint32), w.view(np.uint32))
+            tok = nxt
+        rt.reset()
+        rt.set_effective_context_length(0)  # back to the load-time 400
+        assert rt.max_context == 400
+        assert rt.forward_token_greedy(prompt[0]) >= 0
+    finally:
+        rt.close()
+        om.close()
+
+
+def test_update_rope_recomputes_tables(hip, lane_path):
+    """core.Runtime.UpdateRoPE (internal/backend/core/interfaces.go:14-18): with a
+    new RoPE base the logits follow the oracle built with that base; with the
+    same base nothing changes."""
+    import mantle_amd
+    rt = mantle_amd.new_backend().load_model(lane_path, max_context=32)
+    om = models.oracle_model(lane_path, dict(models.LANE, rope_base=5e4), 32)
+    try:
+        rt.update_rope(0.0)
+        rt.update_rope(5e4)
+        assert rt.model_config()["rope_base"] == 5e4
+        tok = 9
+        for _ in range(6):
+            lg = rt.forward_token(tok)
+            nxt, w = om.forward_greedy(tok, want_logits=True)
+            np.testing.assert_array_equal(lg.view(np.uint32), w.view(np.uint32))
+            tok = nxt
+    finally:
+        rt.close()
+        om.close()

@@ -78,8 +78,8 @@ def test_rope_f64_close(hip, oracle):
     x = np.random.default_rng(1).standard_normal(hd * nh).astype(np.float32)
     inv = np.array([1.0 / (1e6 ** (2 * i / hd)) for i in range(hd // 2)], dtype=np.float64)
     xd = g.dev(x)
-    g.call("mantleHipApplyRoPEInplaceF32", g.ptr(xd), g.ptr(g.keep(inv)), pos, ctypes.c_float(1.0), hd, hd // 2, nh,
-           g.stream())
+    g.call("mantleHipApplyRoPEInplaceF64FreqF32", g.ptr(xd), g.ptr(g.keep(inv)), pos, ctypes.c_float(1.0), hd, hd // 2,
+           nh, g.stream())
     c, s = oracle.rope_tables(1e6, hd, pos)
     np.testing.assert_allclose(g.host(xd), oracle.apply_rope(x, nh, hd, c, s), rtol=1e-6, atol=1e-6)
 
@@ -242,16 +242,121 @@ def test_attention_f16_cache_bitexact(hip, oracle, path, isa, n_head, kv_heads, 
     g.call("mantleHipSetAttentionPath", ATTN_PATHS[path])
     try:
         out = g.empty(n_head * head_dim)
-        scratch = g.empty(n_head * (pos + 1))
+        # mantleCudaAttentionInnerF16CacheF32's argument list (softmax.h:70-83): no scratch
         g.call("mantleHipAttentionInnerF16CacheF32", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)),
-               g.ptr(out), g.ptr(scratch), pos, 0, kv, head_dim, n_head, kv_heads, pos + 1, ctypes.c_float(scale),
-               g.stream())
+               g.ptr(out), pos, 0, kv, head_dim, n_head, kv_heads, pos + 1, ctypes.c_float(scale), g.stream())
         got = g.host(out)
     finally:
         g.call("mantleHipSetAttentionPath", 0)
         g.call("mantleHipSetParityISA", 2)
     g.assert_bitexact(got, oracle.attn_heads_f16(q, ck, cv, pos, kv, head_dim, n_head, kv_heads, float(scale)),
                       "f16 attention")
+
+
+def _mixed_cache(oracle, kind, x, rows, kv):
+    """A row-major cache of `kind` from fp32 rows x: (cache, per-row scales or None)."""
+    if kind == "f32":
+        return x.astype(np.float32), None
+    if kind == "f16":
+        return _f16(oracle, x), None
+    q = np.empty(rows * kv, np.int8)
+    sc = np.empty(rows, np.float32)
+    for t in range(rows):
+        q[t * kv:(t + 1) * kv], sc[t] = oracle.store_q8(x[t * kv:(t + 1) * kv])
+    return q, sc
+
+
+@pytest.mark.parametrize("kt,vt", [("f16", "q8_0"), ("q8_0", "f16"), ("q8_0", "q8_0"), ("f16", "f16")])
+@pytest.mark.parametrize("pos", [0, 200, 1100])
+def test_attention_mixed_cache_entry_bitexact(hip, oracle, kt, vt, pos):
+    """mantleCudaAttentionInnerMixedCacheF32's argument list (softmax.h:84-104):
+    each of K and V f16 or q8_0, RunAttnHeads' arithmetic per type
+    (attnpool.go:100-135), bit-identical to the oracle."""
+    n_head, kv_heads, head_dim = 16, 8, 128
+    kv = kv_heads * head_dim
+    rng = np.random.default_rng(pos + 3)
+    q = rng.standard_normal(n_head * head_dim).astype(np.float32)
+    kx = (rng.standard_normal((pos + 1) * kv) * 2).astype(np.float32)
+    vx = rng.standard_normal((pos + 1) * kv).astype(np.float32)
+    ck, ks = _mixed_cache(oracle, kt, kx, pos + 1, kv)
+    cv, vs = _mixed_cache(oracle, vt, vx, pos + 1, kv)
+    scale = np.float32(1.0 / np.sqrt(head_dim))
+    out = g.empty(n_head * head_dim)
+    dk, dv = g.keep(ck), g.keep(cv)
+    dks = g.keep(ks) if ks is not None else None
+    dvs = g.keep(vs) if vs is not None else None
+    g.call("mantleHipAttentionInnerMixedCacheF32", g.ptr(g.keep(q)),
+           g.ptr(dk) if kt == "f16" else None, g.ptr(dv) if vt == "f16" else None,
+           g.ptr(dk) if kt == "q8_0" else None, g.ptr(dv) if vt == "q8_0" else None,
+           g.ptr(dks) if dks is not None else None, g.ptr(dvs) if dvs is not None else None, g.ptr(out),
+           int(kt == "q8_0"), int(vt == "q8_0"), pos, 0, kv, head_dim, n_head, kv_heads, 0, ctypes.c_float(scale),
+           g.stream())
+    want = oracle.attn_heads_mixed(2, q, kt, ck, ks, vt, cv, vs, pos, 0, 0, kv, head_dim, n_head, kv_heads,
+                                   float(scale))
+    g.assert_bitexact(g.host(out), want, f"mixed attention {kt}/{vt}")
+
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("pos,start,cache_len", [(300, 0, 0), (300, 45, 0), (300, 45, 256), (999, 744, 256),
+                                                 (130, 0, 100)])
+def test_attention_window_and_ring_bitexact(hip, oracle, kind, pos, start, cache_len):
+    """RunAttnHeads' window start and ring placement (attnpool.go:88-99: key t at
+    row t % cacheLen when 0 < cacheLen < pos + 1) through the C ABI, each cache
+    type; (130, 0, 100) is the ring read past its length (keys wrap onto
+    overwritten rows, as the CPU reads them)."""
+    n_head, kv_heads, head_dim = 16, 8, 128
+    kv = kv_heads * head_dim
+    rows = cache_len if 0 < cache_len < pos + 1 else pos + 1
+    rng = np.random.default_rng(pos + start + cache_len)
+    q = rng.standard_normal(n_head * head_dim).astype(np.float32)
+    ck, ks = _mixed_cache(oracle, kind, (rng.standard_normal(rows * kv) * 2).astype(np.float32), rows, kv)
+    cv, vs = _mixed_cache(oracle, kind, rng.standard_normal(rows * kv).astype(np.float32), rows, kv)
+    scale = np.float32(1.0 / np.sqrt(head_dim))
+    win = pos - start + 1
+    out = g.empty(n_head * head_dim)
+    scratch = g.empty(n_head * win)
+    if kind == "f32":
+        g.call("mantleHipAttentionInnerF32Cache", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)), g.ptr(out),
+               g.ptr(scratch), pos, start, kv, head_dim, n_head, kv_heads, cache_len, ctypes.c_float(scale), g.stream())
+    elif kind == "f16":
+        g.call("mantleHipAttentionInnerF16CacheF32", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)),
+               g.ptr(out), pos, start, kv, head_dim, n_head, kv_heads, cache_len, ctypes.c_float(scale), g.stream())
+    else:
+        g.call("mantleHipAttentionInnerQ8CacheF32", g.ptr(g.keep(q)), g.ptr(g.keep(ck)), g.ptr(g.keep(cv)),
+               g.ptr(g.keep(ks)), g.ptr(g.keep(vs)), g.ptr(out), g.ptr(scratch), pos, start, kv, head_dim, n_head,
+               kv_heads, cache_len, ctypes.c_float(scale), g.stream())
+    want = oracle.attn_heads_mixed(2, q, kind, ck, ks, kind, cv, vs, pos, start, cache_len, kv, head_dim, n_head,
+                                   kv_heads, float(scale))
+    g.assert_bitexact(g.host(out), want, f"window/ring {kind} pos={pos} start={start} cacheLen={cache_len}")
+
+
+def test_rope_f32_invfreq_reference_kat(hip):
+    """TestApplyRoPEInplaceF32 (internal/backend/cuda/native/attn_fused_test.go:32-105):
+    4 heads x 16, pos 7, attnScale 1.25, x = 0.1 i - 1.5, float32 invFreq =
+    1/10000^(2i/16), against applyRoPEScalarRef (float64 angle, cos/sin to float32,
+    scaled) within 1e-4; attnScale 0 is taken as 1."""
+    import math
+    nh, hd, half, pos = 4, 16, 8, 7
+    x = np.array([np.float32(i) * np.float32(0.1) - np.float32(1.5) for i in range(nh * hd)], np.float32)
+    inv = np.array([1.0 / math.pow(10000, 2 * i / hd) for i in range(half)], np.float32)
+
+    def ref(scale):
+        r = x.copy()
+        for h in range(nh):
+            for i in range(half):
+                ang = float(pos) * float(inv[i])
+                c = np.float32(math.cos(ang)) * np.float32(scale)
+                s_ = np.float32(math.sin(ang)) * np.float32(scale)
+                x0, x1 = r[h * hd + i], r[h * hd + i + half]
+                r[h * hd + i] = x0 * c - x1 * s_
+                r[h * hd + i + half] = x0 * s_ + x1 * c
+        return r
+
+    for scale, want_scale in ((1.25, 1.25), (0.0, 1.0)):
+        xd = g.dev(x)
+        g.call("mantleHipApplyRoPEInplaceF32", g.ptr(xd), g.ptr(g.keep(inv)), pos, ctypes.c_float(scale), hd, half,
+               nh, g.stream())
+        np.testing.assert_allclose(g.host(xd), ref(want_scale), atol=1e-4, rtol=0)
 
 
 def test_store_kv_f16_row_truncates(hip, oracle):

@@ -137,20 +137,27 @@ def test_host_validation_rejects_bad_arguments():
     assert L.mantleHipQuantMatVecK4W4A8QF32(fake, fake, fake, fake, fake, fake, 0, 1, 32, 1, None) == 1
     assert L.mantleHipRMSNormF32(None, fake, fake, C.c_float(1e-6), 8, None) == 1
     assert L.mantleHipRMSNormF32(fake, fake, fake, C.c_float(1e-6), 0, None) == 1
-    assert L.mantleHipAttentionInnerF32Cache(fake, fake, fake, fake, fake, 5, 1, 16, 8, 4, 2, 6, C.c_float(1), None) == 1
+    assert L.mantleHipAttentionInnerF32Cache(fake, fake, fake, fake, fake, 5, 6, 16, 8, 4, 2, 6, C.c_float(1), None) == 1  # start > pos
     assert L.mantleHipAttentionInnerF32Cache(fake, fake, fake, fake, fake, 5, 0, 16, 8, 4, 3, 6, C.c_float(1), None) == 1
     assert L.mantleHipApplyRoPEInplaceTableF32(fake, fake, fake, 8, 5, 1, None) == 1
     assert L.mantleHipSoftmaxRowsF32(fake, 0, 4, None) == 1
     assert L.mantleHipArgMaxF32(fake, 0, fake, None) == 1
     assert L.mantleHipSetParityISA(7) == 1
-    # q8_0 cache: rows past 4096 values, a null row, a non-zero start, head_dim 96 (no split kernel)
+    # q8_0 cache: rows past 4096 values, a null row, a start past pos, head_dim 96 (no split kernel)
     assert L.mantleHipStoreKVQ8Row(fake, fake, fake, fake, fake, fake, 0, 5000, None) == 1
     assert L.mantleHipStoreKVQ8Row(fake, fake, fake, fake, None, fake, 0, 1024, None) == 1
     assert L.mantleHipStoreKVQ8Row(fake, fake, fake, fake, fake, fake, 0, 0, None) == 1
-    assert L.mantleHipAttentionInnerQ8CacheF32(fake, fake, fake, fake, fake, fake, fake, 5, 1, 1024, 128, 16, 8, 6,
+    assert L.mantleHipAttentionInnerQ8CacheF32(fake, fake, fake, fake, fake, fake, fake, 5, 6, 1024, 128, 16, 8, 6,
                                                C.c_float(1), None) == 1
     assert L.mantleHipAttentionInnerQ8CacheF32(fake, fake, fake, fake, fake, fake, fake, 5, 0, 768, 96, 16, 8, 6,
                                                C.c_float(1), None) == 1
+    # the reference signatures (softmax.h:70-104): no scratch argument
+    assert L.mantleHipAttentionInnerF16CacheF32(fake, fake, fake, fake, 5, 6, 1024, 128, 16, 8, 0, C.c_float(1),
+                                                None) == 1
+    assert L.mantleHipAttentionInnerMixedCacheF32(fake, fake, fake, fake, fake, None, fake, fake, 1, 0, 5, 0, 1024, 128,
+                                                  16, 8, 0, C.c_float(1), None) == 1  # q8_0 K without scales
+    assert L.mantleHipApplyRoPEInplaceF32(None, fake, 3, C.c_float(1), 128, 64, 2, None) == 1
+    assert L.mantleHipApplyRoPEInplaceF64FreqF32(fake, fake, 3, C.c_float(1), 128, 65, 2, None) == 1  # 2*half > hd
     assert L.mantleHipSetKVCacheType(3) == 1
     assert L.mantleHipSetKVCacheType(2) == 0 and L.mantleHipGetKVCacheType() == 2
     assert L.mantleHipSetKVCacheType(0) == 0
