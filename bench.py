@@ -29,7 +29,6 @@ if ROOT not in sys.path:
 PEAK_HBM_GBS = 8000.0
 PEAK_MFMA_F16_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 PROMPT_LEN = 31
-CPU_BASELINE_README_TOKS = 3.20  # Qwen3-0.6B k4, Mantle CPU, README.md:43-60
 
 
 def log(*a):
@@ -213,32 +212,61 @@ def traffic_from_profile():
     return None
 
 
-def cpu_baseline(path, cfg, prompt, budget_s=15.0, max_tokens=24):
-    """The oracle (C restatement of Mantle's CPU path) on this host: decode tok/s."""
+def host_cpu():
+    """CPU model, logical CPUs, the CPUs this process may run on, and the ISA
+    Mantle's CPU path would dispatch to (AVX-512 if avx512f, else AVX2,
+    internal/backend/simd/tensor_cpu.go:18-24)."""
+    model, flags = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    isa = "avx512" if "avx512f" in flags else ("avx2" if "avx2" in flags else "scalar")
+    return dict(model=model, nproc=os.cpu_count() or 1, usable=usable, isa=isa)
+
+
+def cpu_baseline(path, cfg, prompt, steps=128, steps_1t=8):
+    """The oracle (C restatement of Mantle's CPU path) on this host: the prompt
+    token by token, then `steps` greedy decode steps on every usable core
+    (rows and heads split over threads as matVecWithQuant splits rows,
+    internal/backend/simd/matvec.go:175-208), then `steps_1t` more on one thread."""
     from oracle import oracle as o
     from tests import models
 
-    threads = min(16, os.cpu_count() or 1)
-    o.set_threads(threads)
-    m = models.oracle_model(path, cfg, PROMPT_LEN + max_tokens + 2)
+    hc = host_cpu()
+    threads = hc["usable"]
+    m = models.oracle_model(path, cfg, PROMPT_LEN + steps + steps_1t + 2)
     try:
+        o.set_threads(threads)
         t0 = time.perf_counter()
         nxt = None
         for t in prompt:
             nxt = m.forward_greedy(t)
         t_prefill = time.perf_counter() - t0
-        n = 0
         t0 = time.perf_counter()
-        while n < max_tokens and time.perf_counter() - t0 < budget_s:
+        for _ in range(steps):
             nxt = m.forward_greedy(nxt)
-            n += 1
         dt = time.perf_counter() - t0
+        o.set_threads(1)
+        t0 = time.perf_counter()
+        for _ in range(steps_1t):
+            nxt = m.forward_greedy(nxt)
+        dt1 = time.perf_counter() - t0
     finally:
         m.close()
-    return dict(value=n / dt, unit="tok/s", cores=threads, kind="port",
-                sample=f"{PROMPT_LEN}-token prompt ({PROMPT_LEN / t_prefill:.2f} tok/s) then {n} greedy decode "
-                       f"steps of the same Qwen3-0.6B k4 model, {threads} threads, oracle/ C restatement "
-                       f"of Mantle's archsimd path (AVX-512 reduction order)")
+    return dict(value=round(steps / dt, 3), unit="tok/s", cores=threads, kind="port",
+                value_1thread=round(steps_1t / dt1, 3),
+                cpu_model=hc["model"], nproc=hc["nproc"], host_isa=hc["isa"], reduction_order="avx512",
+                steps=steps, steps_1thread=steps_1t, prefill_tok_s=round(PROMPT_LEN / t_prefill, 3),
+                sample=f"Qwen3-0.6B k4 (config 1): {PROMPT_LEN}-token prompt, then {steps} greedy decode steps on "
+                       f"{threads} threads (all CPUs this process may use; nproc {hc['nproc']}), then {steps_1t} "
+                       f"more on 1 thread; oracle/ C restatement of Mantle's archsimd path in the AVX-512 "
+                       f"reduction order (host dispatch would pick {hc['isa']}), {hc['model']}")
 
 
 def weight_bytes_per_token(cfg):
@@ -403,7 +431,8 @@ def main():
     if not args.no_cpu:
         try:
             cpu = cpu_baseline(path, QWEN3_0_6B, prompt)
-            log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+            log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads, "
+                f"{cpu['value_1thread']:.3f} tok/s on 1 ({cpu['cpu_model']})")
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline failed: {e!r}")
     bytes_per_token = weight_bytes_per_token(QWEN3_0_6B)
@@ -417,7 +446,8 @@ def main():
         "ms_per_step": round(dt / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(tps / CPU_BASELINE_README_TOKS, 2),
+        # the CPU leg measured on this host (BASELINE.md publishes no number for this metric)
+        "vs_baseline": round(tps / cpu["value"], 2) if cpu else None,
         "dtype": "k4 weights x int8 activations, int32 block dots, fp32 accumulation",
         "data": "synthetic: random-init N(0,0.02) weights seed 0 packed to MCF k4, 31 uniform token ids seed 1",
         "config": {"workload": "Qwen3-0.6B-shape k4 greedy decode, batch 1 (28 blocks, d1024, ffn3072, 16/8 heads, "
