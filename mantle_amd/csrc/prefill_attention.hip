@@ -8,11 +8,21 @@
 // kernel produces the same outputs for every position at once: out[t] =
 // softmax(q_t . K[0..t] * scale) V[0..t] per query head, K/V of its KV group.
 // Inputs are bf16.  The MFMA operands are fp16 (same rate as bf16): q and k
-// after RoPE, V (bf16 values are exact in fp16) and the probabilities.  With
-// bf16 operands the rounding of the RoPE'd q / k alone put 0.2% of outputs
-// past max-abs 1e-3 + rel 1e-2 of the CPU result (5e-3 worst); fp16 keeps them
-// under 6e-4.  Accumulation and the softmax are fp32: the result matches the
-// CPU path within that tolerance, not bit for bit.
+// after RoPE, V and the probabilities.  With bf16 operands the rounding of the
+// RoPE'd q / k alone put 0.2% of outputs past max-abs 1e-3 + rel 1e-2 of the
+// CPU result (5e-3 worst), and bf16 probabilities put the worst output at
+// 1.8x that tolerance (a float64 simulation at S = 512); fp16 keeps them under
+// 6e-4.  fp16's range is narrower than bf16's: every operand is scaled by a
+// power of two into [2^14, 2^15] before the conversion -- q per query (folded
+// into that lane's softmax scale), K and V per 32-key tile of a KV head (K's
+// factor into the tile's softmax scale; V's through the tile's probabilities,
+// relative to the largest V factor the workgroup sees, which multiplies the
+// output).  Power-of-two scaling commutes with rounding, so the scores are the
+// same bits the unscaled fp16 operands give wherever those neither overflow
+// nor underflow; values more than 2^28 below their block's largest one still
+// fall into fp16's subnormals, and a tile's probabilities move down by its V
+// factor (negligible ones first reach the subnormals).  Accumulation and the softmax are fp32: the result matches the CPU
+// path within the tolerance above, not bit for bit.
 //
 // Layout (queries are MFMA columns throughout):
 //  * S^T = K . Q^T per 32-key tile: A = K rows from LDS (RoPE applied while
@@ -83,6 +93,8 @@ struct PrefillArgs {
     float* out;  // fp32 [seq][n_head][128]
     uint16_t* kr;  // workspace: fp16 RoPE'd K [kv_heads][seq_pad][128]
     uint16_t* vtr;  // workspace: fp16 V^T [kv_heads][128][seq_pad]
+    float* kfac;    // workspace: [kv_heads][seq_pad/32] the K tile's power-of-two factor (stored K = K * 2^-e)
+    int* vexp;      // workspace: [kv_heads][seq_pad/32] the V tile's exponent e (stored V = V * 2^-e)
     int seq, seq_pad, n_head, kv_heads;
     int heads_per_wg;  // 2 (GQA groups of an even size) or 1
     int q_block;       // queries per workgroup and head
@@ -96,51 +108,96 @@ struct TileRegs {
     u32x4v v0, v1;  // V^T row tid/2, keys 16*(tid%2) .. +16
 };
 
+// The power of two 2^e that brings a block whose max |x| is m into
+// [2^14, 2^15] (fp16-safe after rounding, clear of fp16's subnormals): e = E -
+// 15 for m = f * 2^E, f in [0.5, 1), clamped to [-100, 113] (bf16's largest
+// values fit); 0 for an all-zero or NaN block (NaN propagates as on the CPU).
+__device__ __forceinline__ int range_exp(float m) {
+    if (!(m > 0.0f)) return 0;
+    if (isinf(m)) return 113;
+    int E;
+    (void)frexpf(m, &E);
+    const int e = E - 15;
+    return e < -100 ? -100 : (e > 113 ? 113 : e);
+}
+
+// Max over the workgroup (256 threads) of a non-negative value; red: 4 floats.
+__device__ __forceinline__ float wg_max256(float v, float* red) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
 // Pre-pass: workgroup (kv head g, keys t0..t0+31) writes K RoPE'd in fp16 and
-// V transposed in fp16 (through LDS), zeros for keys past seq.
+// V transposed in fp16 (through LDS), zeros for keys past seq, each scaled by
+// the tile's power of two into fp16 range (factors in kfac / vexp).
 __global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
     __shared__ __align__(16) uint16_t vs[kPfHd * 40];
+    __shared__ float red[8];
     const int tid = threadIdx.x;
     const int nkb = a.seq_pad / kPfKeys;
-    const int g = (int)blockIdx.x / nkb, t0 = ((int)blockIdx.x % nkb) * kPfKeys;
+    const int g = (int)blockIdx.x / nkb, tile = (int)blockIdx.x % nkb, t0 = tile * kPfKeys;
     const int kv_row = a.kv_heads * kPfHd;
-    {  // K: key tid/8, pairs hd [8c, 8c+8) + 64
-        const int kk = tid >> 3, kc = tid & 7;
-        const int t = t0 + kk;
-        u32x4v w0 = {0, 0, 0, 0}, w1 = {0, 0, 0, 0};
-        if (t < a.seq) {
-            const uint16_t* krow = a.k + (size_t)t * kv_row + g * kPfHd;
-            float x0[8], x1[8];
-            unpack8(*reinterpret_cast<const u32x4v*>(krow + 8 * kc), x0);
-            unpack8(*reinterpret_cast<const u32x4v*>(krow + 64 + 8 * kc), x1);
-            if (a.rope_cos) {
-                float cs[8], sn[8];
+    // K: key tid/8, pairs hd [8c, 8c+8) + 64
+    const int kk = tid >> 3, kc = tid & 7;
+    const int t = t0 + kk;
+    float x0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, x1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (t < a.seq) {
+        const uint16_t* krow = a.k + (size_t)t * kv_row + g * kPfHd;
+        unpack8(*reinterpret_cast<const u32x4v*>(krow + 8 * kc), x0);
+        unpack8(*reinterpret_cast<const u32x4v*>(krow + 64 + 8 * kc), x1);
+        if (a.rope_cos) {
+            float cs[8], sn[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    cs[j] = a.rope_cos[(size_t)t * 64 + 8 * kc + j];
-                    sn[j] = a.rope_sin[(size_t)t * 64 + 8 * kc + j];
-                }
-                rope8(x0, x1, cs, sn);
+            for (int j = 0; j < 8; j++) {
+                cs[j] = a.rope_cos[(size_t)t * 64 + 8 * kc + j];
+                sn[j] = a.rope_sin[(size_t)t * 64 + 8 * kc + j];
             }
-            w0.x = pack_f16(x0[0], x0[1]); w0.y = pack_f16(x0[2], x0[3]);
-            w0.z = pack_f16(x0[4], x0[5]); w0.w = pack_f16(x0[6], x0[7]);
-            w1.x = pack_f16(x1[0], x1[1]); w1.y = pack_f16(x1[2], x1[3]);
-            w1.z = pack_f16(x1[4], x1[5]); w1.w = pack_f16(x1[6], x1[7]);
+            rope8(x0, x1, cs, sn);
         }
+    }
+    // V: keys 2p, 2p+1, hd [8c, 8c+8)
+    const int vp = tid & 15, vc = tid >> 4;
+    float e0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, e1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int ta = t0 + 2 * vp, tb = ta + 1;
+    if (ta < a.seq) unpack8(*reinterpret_cast<const u32x4v*>(a.v + (size_t)ta * kv_row + g * kPfHd + 8 * vc), e0);
+    if (tb < a.seq) unpack8(*reinterpret_cast<const u32x4v*>(a.v + (size_t)tb * kv_row + g * kPfHd + 8 * vc), e1);
+    float km = 0.0f, vm = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        km = fmaxf(km, fmaxf(fabsf(x0[j]), fabsf(x1[j])));
+        vm = fmaxf(vm, fmaxf(fabsf(e0[j]), fabsf(e1[j])));
+    }
+    const int ek = range_exp(wg_max256(km, red));
+    const int ev = range_exp(wg_max256(vm, red + 4));
+    if (tid == 0) {
+        a.kfac[g * nkb + tile] = ldexpf(1.0f, ek);
+        a.vexp[g * nkb + tile] = ev;
+    }
+    {
+        const float f = ldexpf(1.0f, -ek);
+#pragma unroll
+        for (int j = 0; j < 8; j++) { x0[j] *= f; x1[j] *= f; }
+    }
+    {
+        const float f = ldexpf(1.0f, -ev);
+#pragma unroll
+        for (int j = 0; j < 8; j++) { e0[j] *= f; e1[j] *= f; }
+    }
+    {
+        u32x4v w0, w1;
+        w0.x = pack_f16(x0[0], x0[1]); w0.y = pack_f16(x0[2], x0[3]);
+        w0.z = pack_f16(x0[4], x0[5]); w0.w = pack_f16(x0[6], x0[7]);
+        w1.x = pack_f16(x1[0], x1[1]); w1.y = pack_f16(x1[2], x1[3]);
+        w1.z = pack_f16(x1[4], x1[5]); w1.w = pack_f16(x1[6], x1[7]);
         uint16_t* dst = a.kr + ((size_t)g * a.seq_pad + t) * kPfHd;
         *reinterpret_cast<u32x4v*>(dst + 8 * kc) = w0;
         *reinterpret_cast<u32x4v*>(dst + 64 + 8 * kc) = w1;
     }
-    {  // V: keys 2p, 2p+1, hd [8c, 8c+8) -> LDS [hd][key]
-        const int vp = tid & 15, vc = tid >> 4;
-        float e0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, e1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        const int ta = t0 + 2 * vp, tb = ta + 1;
-        if (ta < a.seq) unpack8(*reinterpret_cast<const u32x4v*>(a.v + (size_t)ta * kv_row + g * kPfHd + 8 * vc), e0);
-        if (tb < a.seq) unpack8(*reinterpret_cast<const u32x4v*>(a.v + (size_t)tb * kv_row + g * kPfHd + 8 * vc), e1);
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            *reinterpret_cast<uint32_t*>(&vs[(8 * vc + j) * 40 + 2 * vp]) = pack_f16(e0[j], e1[j]);
-    }
+    for (int j = 0; j < 8; j++)
+        *reinterpret_cast<uint32_t*>(&vs[(8 * vc + j) * 40 + 2 * vp]) = pack_f16(e0[j], e1[j]);
     __syncthreads();
     {  // V^T row hd = tid/2, keys 16*(tid%2) .. +16
         const int hd = tid >> 1, hf = tid & 1;
@@ -176,8 +233,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
     // ---- this wave's queries, RoPE'd, as MFMA B operands: qb_op[s] holds
     // hd 16s + 8*h2 + j (j < 8) of query myq
     f16x8 qop[8];
+    float qfac = 1.0f;  // this query's power-of-two range factor (stored q = q * 2^-e)
     {
         const uint16_t* qrow = a.q + ((size_t)qc * a.n_head + head) * kPfHd;
+        float qx[4][2][8];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const int d = 16 * s + 8 * h2;
@@ -194,10 +253,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             }
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                qop[s][j] = (_Float16)x0[j];
-                qop[s + 4][j] = (_Float16)x1[j];
+                qx[s][0][j] = x0[j];
+                qx[s][1][j] = x1[j];
             }
         }
+        float qm = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) qm = fmaxf(qm, fmaxf(fabsf(qx[s][0][j]), fabsf(qx[s][1][j])));
+        qm = fmaxf(qm, __shfl_xor(qm, 32, 64));  // the other half of the query's 128 values
+        const int eq = range_exp(qm);
+        const float f = ldexpf(1.0f, -eq);
+        qfac = ldexpf(1.0f, eq);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                qop[s][j] = (_Float16)(qx[s][0][j] * f);
+                qop[s + 4][j] = (_Float16)(qx[s][1][j] * f);
+            }
     }
 
     // ---- tile staging (plain copies of the pre-pass output)
@@ -230,10 +305,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
 #pragma unroll
         for (int i = 0; i < 16; i++) o[t][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
-    const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+    const float sl2 = a.scale * 1.4426950408889634f * qfac;  // scale * log2(e), this query's range factor
 
     const int kend = min(q0 + a.q_block, a.seq);  // keys this workgroup needs
     const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
+    // the largest V tile exponent among those tiles: the output's factor 2^vmax;
+    // tile j's probabilities carry 2^(e_j - vmax) <= 1
+    const int nkb = a.seq_pad / kPfKeys;
+    const float* kfac = a.kfac + (size_t)kvh * nkb;
+    const int* vexp = a.vexp + (size_t)kvh * nkb;
+    __shared__ int vred[4];
+    int vmax;
+    {
+        int e = -1000;
+        for (int i = tid; i < ntiles; i += 256) e = max(e, vexp[i]);
+        for (int off = 32; off > 0; off >>= 1) e = max(e, __shfl_xor(e, off, 64));
+        if (lane == 0) vred[wave] = e;
+        __syncthreads();
+        vmax = max(max(vred[0], vred[1]), max(vred[2], vred[3]));
+    }
     TileRegs tr;
     load_tile(tr, 0);
     store_tile(tr, 0);
@@ -243,6 +333,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
         const int t0 = it * kPfKeys;
         if (it + 1 < ntiles) load_tile(tr, t0 + kPfKeys);
         if (t0 <= qw + 31) {  // some key of the tile is visible to some query of this wave
+            const float sl2t = sl2 * kfac[it];  // the tile's K factor
+            const int vd = vexp[it] - vmax;     // its V factor relative to the output's
             // S^T = K . Q^T
             f32x16 sacc;
 #pragma unroll
@@ -269,14 +361,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
                 }
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float m_new = fmaxf(m_run, mt * sl2);
+            const float m_new = fmaxf(m_run, mt * sl2t);
             float ls = 0.0f;
             f16x8 pb[2];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2, -m_new));
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_new));
                 ls += pv;
                 pb[i >> 3][i & 7] = (_Float16)pv;
+            }
+            if (vd != 0) {  // wave-uniform: V stored at a smaller scale than the output's
+                const float vf = ldexpf(1.0f, vd);
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    pb[i >> 3][i & 7] = (_Float16)(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_new)) * vf);
             }
             ls += __shfl_xor(ls, 32, 64);
             // rescale only when some query's running maximum moved (alpha = 1
@@ -313,7 +411,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
 
     // ---- out[myq][head][hd] = O^T[hd][myq] / l
     if (myq < a.seq) {
-        const float inv = 1.0f / l_run;
+        const float inv = ldexpf(1.0f / l_run, vmax);
         float* orow = a.out + ((size_t)myq * a.n_head + head) * kPfHd;
 #pragma unroll
         for (int t = 0; t < 4; t++)
@@ -331,7 +429,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
 
 size_t attention_prefill_workspace(int seq, int kv_heads) {
     const size_t seq_pad = (size_t)(seq + kPfKeys - 1) / kPfKeys * kPfKeys;
-    return (size_t)kv_heads * seq_pad * kPfHd * 2 * sizeof(uint16_t);
+    return (size_t)kv_heads * seq_pad * kPfHd * 2 * sizeof(uint16_t) + (size_t)kv_heads * (seq_pad / kPfKeys) * 8;
 }
 
 hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -356,6 +454,8 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     a.seq_pad = (seq + kPfKeys - 1) / kPfKeys * kPfKeys;
     a.kr = static_cast<uint16_t*>(workspace);
     a.vtr = a.kr + (size_t)kv_heads * a.seq_pad * kPfHd;
+    a.kfac = reinterpret_cast<float*>(a.vtr + (size_t)kv_heads * a.seq_pad * kPfHd);
+    a.vexp = reinterpret_cast<int*>(a.kfac + (size_t)kv_heads * (a.seq_pad / kPfKeys));
     a.n_head = n_head;
     a.kv_heads = kv_heads;
     a.heads_per_wg = (n_head / kv_heads) % 2 == 0 ? 2 : 1;

@@ -135,3 +135,37 @@ def test_prefill_rejects_bad_shapes(hip):
     assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 0, 16, 8, 128, f, p, big, None) != 0  # empty
     assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 8, 128, f, p, 16, None) != 0  # workspace
     assert L.mantleHipAttentionPrefillBF16(p, p, p, None, None, p, 4, 16, 8, 128, f, None, big, None) != 0
+
+
+@pytest.mark.parametrize("case", ["v_1e5", "k_1e5_q_1e-6", "q_1e5_k_1e-6", "all_1e-6", "mixed_tiles"])
+def test_prefill_fp16_range(hip, oracle, case):
+    """bf16 inputs outside fp16's range (|x| > 65504) or in its subnormals
+    (|x| < 6.1e-5): the kernel scales each operand block by a power of two
+    before its fp16 conversion, so it still matches the CPU path (fp32 on the
+    bf16 values) within max-abs 1e-3 (relative to the output's scale) + rel 1e-2."""
+    seq, nh, kvh = 130, 16, 8
+    rng = np.random.default_rng(17)
+    qs, ks, vs = {"v_1e5": (1, 1, 1e5), "k_1e5_q_1e-6": (1e-6, 1e5, 1), "q_1e5_k_1e-6": (1e5, 1e-6, 1),
+                  "all_1e-6": (1e-6, 1e-6, 1e-6), "mixed_tiles": (1, 1, 1)}[case]
+    q = rng.standard_normal(seq * nh * HD).astype(np.float32) * np.float32(qs)
+    k = rng.standard_normal(seq * kvh * HD).astype(np.float32) * np.float32(ks)
+    v = rng.standard_normal(seq * kvh * HD).astype(np.float32) * np.float32(vs)
+    if case == "mixed_tiles":  # V tiles of very different magnitudes, one K tile past fp16's range
+        v.reshape(seq, -1)[32:64] *= np.float32(3e5)
+        v.reshape(seq, -1)[96:] *= np.float32(1e-5)
+        k.reshape(seq, -1)[64:96] *= np.float32(2e5)
+        q *= np.float32(1e-5)
+    qb, qf = bf16(q)
+    kb, kf = bf16(k)
+    vb, vf = bf16(v)
+    qf, kf, vf = qf.reshape(seq, nh * HD), kf.reshape(seq, kvh * HD), vf.reshape(seq, kvh * HD)
+    cos, sin = rope_tables(oracle, seq)
+    scale = float(np.float32(1.0 / np.sqrt(HD)))
+    got = run_gpu((qb, kb, vb), cos, sin, seq, nh, kvh, scale)
+    want = oracle_prefill(oracle, qf, kf, vf, cos, sin, seq, nh, kvh, scale)
+    assert np.isfinite(want).all() and np.isfinite(got).all()
+    # the absolute tolerance scales with the largest |v| a row's keys (0..t) reach
+    vis = np.maximum.accumulate(np.abs(vf).max(axis=1))[:, None]
+    bad = np.abs(got - want) > ATOL * vis + RTOL * np.abs(want)
+    assert not bad.any(), f"{int(bad.sum())} outputs out of tolerance, first at {np.argwhere(bad)[0]}"
+
