@@ -73,6 +73,16 @@ int mantleHipQuantMatVecK4F32(const uint8_t* qData, const uint16_t* superScalesF
 int mantleHipQuantMatVecK4W4A8F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                                   const float* x, float* y, int rows, int blocksPerRow, int cols, int batch,
                                   int8_t* qxScratch, float* xScaleScratch, mantleHipStream_t stream);
+/* mantleHipQuantMatVecK4W4A8F32 without the scratch arguments, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc); no reference counterpart.  The quantised activation lives in a fixed library
+ * array per device (110,592 bytes, held until the process ends): cols <= 12288 and
+ * batch <= 8, larger sizes are rejected (hipErrorInvalidValue, with a message on stderr).
+ * Nothing is allocated or freed.  Calls on one device share that array: calls that overlap
+ * on one GPU (other streams) race. */
+int mantleHipQuantMatVecK4W4A8F32NoAlloc(const uint8_t* qData, const uint16_t* superScalesF16,
+                                         const uint8_t* subScales, const float* x, float* y, int rows,
+                                         int blocksPerRow, int cols, int batch, mantleHipStream_t stream);
 /* Same GEMV on an activation already quantised by mantleHipQuantizeVecBlocksF32
  * (MatVecWithQuant with a PrepareQuantVec result, internal/backend/simd/matvec.go:150-152,
  * internal/backend/simd/quant_vec.go:7-16): qx [batch][blocksPerRow*32] permuted, xScales [batch][blocksPerRow]. */

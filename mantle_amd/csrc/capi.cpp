@@ -84,6 +84,14 @@ int mantleHipQuantMatVecK4W4A8F32(const uint8_t* qData, const uint16_t* superSca
     return launch_k4_gemv_w4a8(&m, outs, 1, cols, qxScratch, xScaleScratch, batch, kEpiStore, nullptr, S(stream));
 }
 
+int mantleHipQuantMatVecK4W4A8F32NoAlloc(const uint8_t* qData, const uint16_t* superScalesF16,
+                                         const uint8_t* subScales, const float* x, float* y, int rows,
+                                         int blocksPerRow, int cols, int batch, mantleHipStream_t stream) {
+    if (!k4_dims_ok(qData, superScalesF16, subScales, rows, blocksPerRow, cols) || !x || !y) return hipErrorInvalidValue;
+    return launch_k4_gemv_w4a8_noalloc(mat(qData, superScalesF16, subScales, rows), cols, x, y, batch, g_isa.load(),
+                                       S(stream));
+}
+
 int mantleHipQuantMatVecK4W4A8QF32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                                    const int8_t* qx, const float* xScales, float* y, int rows, int blocksPerRow,
                                    int cols, int batch, mantleHipStream_t stream) {

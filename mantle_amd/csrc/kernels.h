@@ -64,6 +64,14 @@ hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int 
                                      const float* norm_w, float eps, int isa, int batch, GemvEpi epi,
                                      unsigned long long* argmax_key, hipStream_t stream, int8_t* q_out = nullptr,
                                      float* q_scale = nullptr);
+// launch_k4_gemv_w4a8 on an fp32 x quantised into a fixed per-device library
+// array (no caller scratch, nothing allocated): cols <= kNoAllocMaxBlocks*32,
+// batch <= kNoAllocMaxBatch.  Calls that overlap on one device share the array.
+constexpr int kNoAllocMaxBlocks = 384;  // 12288 columns (the quantiser stages a row in 64 KiB of LDS)
+constexpr int kNoAllocMaxBatch = 8;
+constexpr size_t kNoAllocScratchBytes = (size_t)kNoAllocMaxBatch * kNoAllocMaxBlocks * 36;  // qx + scales
+hipError_t launch_k4_gemv_w4a8_noalloc(const K4Mat& m, int cols, const float* x, float* y, int batch, int isa,
+                                       hipStream_t stream);
 // y = W * x with fp32 x (W4A32; tolerance-checked, not bit-exact).
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch,
                                 hipStream_t stream);

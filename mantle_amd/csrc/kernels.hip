@@ -17,10 +17,12 @@
 //
 // Compiled with -ffp-contract=off: every fused multiply-add is explicit.
 #include <hip/hip_fp16.h>
+#include <stdio.h>
 #include <stdlib.h>
 
 #include <algorithm>
 #include <array>
+#include <mutex>
 #include <vector>
 
 #include "gemv.h"
@@ -515,6 +517,46 @@ hipError_t launch_k4_gemv_w4a8_fused(const K4Mat* mats, float* const* outs, int 
     if (e != hipSuccess || !q_out) return e;
     // the tile kernel has no quantising epilogue: a separate quantiser launch
     return launch_quantize_vec(outs[0], nullptr, 0.0f, mats[0].rows, 1, isa, q_out, q_scale, nullptr, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The W4A8 GEMV's activation staging (int8 blocks + block scales) for callers
+// that cannot allocate: a fixed library array per device instead of caller
+// scratch.  In host code `scratch` names a host-side stand-in, never its
+// device address: that comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static void* scratch_ptr() {
+    static std::mutex mu;
+    static void* per_dev[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!per_dev[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        per_dev[dev] = p;
+    }
+    return per_dev[dev];
+}
+
+hipError_t launch_k4_gemv_w4a8_noalloc(const K4Mat& m, int cols, const float* x, float* y, int batch, int isa,
+                                       hipStream_t stream) {
+    const int bpr = (cols + 31) / 32;
+    if (cols <= 0 || batch < 1 || batch > kNoAllocMaxBatch || bpr > kNoAllocMaxBlocks) {
+        fprintf(stderr, "mantle_hip: no-alloc W4A8 GEMV takes at most %d columns and batch %d (got %d, %d)\n",
+                kNoAllocMaxBlocks * 32, kNoAllocMaxBatch, cols, batch);
+        return hipErrorInvalidValue;
+    }
+    unsigned char* base = static_cast<unsigned char*>(scratch_ptr());
+    if (!base) return hipErrorInvalidSymbol;
+    int8_t* qx = reinterpret_cast<int8_t*>(base);
+    float* xs = reinterpret_cast<float*>(base + (size_t)kNoAllocMaxBatch * kNoAllocMaxBlocks * 32);
+    // every byte of qx / xs the GEMV reads is written by the quantiser first
+    hipError_t e = launch_quantize_vec(x, nullptr, 0.0f, cols, batch, isa, qx, xs, nullptr, stream);
+    if (e != hipSuccess) return e;
+    float* outs[1] = {y};
+    return launch_k4_gemv_w4a8(&m, outs, 1, cols, qx, xs, batch, kEpiStore, nullptr, stream);
 }
 
 hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float* y, int batch, hipStream_t stream) {
