@@ -9,7 +9,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmantle_hip.so")
+# MANTLE_HIP_LIB selects another build of the same library (the phase-trace one).
+LIB_PATH = os.environ.get("MANTLE_HIP_LIB") or os.path.join(_HERE, "libmantle_hip.so")
 
 P = C.c_void_p
 I = C.c_int

@@ -1,6 +1,8 @@
 """Build libmantle_hip.so for gfx950 in-tree (hipcc, no build system needed).
 
-    python -m mantle_amd.build
+    python -m mantle_amd.build                 # the product library
+    python -m mantle_amd.build --phase-trace   # libmantle_hip_trace.so: the same kernels with
+                                               # workgroup-0 phase timestamps (mantle_amd.phase_trace)
 
 The shared library lands next to this file so that it travels with the
 repository snapshot to the GPU box.
@@ -15,6 +17,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmantle_hip.so")
+TRACE_LIB = os.path.join(HERE, "libmantle_hip_trace.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 SOURCES = ["gemv_lane_store.hip", "gemv_lane_fused.hip", "gemv_lane_b8.hip", "gemv_bf16.hip", "attention.hip", "prefill_attention.hip", "kernels.hip", "runtime.cpp", "capi.cpp",
            "mcf.cpp"]
@@ -46,9 +49,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(OBJ_DIR, src + ".o")
-    cmd = [hipcc(), *COMMON, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(src: str, obj_dir: str = OBJ_DIR, defines: tuple = ()) -> str:
+    obj = os.path.join(obj_dir, src + ".o")
+    cmd = [hipcc(), *COMMON, *defines, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".hip"):
         cmd.insert(1, "-xhip")
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -60,20 +63,23 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = True) -> str:
-    os.makedirs(OBJ_DIR, exist_ok=True)
+def build(verbose: bool = True, phase_trace: bool = False) -> str:
+    obj_dir = OBJ_DIR + ("_trace" if phase_trace else "")
+    lib = TRACE_LIB if phase_trace else LIB
+    defines = ("-DMANTLE_PHASE_TRACE",) if phase_trace else ()
+    os.makedirs(obj_dir, exist_ok=True)
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda src: _compile(src, obj_dir, defines), SOURCES))
+    tmp = lib + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stdout + res.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
-    build()
+    build(phase_trace="--phase-trace" in sys.argv[1:])

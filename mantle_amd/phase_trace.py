@@ -1,0 +1,85 @@
+"""Per-kernel phase breakdown of one decode step (latency study).
+
+    python -m mantle_amd.build --phase-trace     # once: libmantle_hip_trace.so
+    python -m mantle_amd.phase_trace [--steps N]
+
+Runs the Qwen3-0.6B-shape k4 decode on the phase-trace
+build of the library, whose kernels stamp workgroup 0's wall clock (100 MHz)
+at fixed points, and prints, per kernel of the decoder layer, the mean offset
+of each stamp from that workgroup's start and the start-to-start time to the
+next kernel.  Stamps: lane GEMVs 1 loads issued, 2 activation arrived,
+6 RMSNorm scale known, 3 int8 activation staged (prologue done), 4 first unit
+summed, 5 workgroup 0 done; V-sum launch 1 softmax done, 2 V sum and store
+done; the score launch only its start.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KINDS = ["QKV GEMV (RMSNorm prologue)", "attention scores", "softmax + V sum", "Wo GEMV + residual",
+         "gate/up GEMV (RMSNorm, SiLU*up)", "down GEMV + residual"]
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
+    args = ap.parse_args()
+    trace = os.path.join(HERE, "libmantle_hip_trace.so")
+    if not os.path.exists(trace):
+        sys.exit("build the trace library first: python -m mantle_amd.build --phase-trace")
+    os.environ["MANTLE_HIP_LIB"] = trace
+    from . import _lib
+    _lib.LIB_PATH = trace
+    from . import mcf
+    from .backend import new_backend
+    os.makedirs(args.model_dir, exist_ok=True)
+    path = mcf.pack_cached(os.path.join(args.model_dir, "qwen3_0_6b_k4_seed0.mcf"), 0, mcf.QWEN3_0_6B)
+    rt = new_backend().load_model(path, max_context=512)
+    fn = _lib.lib().mantleHipDebugPhaseTrace
+    fn.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_uint)]
+    buf = np.zeros(8192 * 8, dtype=np.uint64)
+    n = C.c_uint()
+    try:
+        rt.prefill_tokens(mcf.uniform_tokens(31, mcf.QWEN3_0_6B["vocab"], 1))
+        rt.synchronize()
+        fn(buf.ctypes.data, 8192, C.byref(n))
+        n0 = n.value
+        rt.decode_steps(args.steps)
+        rt.synchronize()
+        fn(buf.ctypes.data, 8192, C.byref(n))
+        n1 = n.value
+    finally:
+        rt.close()
+    per = (n1 - n0) // args.steps
+    t = buf[:n1 * 8].reshape(n1, 8).astype(np.int64)
+    steps = min(5, args.steps)
+    rows = t[n1 - steps * per:].reshape(steps, per, 8)
+    L = mcf.QWEN3_0_6B["n_layers"]
+    head = per - 6 * L - 1  # stamped launches before the first layer (embed)
+    start = rows[:, :, 0]
+    s2s = np.diff(start, axis=1) * 0.01  # us
+    print(f"stamped launches per step: {per}; step start-to-start "
+          f"{(start[:, -1] - start[:, 0]).mean() * 0.01:.1f} us over the last {steps} steps")
+    print("| kernel | start-to-start us | " + " | ".join(f"stamp {k}" for k in (1, 2, 6, 3, 4, 5)) + " |")
+    print("|---|---:|" + "---:|" * 6)
+    for kind in range(6):
+        idx = [head + 6 * l + kind for l in range(L)]
+        sel = rows[:, idx, :]
+        off = lambda c: ((sel[:, :, c] - sel[:, :, 0]) * 0.01).mean()  # noqa: E731
+        cells = []
+        for c in (1, 2, 6, 3, 4, 5):
+            v = off(c)
+            cells.append(f"{v:.2f}" if (sel[:, :, c] > 0).all() and v >= 0 else "-")
+        ss = s2s[:, [i for i in idx if i < per - 1]].mean()
+        print(f"| {KINDS[kind]} | {ss:.2f} | " + " | ".join(cells) + " |")
+
+
+if __name__ == "__main__":
+    main()
