@@ -35,8 +35,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30):
-    """k4 W4A8 GEMV on pre-quantised activations (the decode GEMV), per-launch HIP events."""
+def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30, modes=("w4a8",)):
+    """k4 GEMV per-launch HIP events: "w4a8" on pre-quantised activations (the decode
+    GEMV, MatVecWithQuant on a PrepareQuantVec result), "w4a32" on the fp32 activations
+    themselves (config 2's N(0,1) x, tolerance-checked arithmetic)."""
     import numpy as np
     import torch
 
@@ -56,7 +58,7 @@ def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30):
         spr = (bpr + 7) // 8
         sub_off = (rows * spr * 2 + 63) & ~63
         data_off = (sub_off + rows * bpr + 63) & ~63
-        for batch in batches:
+        for batch, mode in [(b, m) for m in modes for b in batches]:
             x = torch.randn(batch, cols, device="cuda:0", generator=torch.Generator("cuda:0").manual_seed(2))
             qx = torch.empty(batch * bpr * 32, dtype=torch.int8, device="cuda:0")
             xs = torch.empty(batch * bpr, dtype=torch.float32, device="cuda:0")
@@ -67,8 +69,12 @@ def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30):
 
             def launch(i):
                 p = bufs[i % copies].data_ptr()
-                _lib.call("mantleHipQuantMatVecK4W4A8QF32", p + data_off, p, p + sub_off, qx.data_ptr(),
-                          xs.data_ptr(), y.data_ptr(), rows, bpr, cols, batch, stream.cuda_stream)
+                if mode == "w4a8":
+                    _lib.call("mantleHipQuantMatVecK4W4A8QF32", p + data_off, p, p + sub_off, qx.data_ptr(),
+                              xs.data_ptr(), y.data_ptr(), rows, bpr, cols, batch, stream.cuda_stream)
+                else:
+                    _lib.call("mantleHipQuantMatVecK4F32Batched", p + data_off, p, p + sub_off, x.data_ptr(),
+                              y.data_ptr(), rows, bpr, cols, batch, stream.cuda_stream)
 
             for i in range(copies + 5):
                 launch(i)
@@ -91,11 +97,11 @@ def gemv_microbench(shapes, batches, iters=200, rotate_bytes=1 << 30):
             torch.cuda.synchronize()
             single = np.array([a.elapsed_time(b) for a, b in evs]) * 1e-3
             algo_bytes = psize + 4 * cols * batch + 4 * rows * batch
-            out.append(dict(rows=rows, cols=cols, batch=batch, payload_bytes=psize, algo_bytes=algo_bytes,
+            out.append(dict(rows=rows, cols=cols, batch=batch, mode=mode, payload_bytes=psize, algo_bytes=algo_bytes,
                             avg_us=avg_s * 1e6, single_launch_median_us=float(np.median(single)) * 1e6,
                             gbs=algo_bytes / avg_s / 1e9, frac=algo_bytes / avg_s / 1e9 / PEAK_HBM_GBS,
                             rotation_copies=copies, launches=iters))
-            log(f"gemv {rows}x{cols} B={batch}: {avg_s*1e6:.2f} us avg, {algo_bytes/avg_s/1e9:.0f} GB/s")
+            log(f"gemv {mode} {rows}x{cols} B={batch}: {avg_s*1e6:.2f} us avg, {algo_bytes/avg_s/1e9:.0f} GB/s")
         del bufs, base
         torch.cuda.empty_cache()
     return out
@@ -415,9 +421,10 @@ def main():
 
     gemv = []
     if not args.no_gemv:
-        gemv = gemv_microbench([(151936, 1024), (3072, 1024), (1024, 3072), (2048, 1024)], [1, 8])
+        gemv = gemv_microbench([(151936, 1024), (3072, 1024), (1024, 3072), (2048, 1024)], [1, 8],
+                               modes=("w4a8", "w4a32"))
     prefill = [] if args.no_prefill else prefill_microbench()
-    head = next((g for g in gemv if g["rows"] == 151936 and g["batch"] == 1), None)
+    head = next((g for g in gemv if g["rows"] == 151936 and g["batch"] == 1 and g["mode"] == "w4a8"), None)
     roofline = None
     if head:
         roofline = dict(bound="hbm", achieved=round(head["gbs"], 1), peak=PEAK_HBM_GBS, unit="GB/s",

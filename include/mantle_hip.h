@@ -67,6 +67,12 @@ int mantleHipMatVecBF16F32(const uint16_t* w, const float* x, float* y, int rows
 int mantleHipQuantMatVecK4F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                               const float* x, float* y, int rows, int blocksPerRow, int cols,
                               mantleHipStream_t stream);
+/* mantleHipQuantMatVecK4F32 over `batch` (1..8) fp32 vectors x[batch][cols] -> y[batch][rows],
+ * the weights read once for all of them (config 2's batch-8 rows; Mantle's CPU path runs B
+ * independent GEMVs).  Tolerance-checked like the single-vector form. */
+int mantleHipQuantMatVecK4F32Batched(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                                     const float* x, float* y, int rows, int blocksPerRow, int cols, int batch,
+                                     mantleHipStream_t stream);
 /* W4A8 CPU-parity k4 GEMV: the arithmetic of Mantle's AVX2+ CPU path
  * (internal/backend/simd/matvec.go:154-209, matvec_quant.go:256-296); batch
  * vectors x[batch][cols] -> y[batch][rows].  Bit-exact to the CPU path. */

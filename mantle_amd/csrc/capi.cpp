@@ -70,6 +70,14 @@ int mantleHipQuantMatVecK4F32(const uint8_t* qData, const uint16_t* superScalesF
     return launch_k4_gemv_w4a32(mat(qData, superScalesF16, subScales, rows), cols, x, y, 1, S(stream));
 }
 
+int mantleHipQuantMatVecK4F32Batched(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                                     const float* x, float* y, int rows, int blocksPerRow, int cols, int batch,
+                                     mantleHipStream_t stream) {
+    if (!k4_dims_ok(qData, superScalesF16, subScales, rows, blocksPerRow, cols) || !x || !y || batch < 1 || batch > 8)
+        return hipErrorInvalidValue;
+    return launch_k4_gemv_w4a32(mat(qData, superScalesF16, subScales, rows), cols, x, y, batch, S(stream));
+}
+
 int mantleHipQuantMatVecK4W4A8F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                                   const float* x, float* y, int rows, int blocksPerRow, int cols, int batch,
                                   int8_t* qxScratch, float* xScaleScratch, mantleHipStream_t stream) {

@@ -571,6 +571,11 @@ hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float*
     p.spr = (p.bpr + 7) / 8;
     p.batch = batch;
     p.x = x;
+    if (!lane_gemv_disabled()) {
+        bool used = false;
+        hipError_t e = k4_gemv_w4a32_lane(m, cols, x, y, batch, stream, &used);
+        if (used) return e;
+    }
     return launch_gemv<kModeW4A32>(p, kEpiStore, stream);
 }
 

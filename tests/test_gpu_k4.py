@@ -169,3 +169,28 @@ def test_w4a32_gemv_tolerance(hip, oracle, rows, cols):
     got = g.host(y)
     err = np.abs(got - want)
     assert np.all((err <= 1e-3) | (err <= 1e-2 * np.abs(want))), float(err.max())
+
+
+@pytest.mark.parametrize("rows,cols", [(3072, 1024), (1024, 3072), (2048, 1024), (151936, 1024)])
+def test_w4a32_gemv_batch8(hip, oracle, rows, cols):
+    """Batched W4A32 (config 2 at B = 8, fp32 activations): each column within
+    max-abs 1e-3 / rel 1e-2 of the oracle and equal to its own batch-1 launch."""
+    from mantle_amd import mcf
+    payload = mcf.quantize_k4(_weights(rows, cols, 2))
+    B, bpr = 8, (cols + 31) // 32
+    x = mcf.fill_normal(B * cols, 78, 1.0)
+    keep, qn, qs, qsub = g.k4_dev(payload, rows, cols)
+    dx = g.keep(x)
+    y = g.empty(B * rows)
+    g.call("mantleHipQuantMatVecK4F32Batched", qn, qs, qsub, g.ptr(dx), g.ptr(y), rows, bpr, cols, B, g.stream())
+    got = g.host(y).reshape(B, rows)
+    oracle.set_threads(8)
+    for b in range(B):
+        want = oracle.matvec_w4a32(payload, rows, cols, x[b * cols:(b + 1) * cols])
+        err = np.abs(got[b] - want)
+        assert np.all((err <= 1e-3) | (err <= 1e-2 * np.abs(want))), (b, float(err.max()))
+    for b in (0, 7):
+        y1 = g.empty(rows)
+        g.call("mantleHipQuantMatVecK4F32Batched", qn, qs, qsub, g.ptr(dx) + 4 * b * cols, g.ptr(y1), rows, bpr, cols,
+               1, g.stream())
+        np.testing.assert_array_equal(g.host(y1), got[b])
