@@ -79,6 +79,14 @@ int mantleHipQuantMatVecK4F32Batched(const uint8_t* qData, const uint16_t* super
 int mantleHipQuantMatVecK4W4A8F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
                                   const float* x, float* y, int rows, int blocksPerRow, int cols, int batch,
                                   int8_t* qxScratch, float* xScaleScratch, mantleHipStream_t stream);
+/* mantleHipQuantMatVecK4W4A8F32 over n activation rows at once (any n >= 1, blocksPerRow a
+ * multiple of 8), on int8 matrix cores: y[v][r] bit-identical to the batch-1 call on row v.
+ * No single counterpart in the reference: it replaces the per-token loop of
+ * mantleCudaQuantMatVecK4F32 calls a prompt's projections make (internal/backend/cuda/native/
+ * softmax.h:32-40) with one call.  Scratch: qx n*cols bytes, scales n*blocksPerRow floats. */
+int mantleHipQuantMatMulK4W4A8F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                                  const float* x, float* y, int rows, int blocksPerRow, int cols, int n,
+                                  int8_t* qxScratch, float* xScaleScratch, mantleHipStream_t stream);
 /* mantleHipQuantMatVecK4W4A8F32 without the scratch arguments, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc); no reference counterpart.  The quantised activation lives in a fixed library

@@ -59,6 +59,7 @@ _SIGS = {
     "mantleHipQuantMatVecK4F32": (I, [P, P, P, P, P, I, I, I, P]),
     "mantleHipQuantMatVecK4F32Batched": (I, [P, P, P, P, P, I, I, I, I, P]),
     "mantleHipQuantMatVecK4W4A8F32": (I, [P, P, P, P, P, I, I, I, I, P, P, P]),
+    "mantleHipQuantMatMulK4W4A8F32": (I, [P, P, P, P, P, I, I, I, I, P, P, P]),
     "mantleHipQuantMatVecK4W4A8QF32": (I, [P, P, P, P, P, P, I, I, I, I, P]),
     "mantleHipQuantMatVecK4W4A8F32NoAlloc": (I, [P, P, P, P, P, I, I, I, I, P]),
     "mantleHipDequantizeK4ToF16": (I, [P, P, P, P, I, I, I, P]),

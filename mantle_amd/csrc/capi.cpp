@@ -92,6 +92,19 @@ int mantleHipQuantMatVecK4W4A8F32(const uint8_t* qData, const uint16_t* superSca
     return launch_k4_gemv_w4a8(&m, outs, 1, cols, qxScratch, xScaleScratch, batch, kEpiStore, nullptr, S(stream));
 }
 
+int mantleHipQuantMatMulK4W4A8F32(const uint8_t* qData, const uint16_t* superScalesF16, const uint8_t* subScales,
+                                  const float* x, float* y, int rows, int blocksPerRow, int cols, int n,
+                                  int8_t* qxScratch, float* xScaleScratch, mantleHipStream_t stream) {
+    if (!k4_dims_ok(qData, superScalesF16, subScales, rows, blocksPerRow, cols) || !x || !y || !qxScratch ||
+        !xScaleScratch || n < 1 || blocksPerRow % 8)
+        return hipErrorInvalidValue;
+    hipError_t e = launch_quantize_vec(x, nullptr, 0.0f, cols, n, g_isa.load(), qxScratch, xScaleScratch, nullptr,
+                                       S(stream));
+    if (e != hipSuccess) return e;
+    return launch_k4_gemm_w4a8(mat(qData, superScalesF16, subScales, rows), cols, qxScratch, xScaleScratch, n, y,
+                               rows, kEpiStore, S(stream));
+}
+
 int mantleHipQuantMatVecK4W4A8F32NoAlloc(const uint8_t* qData, const uint16_t* superScalesF16,
                                          const uint8_t* subScales, const float* x, float* y, int rows,
                                          int blocksPerRow, int cols, int batch, mantleHipStream_t stream) {

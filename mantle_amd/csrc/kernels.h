@@ -55,6 +55,11 @@ struct DecodeState {
 hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, int cols,
                                const int8_t* qx, const float* xs, int batch, GemvEpi epi,
                                unsigned long long* argmax_key, hipStream_t stream);
+// The same product for n activation vectors at once on int8 MFMA (any n >= 1;
+// blocks per row a multiple of 8): y[v * ldy + row] = (W x_v)[row] (kEpiStore)
+// or += it (kEpiResAdd).  Bit-identical to launch_k4_gemv_w4a8 per vector.
+hipError_t launch_k4_gemm_w4a8(const K4Mat& w, int cols, const int8_t* qx, const float* xs, int n, float* y, int ldy,
+                               GemvEpi epi, hipStream_t stream);
 // Same arithmetic, but each workgroup quantises the fp32 activation x itself
 // (after Mantle's RMSNorm with norm_w when non-null): no separate quantiser
 // launch, and the weight loads are issued before the prologue runs.  With
