@@ -858,6 +858,22 @@ static hipError_t allow_lds(void (*kern)(AttnArgs), size_t bytes) {
                                (int)bytes);
 }
 
+// Query row blockIdx.y of a launch_attention_rows launch: moves a's per-row
+// pointers to that row and returns its offset from the first row's position
+// (0 and nothing moved for the single-row launches, whose grid has one row).
+__device__ __forceinline__ int token_row(AttnArgs& a) {
+    const int r = (int)blockIdx.y;
+    if (r == 0) return 0;
+    a.q += (size_t)r * a.q_row;
+    a.out += (size_t)r * a.out_row;
+    a.scores += (size_t)r * a.scores_row;
+    if (a.q_out) {
+        a.q_out += (size_t)r * a.out_row;
+        a.q_scale += (size_t)r * (a.out_row / 32);
+    }
+    return r;
+}
+
 // Scores of head h, chunks sidx, sidx + S, ... into the scores buffer (the
 // body of attention_scores_split; attention_split_fused runs it first).  KV:
 // the cache element type.  kKvF16: DotF16, the scalar order in every ISA
@@ -923,7 +939,7 @@ __global__ __launch_bounds__(kThreads) void attention_scores_split(AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x % a.n_head, sidx = blockIdx.x / a.n_head;
     const int S = gridDim.x / a.n_head;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos_host) + token_row(a);
     if (sidx >= pos / kAttnKeys + 1) return;  // whole workgroup: no chunk of this context for it
     PHASE_SLOT();
     PHASE(0);
@@ -1243,7 +1259,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_split(AttnArgs a) {
     const int h = blockIdx.x / nd, db = blockIdx.x % nd;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvh = h * a.kv_heads / a.n_head;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos_host) + token_row(a);
     const int pcap = (a.max_ctx + 31) / 32 * 32;
     const float* sg = a.scores + (size_t)h * a.max_ctx;
     PHASE_SLOT();
@@ -1291,7 +1307,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     const int h = blockIdx.x / nd, db = blockIdx.x % nd;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int kvh = h * a.kv_heads / a.n_head;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos_host) + token_row(a);
     const int pcap = (a.max_ctx + 31) / 32 * 32;
     const float* sg = a.scores + (size_t)h * a.max_ctx;
     float* p = lds;
@@ -1464,6 +1480,58 @@ static unsigned* library_counters(int n_head) {
     return per_dev[dev];
 }
 
+// The two-launch split form (scores, then softmax and V sum) for `rows`
+// query rows (grid rows; 1 for a decode step).
+static hipError_t launch_split_two(const AttnArgs& a, int rows, hipStream_t stream) {
+    const bool vt = a.vt_stride > 0;
+    const int kvt = a.k_type, vtt = a.v_type;
+    const int S = min(kSplitWgs, (a.max_ctx + kAttnKeys - 1) / kAttnKeys);
+    const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
+    const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
+    const int nd = a.head_dim / 32;
+    // kernel[hd 128][vt][cache type]
+    void (*const pv[2][2][3])(AttnArgs) = {
+        {{attention_pv_split<64, false, kKvF32>, attention_pv_split<64, false, kKvF16>,
+          attention_pv_split<64, false, kKvQ8>},
+         {attention_pv_split<64, true, kKvF32>, attention_pv_split<64, true, kKvF16>,
+          attention_pv_split<64, true, kKvQ8>}},
+        {{attention_pv_split<128, false, kKvF32>, attention_pv_split<128, false, kKvF16>,
+          attention_pv_split<128, false, kKvQ8>},
+         {attention_pv_split<128, true, kKvF32>, attention_pv_split<128, true, kKvF16>,
+          attention_pv_split<128, true, kKvQ8>}}};
+    void (*const sc[2][3])(AttnArgs) = {
+        {attention_scores_split<64, kKvF32>, attention_scores_split<64, kKvF16>, attention_scores_split<64, kKvQ8>},
+        {attention_scores_split<128, kKvF32>, attention_scores_split<128, kKvF16>,
+         attention_scores_split<128, kKvQ8>}};
+    auto pvk = pv[a.head_dim == 128][vt][vtt];
+    size_t smem_pv = smem_b;
+    const size_t pcap = (size_t)(a.max_ctx + 31) / 32 * 32;
+    const size_t smem_lv = sizeof(float) * (pcap + 32 + 2 * 32 * kPvPitch + (vtt == kKvQ8 ? 2 * kPvChunk : 0));
+    // (short caches keep the register ring: at a few hundred keys the
+    // loader waves' barriers cost more than they save, 6.30 -> 6.55 us)
+    const bool lv_used = vt && a.max_ctx > kPvLdsMinCtx && smem_lv <= kMaxLds && pv_lds_enabled();
+    if (lv_used) {  // V staged in LDS
+        void (*const lv[2][3])(AttnArgs) = {
+            {attention_pv_lds<64, kKvF32>, attention_pv_lds<64, kKvF16>, attention_pv_lds<64, kKvQ8>},
+            {attention_pv_lds<128, kKvF32>, attention_pv_lds<128, kKvF16>, attention_pv_lds<128, kKvQ8>}};
+        pvk = lv[a.head_dim == 128][vtt];
+        smem_pv = smem_lv;
+    }
+    const size_t smem_sl = sizeof(float) * (2 * ((size_t)(a.max_ctx + 31) / 32 * 32) + 32);
+    if (!lv_used && vtt == kKvQ8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
+        void (*const pvs[2][2])(AttnArgs) = {
+            {attention_pv_split<64, false, kKvQ8, true>, attention_pv_split<64, true, kKvQ8, true>},
+            {attention_pv_split<128, false, kKvQ8, true>, attention_pv_split<128, true, kKvQ8, true>}};
+        pvk = pvs[a.head_dim == 128][vt];
+        smem_pv = smem_sl;
+    }
+    const hipError_t e = allow_lds(pvk, smem_pv);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sc[a.head_dim == 128][kvt], dim3(a.n_head * S, rows), dim3(kThreads), smem_a, stream, a);
+    hipLaunchKernelGGL(pvk, dim3(a.n_head * nd, rows), dim3(kThreads), smem_pv, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || a.head_dim <= 0 ||
         a.head_dim > 256 || (a.head_dim & 3) || (a.kv_stride & 3) || (a.head_stride & 3) || a.max_ctx <= 0)
@@ -1500,7 +1568,6 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     // q8_0 and mixed caches: the two-launch split form only
     if ((any_q8 || kt != vtt) && a.max_ctx > kSplitMaxCtx) return hipErrorInvalidValue;
     const bool f16 = kt == kKvF16;
-    const int kvt = kt;
     if (split_ok && !any_q8 && kt == vtt && (mode == kAttnPathFused || a.max_ctx > kSplitMaxCtx)) {
         AttnArgs f = a;
         if (!f.counters) f.counters = library_counters(a.n_head);
@@ -1524,53 +1591,7 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(kerns[a.head_dim == 128][pg][vt][f16], grid, dim3(kThreads), smem, stream, f);
         return hipGetLastError();
     }
-    if (split_ok) {
-        const int S = min(kSplitWgs, (a.max_ctx + kAttnKeys - 1) / kAttnKeys);
-        const size_t smem_a = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4));
-        const size_t smem_b = sizeof(float) * ((size_t)(a.max_ctx + 31) / 32 * 32 + 8);
-        const int nd = a.head_dim / 32;
-        // kernel[hd 128][vt][cache type]
-        void (*const pv[2][2][3])(AttnArgs) = {
-            {{attention_pv_split<64, false, kKvF32>, attention_pv_split<64, false, kKvF16>,
-              attention_pv_split<64, false, kKvQ8>},
-             {attention_pv_split<64, true, kKvF32>, attention_pv_split<64, true, kKvF16>,
-              attention_pv_split<64, true, kKvQ8>}},
-            {{attention_pv_split<128, false, kKvF32>, attention_pv_split<128, false, kKvF16>,
-              attention_pv_split<128, false, kKvQ8>},
-             {attention_pv_split<128, true, kKvF32>, attention_pv_split<128, true, kKvF16>,
-              attention_pv_split<128, true, kKvQ8>}}};
-        void (*const sc[2][3])(AttnArgs) = {
-            {attention_scores_split<64, kKvF32>, attention_scores_split<64, kKvF16>, attention_scores_split<64, kKvQ8>},
-            {attention_scores_split<128, kKvF32>, attention_scores_split<128, kKvF16>,
-             attention_scores_split<128, kKvQ8>}};
-        auto pvk = pv[a.head_dim == 128][vt][vtt];
-        size_t smem_pv = smem_b;
-        const size_t pcap = (size_t)(a.max_ctx + 31) / 32 * 32;
-        const size_t smem_lv = sizeof(float) * (pcap + 32 + 2 * 32 * kPvPitch + (vtt == kKvQ8 ? 2 * kPvChunk : 0));
-        // (short caches keep the register ring: at a few hundred keys the
-        // loader waves' barriers cost more than they save, 6.30 -> 6.55 us)
-        const bool lv_used = vt && a.max_ctx > kPvLdsMinCtx && smem_lv <= kMaxLds && pv_lds_enabled();
-        if (lv_used) {  // V staged in LDS
-            void (*const lv[2][3])(AttnArgs) = {
-                {attention_pv_lds<64, kKvF32>, attention_pv_lds<64, kKvF16>, attention_pv_lds<64, kKvQ8>},
-                {attention_pv_lds<128, kKvF32>, attention_pv_lds<128, kKvF16>, attention_pv_lds<128, kKvQ8>}};
-            pvk = lv[a.head_dim == 128][vtt];
-            smem_pv = smem_lv;
-        }
-        const size_t smem_sl = sizeof(float) * (2 * ((size_t)(a.max_ctx + 31) / 32 * 32) + 32);
-        if (!lv_used && vtt == kKvQ8 && smem_sl <= kMaxLds) {  // q8_0 scales beside the probabilities
-            void (*const pvs[2][2])(AttnArgs) = {
-                {attention_pv_split<64, false, kKvQ8, true>, attention_pv_split<64, true, kKvQ8, true>},
-                {attention_pv_split<128, false, kKvQ8, true>, attention_pv_split<128, true, kKvQ8, true>}};
-            pvk = pvs[a.head_dim == 128][vt];
-            smem_pv = smem_sl;
-        }
-        const hipError_t e = allow_lds(pvk, smem_pv);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(sc[a.head_dim == 128][kvt], dim3(a.n_head * S), dim3(kThreads), smem_a, stream, a);
-        hipLaunchKernelGGL(pvk, dim3(a.n_head * nd), dim3(kThreads), smem_pv, stream, a);
-        return hipGetLastError();
-    }
+    if (split_ok) return launch_split_two(a, 1, stream);
     if (fast_hd && mode != kAttnPathGeneral) {
         const size_t smem = sizeof(float) * (kAttnV4Hdr + (size_t)kAttnKeys * (a.head_dim + 4) +
                                              (lds_scores ? (a.max_ctx + 31) / 32 * 32 : 0));
@@ -1584,6 +1605,28 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     const size_t smem = sizeof(float) * (kAttnHdr + (size_t)kc * (a.head_dim + 1) + (lds_scores ? a.max_ctx : 0));
     hipLaunchKernelGGL(attention_decode_kernel, dim3(a.n_head), dim3(kThreads), smem, stream, a);
     return hipGetLastError();
+}
+
+hipError_t launch_attention_rows(const AttnArgs& a, int rows, hipStream_t stream) {
+    if (rows < 1 || a.fused || a.pos_dev || a.pos_host < 0 || a.pos_host + rows > a.max_ctx ||
+        (a.head_dim != 64 && a.head_dim != 128) || !a.scores || a.max_ctx > kSplitMaxCtx ||
+        (rows > 1 && (a.q_row < a.n_head * a.head_dim || a.out_row < a.n_head * a.head_dim ||
+                      a.scores_row < (size_t)a.n_head * a.max_ctx || (a.q_out && (a.out_row & 31)))))
+        return hipErrorInvalidValue;
+    const int mode = attention_path();
+    if (mode != kAttnPathSplit && mode != kAttnPathFused) return hipErrorInvalidValue;
+    if (!a.q || !a.cache_k || !a.cache_v || !a.out || a.n_head <= 0 || a.kv_heads <= 0 || (a.kv_stride & 3) ||
+        (a.head_stride & 3) || (((uintptr_t)a.cache_k | (uintptr_t)a.cache_v) & 15) ||
+        (a.q_out && !a.q_scale) || (a.rope_cos && !a.rope_sin))
+        return hipErrorInvalidValue;
+    if (a.k_type < kKvF32 || a.k_type > kKvQ8 || a.v_type < kKvF32 || a.v_type > kKvQ8) return hipErrorInvalidValue;
+    if ((a.k_type == kKvQ8 && !a.k_scale) || (a.v_type == kKvQ8 && !a.v_scale)) return hipErrorInvalidValue;
+    if (a.vt_stride > 0 && ((a.vt_stride & 3) || a.vt_stride < (a.max_ctx + 3) / 4 * 4)) return hipErrorInvalidValue;
+    if (a.vt_stride > 0 && a.v_type == kKvQ8 && ((a.vt_stride & 15) || a.vt_stride < (a.max_ctx + 15) / 16 * 16))
+        return hipErrorInvalidValue;
+    if ((a.k_type == kKvQ8 || (a.v_type == kKvQ8 && a.vt_stride == 0)) && ((a.kv_stride & 15) || (a.head_stride & 15)))
+        return hipErrorInvalidValue;
+    return launch_split_two(a, rows, stream);
 }
 
 // storeQ8's element (ops_runtime.go:158-168): q = int32(v*inv + 0.5), or
@@ -1613,7 +1656,11 @@ __global__ __launch_bounds__(kThreads) void kv_append_q8_kernel(KvQ8Args a) {
     float* wbuf = sv + n;
     float* red = wbuf + 4 * 128;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos_host;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos_host) + (int)blockIdx.x;  // row blockIdx.x of `tokens`
+    if (blockIdx.x > 0) {
+        a.k += (size_t)blockIdx.x * a.tok_stride;
+        a.v += (size_t)blockIdx.x * a.tok_stride;
+    }
     if constexpr (PREP_HD > 0) {
         constexpr int HD = PREP_HD, half = HD / 2;
         const int li = lane < half ? lane : 0;
@@ -1677,9 +1724,84 @@ hipError_t launch_kv_append_q8(const KvQ8Args& a, hipStream_t stream) {
     if (!a.pos_dev && a.pos_host < 0) return hipErrorInvalidValue;
     if (a.prep && a.head_dim != 64 && a.head_dim != 128) return hipErrorInvalidValue;
     if (a.rope_cos && !a.rope_sin) return hipErrorInvalidValue;
+    const int rows = a.tokens > 1 ? a.tokens : 1;
+    if (rows > 1 && (a.pos_dev || a.tok_stride < a.kv_heads * a.head_dim)) return hipErrorInvalidValue;
     const size_t smem = sizeof(float) * (2 * (size_t)a.kv_heads * a.head_dim + 4 * 128 + 8);
     auto k = !a.prep ? kv_append_q8_kernel<0> : (a.head_dim == 128 ? kv_append_q8_kernel<128> : kv_append_q8_kernel<64>);
-    hipLaunchKernelGGL(k, dim3(1), dim3(kThreads), smem, stream, a);
+    hipLaunchKernelGGL(k, dim3(rows), dim3(kThreads), smem, stream, a);
+    return hipGetLastError();
+}
+
+// Rows pos .. pos+rows-1 of a prompt: wave w of workgroup (b, r) prepares
+// vector 4b+w of row r -- query heads first, then the kv heads' K, then their
+// V -- with the decode prologue's arithmetic (prep_pair; the f16 cache's
+// rounding), writing q to qo and the K / V rows to the f32 / f16 caches.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_prep_rows_kernel(AttnArgs a, int qkv_row, float* qo) {
+    __shared__ __align__(16) float wbuf[4 * 128];
+    constexpr int half = HD / 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = (int)blockIdx.y;
+    const int pos = a.pos_host + r;
+    const int vi = (int)blockIdx.x * 4 + wave;
+    const int nq = a.n_head, nkv = a.kv_heads;
+    if (vi >= nq + 2 * nkv) return;
+    const int li = lane < half ? lane : 0;
+    const int kind = vi < nq ? 0 : (vi < nq + nkv ? 1 : 2);  // q, k, v
+    const int hh = kind == 0 ? vi : (kind == 1 ? vi - nq : vi - nq - nkv);
+    const int ctype = kind == 1 ? a.k_type : a.v_type;
+    if (kind > 0 && ctype == kKvQ8) return;  // launch_kv_append_q8 writes the q8_0 rows
+    const float* src = (kind == 0 ? a.q : (kind == 1 ? a.k : a.v)) + (size_t)r * qkv_row + hh * HD;
+    const float* nw = kind == 0 ? a.q_norm : (kind == 1 ? a.k_norm : nullptr);
+    const bool norm = nw != nullptr, rope = kind < 2 && a.rope_cos != nullptr;
+    float x0 = src[li], x1 = src[li + half];
+    const float g0 = norm ? nw[li] : 0.0f, g1 = norm ? nw[li + half] : 0.0f;
+    const float cs = rope ? a.rope_cos[(size_t)pos * half + li] : 0.0f;
+    const float sn = rope ? a.rope_sin[(size_t)pos * half + li] : 0.0f;
+    prep_pair<HD>(x0, x1, g0, g1, cs, sn, norm, rope, a.eps, a.isa, wbuf + wave * 128);
+    if (lane >= half) return;
+    if (kind == 0) {
+        float* dst = qo + (size_t)r * a.out_row + hh * HD;
+        dst[lane] = x0;
+        dst[lane + half] = x1;
+        return;
+    }
+    if (ctype == kKvF16) {
+        uint16_t* c16 = reinterpret_cast<uint16_t*>(kind == 1 ? a.cache_k : a.cache_v);
+        const uint16_t h0 = mantle_f32_to_f16_trunc(f16_cache_round(x0));
+        const uint16_t h1 = mantle_f32_to_f16_trunc(f16_cache_round(x1));
+        if (kind == 2 && a.vt_stride > 0) {
+            uint16_t* col = c16 + (size_t)(hh * HD + lane) * a.vt_stride + pos;
+            col[0] = h0;
+            col[(size_t)half * a.vt_stride] = h1;
+        } else {
+            uint16_t* row = c16 + (size_t)hh * a.head_stride + (size_t)pos * a.kv_stride;
+            row[lane] = h0;
+            row[lane + half] = h1;
+        }
+    } else if (kind == 2 && a.vt_stride > 0) {
+        float* col = a.cache_v + (size_t)(hh * HD + lane) * a.vt_stride + pos;
+        col[0] = x0;
+        col[(size_t)half * a.vt_stride] = x1;
+    } else {
+        float* row = (kind == 1 ? a.cache_k : a.cache_v) + (size_t)hh * a.head_stride + (size_t)pos * a.kv_stride;
+        row[lane] = x0;
+        row[lane + half] = x1;
+    }
+}
+
+hipError_t launch_attention_prep_rows(const AttnArgs& a, int rows, int qkv_row, float* qo, hipStream_t stream) {
+    if (rows < 1 || !a.q || !a.k || !a.v || !qo || !a.cache_k || !a.cache_v || a.pos_dev || a.pos_host < 0 ||
+        a.pos_host + rows > a.max_ctx || (a.head_dim != 64 && a.head_dim != 128) || a.n_head <= 0 ||
+        a.kv_heads <= 0 || a.out_row < a.n_head * a.head_dim || qkv_row <= 0 || (a.rope_cos && !a.rope_sin) ||
+        a.key_base || a.key_ring)
+        return hipErrorInvalidValue;
+    const int nv = a.n_head + 2 * a.kv_heads;
+    const dim3 grid((nv + 3) / 4, rows);
+    if (a.head_dim == 128)
+        hipLaunchKernelGGL(attention_prep_rows_kernel<128>, grid, dim3(kThreads), 0, stream, a, qkv_row, qo);
+    else
+        hipLaunchKernelGGL(attention_prep_rows_kernel<64>, grid, dim3(kThreads), 0, stream, a, qkv_row, qo);
     return hipGetLastError();
 }
 

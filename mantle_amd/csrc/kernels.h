@@ -139,8 +139,25 @@ struct AttnArgs {
     const float* v_scale;  // v_scale [max_ctx] (two-launch split path only).  Its step rows must
                            // already be in the cache (fused: launch_kv_append_q8 prepares and
                            // appends the q8_0 rows; this launch prepares q and the other rows)
+    // Token rows (launch_attention_rows only; zero otherwise): query row r of the launch is the
+    // position pos + r; its q, out, scores and q_out / q_scale start q_row, out_row,
+    // scores_row and out_row elements (out_row / 32 scales) further on.
+    int q_row, out_row;
+    size_t scores_row;
 };
 hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream);
+// Attention of `rows` consecutive query positions pos .. pos+rows-1 (causal:
+// row r sees keys 0 .. pos+r) on the two-launch split kernels, each row exactly
+// the decode step's arithmetic at its position.  fused must be 0: q holds the
+// prepared queries and the cache the rows' K / V (launch_attention_prep_rows,
+// launch_kv_append_q8 with tokens).  Requires head_dim 64 / 128 and scores for
+// rows * n_head * max_ctx floats (scores_row >= n_head * max_ctx).
+hipError_t launch_attention_rows(const AttnArgs& a, int rows, hipStream_t stream);
+// The prologue of those rows: per-head RMSNorm and RoPE of q (written to qo,
+// row r at qo + r * a.out_row) and of k, and the K / V rows appended to the
+// f32 / f16 caches (q8_0 sides: launch_kv_append_q8).  a.q / a.k / a.v: the
+// raw projections of row 0, rows qkv_row floats apart.
+hipError_t launch_attention_prep_rows(const AttnArgs& a, int rows, int qkv_row, float* qo, hipStream_t stream);
 // Decode-attention kernel variant for head_dim 64 / 128 (other sizes always
 // take the general kernel).  A model's captured step keeps the variant it was
 // captured with.
@@ -162,6 +179,10 @@ size_t attention_prefill_workspace(int seq, int kv_heads);
 
 hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
                         hipStream_t stream);
+// Embedding rows of tokens[0 .. rows) into x[rows][cols] (a prompt at once).
+hipError_t launch_embed_rows(const K4Mat& emb, int cols, const int* tokens, int rows, float* x, hipStream_t stream);
+// st->pos = pos and cleared argmax slots (a step whose final GEMV runs outside the decode step).
+hipError_t launch_set_step(DecodeState* st, int pos, hipStream_t stream);
 hipError_t launch_embed_bf16(const uint16_t* emb, int vocab, int cols, const int* prompt, DecodeState* st, float* x,
                              hipStream_t stream);
 hipError_t launch_finish_step(DecodeState* st, int* out_tokens, hipStream_t stream);
@@ -202,6 +223,7 @@ struct KvQ8Args {
     float *k_scale, *v_scale;  // [max_ctx]
     int prep;
     int skip_k, skip_v;  // 1: that row is not a q8_0 cache (mixed cache types): left alone
+    int tokens, tok_stride;  // > 1: rows pos .. pos+tokens-1, their k / v tok_stride floats apart
 };
 static constexpr int kKvQ8MaxRow = 4096;  // kv_heads*head_dim: both rows staged in LDS
 hipError_t launch_kv_append_q8(const KvQ8Args& a, hipStream_t stream);

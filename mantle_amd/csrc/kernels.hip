@@ -624,6 +624,43 @@ hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeSta
     return hipGetLastError();
 }
 
+// Embedding rows of `rows` prompt tokens (tokens[r] -> x + r*cols), each as
+// embed_kernel dequantises it.
+__global__ __launch_bounds__(kThreads) void embed_rows_kernel(K4Mat emb, int cols, const int* __restrict__ tokens,
+                                                              float* __restrict__ x) {
+    const int r = blockIdx.x;
+    int tok = tokens[r];
+    if (tok < 0 || tok >= emb.rows) tok = 0;
+    const int bpr = (cols + 31) / 32, spr = (bpr + 7) / 8;
+    float* xr = x + (size_t)r * cols;
+    for (int c = threadIdx.x; c < cols; c += kThreads) {
+        const int b = c >> 5, e = c & 31;
+        const size_t blk = (size_t)tok * bpr + b;
+        const float sc = k4_scale(emb.sup[(size_t)tok * spr + (b >> 3)], emb.sub[blk]);
+        const uint32_t word = reinterpret_cast<const uint32_t*>(emb.nib + blk * 16)[e >> 3];
+        xr[c] = sc == 0.0f ? 0.0f : (float)k4_nib(word, e & 7) * sc;
+    }
+}
+
+hipError_t launch_embed_rows(const K4Mat& emb, int cols, const int* tokens, int rows, float* x, hipStream_t stream) {
+    if (!emb.nib || !tokens || !x || cols <= 0 || rows <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(rows), dim3(kThreads), 0, stream, emb, cols, tokens, x);
+    return hipGetLastError();
+}
+
+// A step's bookkeeping before its final GEMV runs outside the decode step:
+// the position and cleared argmax slots.
+__global__ void set_step_kernel(DecodeState* st, int pos) {
+    if (threadIdx.x == 0) st->pos = pos;
+    for (int i = threadIdx.x; i < kArgmaxSlots; i += blockDim.x) st->argmax_keys[i * kArgmaxStride] = 0ull;
+}
+
+hipError_t launch_set_step(DecodeState* st, int pos, hipStream_t stream) {
+    if (!st || pos < 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(64), 0, stream, st, pos);
+    return hipGetLastError();
+}
+
 // One wave: the max over the argmax slots, then the step bookkeeping.
 __global__ __launch_bounds__(64) void finish_step_kernel(DecodeState* st, int* out_tokens) {
     const int lane = threadIdx.x;

@@ -17,7 +17,10 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <algorithm>
 
 #include <string>
 #include <vector>
@@ -75,6 +78,13 @@ struct mantleHipModel {
     bool split = false;  // split attention kernels (transposed V cache)
     int load_ctx = 0;    // maxContext given at load (SetEffectiveContextLength(0) restores it)
     hipGraphExec_t graph = nullptr;
+    // Batched prompt rows (prefill_rows): buffers for up to pf_cap rows, made on first use
+    struct Prefill {
+        int cap = 0;
+        float *x = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *gate = nullptr, *up = nullptr;
+        float *scores = nullptr, *xs = nullptr, *atts = nullptr;
+        int8_t *qx = nullptr, *attq = nullptr;
+    } pf;
 };
 
 // Layer l's base in a KV cache of `rows` keys per kv column (f32, f16 or int8 elements).
@@ -324,8 +334,17 @@ static bool json_number(const std::string& js, const char* key, double* out) {
     return true;
 }
 
+static void free_prefill(mantleHipModel* m) {
+    auto& p = m->pf;
+    void* bufs[] = {p.x, p.qkv, p.q, p.att, p.gate, p.up, p.scores, p.xs, p.atts, p.qx, p.attq};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    p = mantleHipModel::Prefill{};
+}
+
 static void free_model(mantleHipModel* m) {
     if (!m) return;
+    free_prefill(m);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
     void* bufs[] = {m->arena, m->x, m->qkv, m->attn, m->act, m->logits, m->scores, m->attn_counters, m->xn, m->up, m->qx, m->xs, m->cache_k,
                     m->cache_v, m->k_scale, m->v_scale, m->rope_cos, m->rope_sin, m->state, m->prompt, m->out_tokens};
@@ -789,11 +808,184 @@ extern "C" int mantleHipModelForwardToken(mantleHipModel* m, int tok, float* log
     return hipStreamSynchronize(m->stream);
 }
 
+// Prompt rows at once: the decode step's layer loop (runtime_decode.go:81-203)
+// over R consecutive positions, each projection one int8-MFMA product over all
+// R rows (launch_k4_gemm_w4a8, bit-identical per row to the step's GEMV), the
+// attention row r at position pos + r with the step's kernels
+// (launch_attention_rows), and the final RMSNorm / lm_head / argmax for the
+// last row only -- the prompt's earlier rows need no logits.  Every value the
+// cache and the last row receive equals the per-token steps' (the prefill
+// tests compare the two).  Requires k4 weights, the split attention kernels,
+// head_dim 64 / 128 and row widths of whole 8-block chunks; other models take
+// the per-token steps.
+static constexpr int kPrefillRows = 256;  // rows per pass (scores: rows * n_heads * max_ctx floats)
+
+static bool prefill_rows_ok(const mantleHipModel* m) {
+    const mantleHipQwen3Config& c = m->cfg;
+    const char* e = getenv("MANTLE_HIP_PREFILL");
+    if (e && !strcmp(e, "steps")) return false;
+    return !m->bf16 && m->split && (c.head_dim == 64 || c.head_dim == 128) && c.d_model % 256 == 0 &&
+           m->q_dim % 256 == 0 && c.ffn % 256 == 0 && m->max_ctx <= 32768 &&
+           (attention_path() == kAttnPathSplit || attention_path() == kAttnPathFused);
+}
+
+static hipError_t prefill_alloc(mantleHipModel* m, int rows) {
+    if (m->pf.cap >= rows) return hipSuccess;
+    free_prefill(m);
+    const mantleHipQwen3Config& c = m->cfg;
+    auto& p = m->pf;
+    const size_t R = (size_t)rows;
+    const int wide = std::max(std::max(c.d_model, m->q_dim), c.ffn);
+    hipError_t e;
+#define TRYP(x)                        \
+    do {                               \
+        if ((e = (x)) != hipSuccess) { \
+            free_prefill(m);           \
+            return e;                  \
+        }                              \
+    } while (0)
+    TRYP(hipMalloc((void**)&p.x, sizeof(float) * R * c.d_model));
+    TRYP(hipMalloc((void**)&p.qkv, sizeof(float) * R * (m->q_dim + 2 * m->kv_dim)));
+    TRYP(hipMalloc((void**)&p.q, sizeof(float) * R * m->q_dim));
+    TRYP(hipMalloc((void**)&p.att, sizeof(float) * R * m->q_dim));
+    TRYP(hipMalloc((void**)&p.gate, sizeof(float) * R * c.ffn));
+    TRYP(hipMalloc((void**)&p.up, sizeof(float) * R * c.ffn));
+    TRYP(hipMalloc((void**)&p.scores, sizeof(float) * R * c.n_heads * m->max_ctx));
+    TRYP(hipMalloc((void**)&p.qx, R * wide));
+    TRYP(hipMalloc((void**)&p.xs, sizeof(float) * R * (wide / 32)));
+    TRYP(hipMalloc((void**)&p.attq, R * m->q_dim));
+    TRYP(hipMalloc((void**)&p.atts, sizeof(float) * R * (m->q_dim / 32)));
+#undef TRYP
+    p.cap = rows;
+    return hipSuccess;
+}
+
+// Rows pos .. pos+R-1 (tokens already in m->prompt); leaves the state as the
+// per-token steps would: state->pos = pos + R, next_tok / out_tokens[pos+R-1]
+// the argmax of the last row, logits of the last row.
+static hipError_t prefill_rows(mantleHipModel* m, int R, hipStream_t s) {
+    const mantleHipQwen3Config& c = m->cfg;
+    auto& p = m->pf;
+    const int d = c.d_model, pos = m->pos;
+    const int qkvw = m->q_dim + 2 * m->kv_dim;
+    hipError_t e;
+#define TRY(x)                         \
+    do {                               \
+        if ((e = (x)) != hipSuccess) { \
+            return e;                  \
+        }                              \
+    } while (0)
+    TRY(launch_embed_rows(m->embed, d, m->prompt + pos, R, p.x, s));
+    for (int l = 0; l < c.n_layers; l++) {
+        const auto& L = m->layers[l];
+        // attention: RMSNorm + one int8 activation per row, Q / K / V
+        TRY(launch_quantize_vec(p.x, L.attn_norm, c.eps, d, R, m->isa, p.qx, p.xs, nullptr, s));
+        TRY(launch_k4_gemm_w4a8(L.wq, d, p.qx, p.xs, R, p.qkv, qkvw, kEpiStore, s));
+        TRY(launch_k4_gemm_w4a8(L.wk, d, p.qx, p.xs, R, p.qkv + m->q_dim, qkvw, kEpiStore, s));
+        TRY(launch_k4_gemm_w4a8(L.wv, d, p.qx, p.xs, R, p.qkv + m->q_dim + m->kv_dim, qkvw, kEpiStore, s));
+        AttnArgs a{};
+        a.q = p.qkv;
+        a.k = p.qkv + m->q_dim;
+        a.v = p.qkv + m->q_dim + m->kv_dim;
+        a.q_norm = L.q_norm;
+        a.k_norm = L.k_norm;
+        a.eps = c.eps;
+        a.rope_cos = m->rope_cos;
+        a.rope_sin = m->rope_sin;
+        a.pos_host = pos;
+        a.n_head = c.n_heads;
+        a.kv_heads = c.n_kv_heads;
+        a.head_dim = c.head_dim;
+        a.max_ctx = m->max_ctx;
+        a.scale = (float)(1.0 / sqrt((double)c.head_dim));
+        a.isa = m->isa;
+        a.out_row = m->q_dim;
+        a.cache_k = layer_cache(m, m->cache_k, l, m->max_ctx, m->k_type);
+        a.cache_v = layer_cache(m, m->cache_v, l, m->v_rows, m->v_type);
+        a.k_type = m->k_type;
+        a.v_type = m->v_type;
+        a.vt_stride = m->vt_stride;
+        a.kv_stride = c.head_dim;
+        a.head_stride = m->max_ctx * c.head_dim;
+        if (m->k_type == kKvQ8) a.k_scale = m->k_scale + (size_t)l * m->max_ctx;
+        if (m->v_type == kKvQ8) a.v_scale = m->v_scale + (size_t)l * m->max_ctx;
+        TRY(launch_attention_prep_rows(a, R, qkvw, p.q, s));
+        if (m->k_type == kKvQ8 || m->v_type == kKvQ8) {
+            KvQ8Args q{};
+            q.k = a.k;
+            q.v = a.v;
+            q.k_norm = a.k_norm;
+            q.rope_cos = a.rope_cos;
+            q.rope_sin = a.rope_sin;
+            q.pos_host = pos;
+            q.eps = a.eps;
+            q.isa = a.isa;
+            q.kv_heads = c.n_kv_heads;
+            q.head_dim = c.head_dim;
+            q.cache_k = reinterpret_cast<int8_t*>(a.cache_k);
+            q.cache_v = reinterpret_cast<int8_t*>(a.cache_v);
+            q.head_stride = a.head_stride;
+            q.row_stride = a.kv_stride;
+            q.vt_stride = a.vt_stride;
+            q.k_scale = const_cast<float*>(a.k_scale);
+            q.v_scale = const_cast<float*>(a.v_scale);
+            q.prep = 1;
+            q.skip_k = m->k_type != kKvQ8;
+            q.skip_v = m->v_type != kKvQ8;
+            q.tokens = R;
+            q.tok_stride = qkvw;
+            TRY(launch_kv_append_q8(q, s));
+        }
+        a.q = p.q;
+        a.q_row = m->q_dim;
+        a.scores = p.scores;
+        a.scores_row = (size_t)c.n_heads * m->max_ctx;
+        a.out = p.att;
+        a.q_out = p.attq;  // Wo's int8 activation (head_dim is a multiple of 32)
+        a.q_scale = p.atts;
+        TRY(launch_attention_rows(a, R, s));
+        TRY(launch_k4_gemm_w4a8(L.wo, m->q_dim, p.attq, p.atts, R, p.x, d, kEpiResAdd, s));
+        // FFN: RMSNorm + int8 activation, gate / up, SiLU(gate) * up re-quantised, down
+        TRY(launch_quantize_vec(p.x, L.ffn_norm, c.eps, d, R, m->isa, p.qx, p.xs, nullptr, s));
+        TRY(launch_k4_gemm_w4a8(L.gate, d, p.qx, p.xs, R, p.gate, c.ffn, kEpiStore, s));
+        TRY(launch_k4_gemm_w4a8(L.up, d, p.qx, p.xs, R, p.up, c.ffn, kEpiStore, s));
+        TRY(launch_silu_mul(p.gate, p.up, p.gate, R * c.ffn, s));
+        TRY(launch_quantize_vec(p.gate, nullptr, 0.0f, c.ffn, R, m->isa, p.qx, p.xs, nullptr, s));
+        TRY(launch_k4_gemm_w4a8(L.down, c.ffn, p.qx, p.xs, R, p.x, d, kEpiResAdd, s));
+    }
+    // the last row: final RMSNorm, lm_head, argmax, as the step's end
+    TRY(launch_set_step(m->state, pos + R - 1, s));
+    float* lo[1] = {m->logits};
+    TRY(launch_k4_gemv_w4a8_fused(&m->lm_head, lo, 1, d, p.x + (size_t)(R - 1) * d, m->final_norm, c.eps, m->isa, 1,
+                                  kEpiArgmax, m->state->argmax_keys, s));
+    TRY(launch_finish_step(m->state, m->out_tokens, s));
+    // x holds the last row's residual stream, as after its step (mantleHipModelHidden)
+    TRY(hipMemcpyAsync(m->x, p.x + (size_t)(R - 1) * d, sizeof(float) * d, hipMemcpyDeviceToDevice, s));
+#undef TRY
+    m->pos += R;
+    return hipSuccess;
+}
+
+// All n prompt tokens (already uploaded): passes of up to kPrefillRows rows,
+// or the per-token steps where the batched form does not apply.
+static hipError_t run_prompt(mantleHipModel* m, int n) {
+    if (n <= 1 || !prefill_rows_ok(m)) return run_steps(m, n);
+    if (m->pos + n > m->max_ctx) return hipErrorInvalidValue;
+    hipError_t e = prefill_alloc(m, std::min(n, kPrefillRows));
+    if (e != hipSuccess) return e;
+    for (int done = 0; done < n;) {
+        const int R = std::min(n - done, m->pf.cap);
+        if ((e = prefill_rows(m, R, m->stream)) != hipSuccess) return e;
+        done += R;
+    }
+    return hipSuccess;
+}
+
 extern "C" int mantleHipModelPrefillTokens(mantleHipModel* m, const int* toks, int n, int* next) {
     if (!m || !toks || n <= 0) return hipErrorInvalidValue;
     hipError_t e = upload_tokens(m, toks, n);
     if (e != hipSuccess) return e;
-    if ((e = run_steps(m, n)) != hipSuccess) return e;
+    if ((e = run_prompt(m, n)) != hipSuccess) return e;
     if (next) {
         if ((e = hipMemcpyAsync(next, &m->state->next_tok, sizeof(int), hipMemcpyDeviceToHost, m->stream)) !=
             hipSuccess)
@@ -847,7 +1039,8 @@ extern "C" int mantleHipModelGenerateGreedy(mantleHipModel* m, const int* prompt
     if (p0 + n_prompt + n_gen - 1 > m->max_ctx) return hipErrorInvalidValue;
     hipError_t e = upload_tokens(m, prompt, n_prompt);
     if (e != hipSuccess) return e;
-    if ((e = run_steps(m, n_prompt + n_gen - 1)) != hipSuccess) return e;
+    if ((e = run_prompt(m, n_prompt)) != hipSuccess) return e;
+    if ((e = run_steps(m, n_gen - 1)) != hipSuccess) return e;
     e = hipMemcpyAsync(out_tokens, m->out_tokens + p0 + n_prompt - 1, sizeof(int) * n_gen, hipMemcpyDeviceToHost,
                        m->stream);
     if (e != hipSuccess) return e;
