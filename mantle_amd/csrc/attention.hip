@@ -1607,6 +1607,196 @@ hipError_t launch_attention_decode(const AttnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Prompt rows, batched per kv head: the decode kernels' arithmetic for every
+// (row, head), with each K chunk and V column loaded once for a block of
+// kRowsQ (row, head) queries of one kv group instead of once per query.
+// Query qi of block b is row b*RB + qi/G, head g*G + qi%G (G = n_head /
+// kv_heads, RB = kRowsQ / G rows per block).
+static constexpr int kRowsQ = 32;
+
+// Scores: workgroup (kv head g, key chunk c, row block b) stages the chunk's
+// 64 keys (widened to fp32) and the block's queries in LDS; wave w takes
+// queries w, w+4, ..., lane k key t0+k: s = dot_isa(q, k) * scale, as
+// scores_split_chunks computes it.
+template <int HD, int KV>
+__global__ __launch_bounds__(kThreads) void attention_scores_rows(AttnArgs a, int rows) {
+    extern __shared__ __align__(16) float lds[];
+    constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
+    constexpr int kp = HD + 4, kc = kAttnKeys;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int G = a.n_head / a.kv_heads, RB = kRowsQ / G;
+    const int g = blockIdx.x, c = blockIdx.y;
+    const int r0 = (int)blockIdx.z * RB;
+    const int rn = min(RB, rows - r0);
+    const int pos0 = a.pos_host + r0, t0 = c * kc;
+    if (rn <= 0 || t0 > pos0 + rn - 1) return;  // every row of the block ends before the chunk
+    const int nk = min(kc, pos0 + rn - t0);      // keys up to the block's last position
+    float* kt = lds;                             // [64 keys][kp]
+    float* sq = lds + kc * kp;                   // [queries][HD]
+    ChunkRegs ck;
+    ChunkRegs16 ck16;
+    ChunkRegs8 ck8;
+    if constexpr (Q8)
+        chunk_issue8_t<HD>(ck8, reinterpret_cast<const int8_t*>(a.cache_k) + (size_t)g * a.head_stride, a.kv_stride,
+                           t0, nk, kp);
+    else if constexpr (F16)
+        chunk_issue16_t<HD>(ck16, reinterpret_cast<const uint16_t*>(a.cache_k) + (size_t)g * a.head_stride,
+                            a.kv_stride, t0, nk, kp, -1);
+    else
+        chunk_issue_t<HD>(ck, a.cache_k + (size_t)g * a.head_stride, a.kv_stride, t0, nk, HD, kp, -1);
+    const int nq = rn * G;
+    for (int i = tid * 4; i < nq * HD; i += kThreads * 4) {
+        const int qi = i / HD, d = i - qi * HD;
+        const int ri = qi / G, hi = qi - ri * G;
+        *reinterpret_cast<f32x4*>(sq + i) =
+            *reinterpret_cast<const f32x4*>(a.q + (size_t)(r0 + ri) * a.q_row + (g * G + hi) * HD + d);
+    }
+    if constexpr (Q8) chunk_store8(ck8, kt);
+    else if constexpr (F16) chunk_store16(ck16, kt, kp, nullptr, t0, nk, -1, HD);
+    else chunk_store_v4(ck, kt, kp, nullptr, t0, nk, -1, HD);
+    __syncthreads();
+    const int t = t0 + lane;
+    for (int qi = wave; qi < nq; qi += kThreads / 64) {
+        const int ri = qi / G, hi = qi - ri * G;
+        if (t > pos0 + ri) continue;
+        float* sg = a.scores + (size_t)(r0 + ri) * a.scores_row + (size_t)(g * G + hi) * a.max_ctx;
+        const float4* qv = reinterpret_cast<const float4*>(sq + qi * HD);
+        const float4* kv = reinterpret_cast<const float4*>(kt + lane * kp);
+        if constexpr (Q8) sg[t] = (dot_parity_v4<HD, kIsaScalar>(qv, kv) * a.k_scale[t]) * a.scale;
+        else sg[t] = (F16 ? dot_parity_v4<HD, kIsaScalar>(qv, kv) : dot_v4_isa<HD>(qv, kv, a.isa)) * a.scale;
+    }
+}
+
+// Softmax of (row blockIdx.y, head blockIdx.x) in place in the scores buffer
+// (head_softmax: max, exponentials, the ordered sum, x *= 1/sum).
+__global__ __launch_bounds__(kThreads) void attention_softmax_rows(AttnArgs a) {
+    __shared__ float red[8];
+    const int h = blockIdx.x, r = blockIdx.y;
+    float* sg = a.scores + (size_t)r * a.scores_row + (size_t)h * a.max_ctx;
+    head_softmax<true>(sg, sg, red, a.pos_host + r);
+}
+
+// The V sum, transposed cache: workgroup (kv head g, row block b); wave w
+// holds columns 64*(w % CW) .. +63 of the head (CW = HD / 64 column waves)
+// and sums queries qp, qp + QW, ... (qp = w / CW, QW = 4 / CW), lane = column.
+// Per 64-key chunk a lane loads its column's keys once (widened to fp32) and
+// applies them to each of its queries in key order, acc + p*v (q8_0:
+// acc + (p*q)*s), the probabilities and scales read as wave-uniform values:
+// the ordered sum of VColumn::sum for every (query, column).
+template <int HD, int KV>
+__global__ __launch_bounds__(kThreads) void attention_pv_rows(AttnArgs a, int rows) {
+    constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
+    constexpr int CW = HD / 64, QW = 4 / CW, NQ = kRowsQ / QW;  // queries per wave
+    constexpr int kc = 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the probabilities load as scalars
+    const int G = a.n_head / a.kv_heads, RB = kRowsQ / G;
+    const int g = blockIdx.x;
+    const int r0 = (int)blockIdx.y * RB;
+    const int rn = min(RB, rows - r0);
+    if (rn <= 0) return;
+    const int pos0 = a.pos_host + r0;
+    const int col = (wave % CW) * 64 + lane, qp = wave / CW;
+    const size_t cidx = (size_t)(g * HD + col) * a.vt_stride;
+    const float* vcol = a.cache_v + cidx;
+    const uint16_t* vcol16 = reinterpret_cast<const uint16_t*>(a.cache_v) + cidx;
+    const int8_t* vcol8 = reinterpret_cast<const int8_t*>(a.cache_v) + cidx;
+    float acc[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; j++) acc[j] = 0.0f;
+    const int last = pos0 + rn - 1;  // the block's last position
+    for (int t0 = 0; t0 <= last; t0 += kc) {
+        float v[kc];
+        // keys past `last` are read at the last whole group (never added)
+        if constexpr (Q8) {
+#pragma unroll
+            for (int j = 0; j < kc / 16; j++) {
+                const int tk = min(t0 + 16 * j, last & ~15);
+                const u32x4 b = *reinterpret_cast<const u32x4*>(vcol8 + tk);
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    v[16 * j + 4 * w] = q8_byte_sdwa<0>(b[w]);
+                    v[16 * j + 4 * w + 1] = q8_byte_sdwa<1>(b[w]);
+                    v[16 * j + 4 * w + 2] = q8_byte_sdwa<2>(b[w]);
+                    v[16 * j + 4 * w + 3] = q8_byte_sdwa<3>(b[w]);
+                }
+            }
+        } else if constexpr (F16) {
+#pragma unroll
+            for (int j = 0; j < kc / 4; j++) {
+                const u32x2 h = *reinterpret_cast<const u32x2*>(vcol16 + min(t0 + 4 * j, last & ~3));
+                v[4 * j] = f16_cache_load((uint16_t)(h.x & 0xFFFFu));
+                v[4 * j + 1] = f16_cache_load((uint16_t)(h.x >> 16));
+                v[4 * j + 2] = f16_cache_load((uint16_t)(h.y & 0xFFFFu));
+                v[4 * j + 3] = f16_cache_load((uint16_t)(h.y >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kc / 4; j++) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(vcol + min(t0 + 4 * j, last & ~3));
+                v[4 * j] = x.x;
+                v[4 * j + 1] = x.y;
+                v[4 * j + 2] = x.z;
+                v[4 * j + 3] = x.w;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NQ; j++) {
+            const int qi = qp + QW * j;
+            const int ri = qi / G, hi = qi - ri * G;
+            const int pos = pos0 + ri;
+            if (ri >= rn || t0 > pos) continue;  // wave-uniform
+            const float* __restrict__ p =
+                a.scores + (size_t)(r0 + ri) * a.scores_row + (size_t)(g * G + hi) * a.max_ctx + t0;
+            const float* __restrict__ sc = Q8 ? a.v_scale + t0 : p;
+            float s = acc[j];
+            if (t0 + kc - 1 <= pos) {
+#pragma unroll
+                for (int k = 0; k < kc; k++) s = s + (Q8 ? (p[k] * v[k]) * sc[k] : p[k] * v[k]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < kc; k++)
+                    if (t0 + k <= pos) s = s + (Q8 ? (p[k] * v[k]) * sc[k] : p[k] * v[k]);
+            }
+            acc[j] = s;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; j++) {
+        const int qi = qp + QW * j;
+        const int ri = qi / G, hi = qi - ri * G;
+        const bool live = ri < rn;
+        AttnArgs o = a;  // the row's output pointers
+        const size_t r = (size_t)(r0 + (live ? ri : 0));
+        o.out = a.out + r * a.out_row;
+        if (a.q_out) {
+            o.q_out = a.q_out + r * a.out_row;
+            o.q_scale = a.q_scale + r * (a.out_row / 32);
+        }
+        store_attn_out(o, (g * G + hi) * HD + col, acc[j], live);
+    }
+}
+
+static hipError_t launch_rows_batched(const AttnArgs& a, int rows, hipStream_t stream) {
+    const int G = a.n_head / a.kv_heads, RB = kRowsQ / G;
+    const int nblk = (rows + RB - 1) / RB;
+    const int last = a.pos_host + rows - 1;
+    const int nchunks = last / kAttnKeys + 1;
+    const bool hd128 = a.head_dim == 128;
+    void (*const sc[2][3])(AttnArgs, int) = {
+        {attention_scores_rows<64, kKvF32>, attention_scores_rows<64, kKvF16>, attention_scores_rows<64, kKvQ8>},
+        {attention_scores_rows<128, kKvF32>, attention_scores_rows<128, kKvF16>, attention_scores_rows<128, kKvQ8>}};
+    void (*const pv[2][3])(AttnArgs, int) = {
+        {attention_pv_rows<64, kKvF32>, attention_pv_rows<64, kKvF16>, attention_pv_rows<64, kKvQ8>},
+        {attention_pv_rows<128, kKvF32>, attention_pv_rows<128, kKvF16>, attention_pv_rows<128, kKvQ8>}};
+    const size_t smem = sizeof(float) * ((size_t)kAttnKeys * (a.head_dim + 4) + (size_t)kRowsQ * a.head_dim);
+    hipLaunchKernelGGL(sc[hd128][a.k_type], dim3(a.kv_heads, nchunks, nblk), dim3(kThreads), smem, stream, a, rows);
+    hipLaunchKernelGGL(attention_softmax_rows, dim3(a.n_head, rows), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(pv[hd128][a.v_type], dim3(a.kv_heads, nblk), dim3(kThreads), 0, stream, a, rows);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention_rows(const AttnArgs& a, int rows, hipStream_t stream) {
     if (rows < 1 || a.fused || a.pos_dev || a.pos_host < 0 || a.pos_host + rows > a.max_ctx ||
         (a.head_dim != 64 && a.head_dim != 128) || !a.scores || a.max_ctx > kSplitMaxCtx ||
@@ -1626,6 +1816,11 @@ hipError_t launch_attention_rows(const AttnArgs& a, int rows, hipStream_t stream
         return hipErrorInvalidValue;
     if ((a.k_type == kKvQ8 || (a.v_type == kKvQ8 && a.vt_stride == 0)) && ((a.kv_stride & 15) || (a.head_stride & 15)))
         return hipErrorInvalidValue;
+    // the batched form: transposed V, whole kv groups in a block of kRowsQ queries
+    const int G = a.kv_heads > 0 ? a.n_head / a.kv_heads : 0;
+    const bool batched = a.vt_stride > 0 && G > 0 && a.n_head == G * a.kv_heads && kRowsQ % G == 0 &&
+                         a.key_base == 0 && a.key_ring == 0;
+    if (batched && !getenv("MANTLE_HIP_ROWS_PER_QUERY")) return launch_rows_batched(a, rows, stream);
     return launch_split_two(a, rows, stream);
 }
 

@@ -818,7 +818,16 @@ extern "C" int mantleHipModelForwardToken(mantleHipModel* m, int tok, float* log
 // tests compare the two).  Requires k4 weights, the split attention kernels,
 // head_dim 64 / 128 and row widths of whole 8-block chunks; other models take
 // the per-token steps.
-static constexpr int kPrefillRows = 256;  // rows per pass (scores: rows * n_heads * max_ctx floats)
+static constexpr int kPrefillRows = 1024;                      // rows per pass at most ...
+static constexpr size_t kPrefillScoreBytes = (size_t)512 << 20;  // ... and their scores within 512 MiB
+
+static int prefill_pass_rows(const mantleHipModel* m, int n) {
+    const size_t per_row = sizeof(float) * (size_t)m->cfg.n_heads * m->max_ctx;
+    size_t r = kPrefillScoreBytes / per_row;
+    r = r < 16 ? 16 : r;
+    r = r > (size_t)kPrefillRows ? (size_t)kPrefillRows : r;
+    return n < (int)r ? n : (int)r;
+}
 
 static bool prefill_rows_ok(const mantleHipModel* m) {
     const mantleHipQwen3Config& c = m->cfg;
@@ -971,7 +980,7 @@ static hipError_t prefill_rows(mantleHipModel* m, int R, hipStream_t s) {
 static hipError_t run_prompt(mantleHipModel* m, int n) {
     if (n <= 1 || !prefill_rows_ok(m)) return run_steps(m, n);
     if (m->pos + n > m->max_ctx) return hipErrorInvalidValue;
-    hipError_t e = prefill_alloc(m, std::min(n, kPrefillRows));
+    hipError_t e = prefill_alloc(m, prefill_pass_rows(m, n));
     if (e != hipSuccess) return e;
     for (int done = 0; done < n;) {
         const int R = std::min(n - done, m->pf.cap);

@@ -97,3 +97,13 @@ def test_generate_greedy_rows_match_steps(hip, lane_path):
             rt.close()
             os.environ.pop("MANTLE_HIP_PREFILL", None)
     assert outs[0] == outs[1]
+
+
+def test_prefill_rows_gqa4_wide_rows(hip, tmp_models):
+    """Four query heads per kv head (Qwen3-4B's 32 / 8) and 2560 / 9728-wide rows."""
+    path = models.pack(str(tmp_models / "wide4b_rows.mcf"), 1, models.WIDE4B)
+    prompt = models.prompt(70, models.WIDE4B["vocab"], 4)
+    rows = _run(path, 128, prompt, 3, None)
+    steps = _run(path, 128, prompt, 3, "steps")
+    for i, (a, b) in enumerate(zip(rows, steps)):
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"output {i}")
