@@ -1677,21 +1677,25 @@ __global__ __launch_bounds__(kThreads) void attention_softmax_rows(AttnArgs a) {
     head_softmax<true>(sg, sg, red, a.pos_host + r);
 }
 
-// The V sum, transposed cache: workgroup (kv head g, row block b); wave w
-// holds columns 64*(w % CW) .. +63 of the head (CW = HD / 64 column waves)
-// and sums queries qp, qp + QW, ... (qp = w / CW, QW = 4 / CW), lane = column.
-// Per 64-key chunk a lane loads its column's keys once (widened to fp32) and
-// applies them to each of its queries in key order, acc + p*v (q8_0:
-// acc + (p*q)*s), the probabilities and scales read as wave-uniform values:
-// the ordered sum of VColumn::sum for every (query, column).
+// The V sum, transposed cache: workgroup (kv head g, block b of kPvRowsQ
+// queries); wave w holds columns 64*(w % CW) .. +63 of the head (CW = HD / 64
+// column waves) and sums queries qp, qp + QW, ... (qp = w / CW, QW = 4 / CW),
+// lane = column.  Per 64-key chunk a lane loads its column's keys once
+// (widened to fp32) and applies them to each of its queries in key order,
+// acc + p*v (q8_0: acc + (p*q)*s); the block's probabilities (and the keys'
+// q8_0 scales) of the chunk are staged in LDS by the whole workgroup and read
+// as broadcasts: the ordered sum of VColumn::sum for every (query, column).
+static constexpr int kPvRowsQ = 16;
+
 template <int HD, int KV>
 __global__ __launch_bounds__(kThreads) void attention_pv_rows(AttnArgs a, int rows) {
     constexpr bool F16 = KV == kKvF16, Q8 = KV == kKvQ8;
-    constexpr int CW = HD / 64, QW = 4 / CW, NQ = kRowsQ / QW;  // queries per wave
-    constexpr int kc = 64;
+    constexpr int CW = HD / 64, QW = 4 / CW, NQ = kPvRowsQ / QW;  // queries per wave
+    constexpr int kc = 64, PP = kc + 4;                          // keys per chunk, staged pitch
+    __shared__ __align__(16) float ps[kPvRowsQ * PP + kc];       // [query][key], then q8_0 scales
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the probabilities load as scalars
-    const int G = a.n_head / a.kv_heads, RB = kRowsQ / G;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.n_head / a.kv_heads, RB = kPvRowsQ / G;
     const int g = blockIdx.x;
     const int r0 = (int)blockIdx.y * RB;
     const int rn = min(RB, rows - r0);
@@ -1706,7 +1710,25 @@ __global__ __launch_bounds__(kThreads) void attention_pv_rows(AttnArgs a, int ro
 #pragma unroll
     for (int j = 0; j < NQ; j++) acc[j] = 0.0f;
     const int last = pos0 + rn - 1;  // the block's last position
+    const int nq = rn * G;
     for (int t0 = 0; t0 <= last; t0 += kc) {
+        __syncthreads();  // the previous chunk's probabilities are read
+        // stage: query qi's probabilities t0 .. t0+63 (up to its own position)
+        for (int i = tid; i < nq * (kc / 4); i += kThreads) {
+            const int qi = i / (kc / 4), k4 = i - qi * (kc / 4);
+            const int ri = qi / G, hi = qi - ri * G;
+            const int lim = pos0 + ri - t0;  // last key of this query in the chunk
+            if (4 * k4 > lim) continue;
+            const float* src = a.scores + (size_t)(r0 + ri) * a.scores_row + (size_t)(g * G + hi) * a.max_ctx + t0;
+            f32x4 v4;
+            v4.x = src[4 * k4];
+            v4.y = 4 * k4 + 1 <= lim ? src[4 * k4 + 1] : 0.0f;
+            v4.z = 4 * k4 + 2 <= lim ? src[4 * k4 + 2] : 0.0f;
+            v4.w = 4 * k4 + 3 <= lim ? src[4 * k4 + 3] : 0.0f;
+            *reinterpret_cast<f32x4*>(ps + qi * PP + 4 * k4) = v4;
+        }
+        if constexpr (Q8)
+            if (tid < kc) ps[kPvRowsQ * PP + tid] = a.v_scale[min(t0 + tid, last)];
         float v[kc];
         // keys past `last` are read at the last whole group (never added)
         if constexpr (Q8) {
@@ -1741,23 +1763,35 @@ __global__ __launch_bounds__(kThreads) void attention_pv_rows(AttnArgs a, int ro
                 v[4 * j + 3] = x.w;
             }
         }
+        __syncthreads();
+        const float* sc = ps + kPvRowsQ * PP;
 #pragma unroll
         for (int j = 0; j < NQ; j++) {
             const int qi = qp + QW * j;
-            const int ri = qi / G, hi = qi - ri * G;
+            const int ri = qi / G;
             const int pos = pos0 + ri;
             if (ri >= rn || t0 > pos) continue;  // wave-uniform
-            const float* __restrict__ p =
-                a.scores + (size_t)(r0 + ri) * a.scores_row + (size_t)(g * G + hi) * a.max_ctx + t0;
-            const float* __restrict__ sc = Q8 ? a.v_scale + t0 : p;
+            const float* pq = ps + qi * PP;
             float s = acc[j];
+            auto term = [&](int k, float pk) { return Q8 ? (pk * v[k]) * sc[k] : pk * v[k]; };
             if (t0 + kc - 1 <= pos) {
 #pragma unroll
-                for (int k = 0; k < kc; k++) s = s + (Q8 ? (p[k] * v[k]) * sc[k] : p[k] * v[k]);
+                for (int k4 = 0; k4 < kc / 4; k4++) {
+                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(pq + 4 * k4);
+                    s = s + term(4 * k4, p4.x);
+                    s = s + term(4 * k4 + 1, p4.y);
+                    s = s + term(4 * k4 + 2, p4.z);
+                    s = s + term(4 * k4 + 3, p4.w);
+                }
             } else {
 #pragma unroll
-                for (int k = 0; k < kc; k++)
-                    if (t0 + k <= pos) s = s + (Q8 ? (p[k] * v[k]) * sc[k] : p[k] * v[k]);
+                for (int k4 = 0; k4 < kc / 4; k4++) {
+                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(pq + 4 * k4);
+                    const float pk[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        if (t0 + 4 * k4 + c <= pos) s = s + term(4 * k4 + c, pk[c]);
+                }
             }
             acc[j] = s;
         }
@@ -1781,6 +1815,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_rows(AttnArgs a, int ro
 static hipError_t launch_rows_batched(const AttnArgs& a, int rows, hipStream_t stream) {
     const int G = a.n_head / a.kv_heads, RB = kRowsQ / G;
     const int nblk = (rows + RB - 1) / RB;
+    const int RBv = kPvRowsQ / G, nblk_v = (rows + RBv - 1) / RBv;
     const int last = a.pos_host + rows - 1;
     const int nchunks = last / kAttnKeys + 1;
     const bool hd128 = a.head_dim == 128;
@@ -1793,7 +1828,7 @@ static hipError_t launch_rows_batched(const AttnArgs& a, int rows, hipStream_t s
     const size_t smem = sizeof(float) * ((size_t)kAttnKeys * (a.head_dim + 4) + (size_t)kRowsQ * a.head_dim);
     hipLaunchKernelGGL(sc[hd128][a.k_type], dim3(a.kv_heads, nchunks, nblk), dim3(kThreads), smem, stream, a, rows);
     hipLaunchKernelGGL(attention_softmax_rows, dim3(a.n_head, rows), dim3(kThreads), 0, stream, a);
-    hipLaunchKernelGGL(pv[hd128][a.v_type], dim3(a.kv_heads, nblk), dim3(kThreads), 0, stream, a, rows);
+    hipLaunchKernelGGL(pv[hd128][a.v_type], dim3(a.kv_heads, nblk_v), dim3(kThreads), 0, stream, a, rows);
     return hipGetLastError();
 }
 
@@ -1818,7 +1853,7 @@ hipError_t launch_attention_rows(const AttnArgs& a, int rows, hipStream_t stream
         return hipErrorInvalidValue;
     // the batched form: transposed V, whole kv groups in a block of kRowsQ queries
     const int G = a.kv_heads > 0 ? a.n_head / a.kv_heads : 0;
-    const bool batched = a.vt_stride > 0 && G > 0 && a.n_head == G * a.kv_heads && kRowsQ % G == 0 &&
+    const bool batched = a.vt_stride > 0 && G > 0 && a.n_head == G * a.kv_heads && kRowsQ % G == 0 && kPvRowsQ % G == 0 &&
                          a.key_base == 0 && a.key_ring == 0;
     if (batched && !getenv("MANTLE_HIP_ROWS_PER_QUERY")) return launch_rows_batched(a, rows, stream);
     return launch_split_two(a, rows, stream);
