@@ -93,22 +93,24 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
     }
 
     // staging registers of one chunk
-    uint4 rw[WN_ITEMS], rx[XQ_ITEMS];
+    uint32_t rw[WN_ITEMS][4], rx[XQ_ITEMS][4];
     uint32_t rsub[SW_ITEMS];
     uint16_t rsup[SW_ITEMS];
     float rxs[XS_ITEMS];
-    auto load_chunk = [&](int b0) {
+    auto load_chunk = [&](int b0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < WN_ITEMS; i++) {
             const int it = tid + 256 * i, r = it >> 3, part = it & 7;
             const int gr = row0 + r < rows ? row0 + r : rows - 1;
-            rw[i] = reinterpret_cast<const uint4*>(a.w.nib)[(size_t)gr * bpr + b0 + part];
+            const uint4 u = reinterpret_cast<const uint4*>(a.w.nib)[(size_t)gr * bpr + b0 + part];
+            rw[i][0] = u.x; rw[i][1] = u.y; rw[i][2] = u.z; rw[i][3] = u.w;
         }
 #pragma unroll
         for (int i = 0; i < XQ_ITEMS; i++) {
             const int it = tid + 256 * i, v = (it >> 4) < TT ? it >> 4 : TT - 1, part = it & 15;
             const int gv = v0 + v < a.n ? v0 + v : a.n - 1;
-            rx[i] = reinterpret_cast<const uint4*>(a.qx + (size_t)gv * bpr * 32 + (size_t)b0 * 32)[part];
+            const uint4 u = reinterpret_cast<const uint4*>(a.qx + (size_t)gv * bpr * 32 + (size_t)b0 * 32)[part];
+            rx[i][0] = u.x; rx[i][1] = u.y; rx[i][2] = u.z; rx[i][3] = u.w;
         }
 #pragma unroll
         for (int i = 0; i < SW_ITEMS; i++) {
@@ -127,17 +129,17 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
         }
     };
     // stores the staged chunk; true if one of its scales is not finite
-    auto store_chunk = [&]() -> bool {
+    auto store_chunk = [&]() __attribute__((always_inline)) -> bool {
         bool odd = false;
 #pragma unroll
         for (int i = 0; i < WN_ITEMS; i++) {
             const int it = tid + 256 * i;
-            *reinterpret_cast<uint4*>(wn + (it >> 3) * WP + (it & 7) * 4) = rw[i];
+            *reinterpret_cast<uint4*>(wn + (it >> 3) * WP + (it & 7) * 4) = make_uint4(rw[i][0], rw[i][1], rw[i][2], rw[i][3]);
         }
 #pragma unroll
         for (int i = 0; i < XQ_ITEMS; i++) {
             const int it = tid + 256 * i;
-            if (TT * 16 % 256 == 0 || it < TT * 16) *reinterpret_cast<uint4*>(xq + (it >> 4) * XP + (it & 15) * 4) = rx[i];
+            if (TT * 16 % 256 == 0 || it < TT * 16) *reinterpret_cast<uint4*>(xq + (it >> 4) * XP + (it & 15) * 4) = make_uint4(rx[i][0], rx[i][1], rx[i][2], rx[i][3]);
         }
 #pragma unroll
         for (int i = 0; i < SW_ITEMS; i++) {
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
         xbase = xq + (wt0 + l16) * XP + kq;
 
     // The chunk in LDS, with (SKIP) or without the zero-scale test.
-    auto chunk_math = [&](auto skip_tag) {
+    auto chunk_math = [&](auto skip_tag) __attribute__((always_inline)) {
         constexpr bool SKIP = decltype(skip_tag)::value;
         // The MFMAs of a group of blocks are issued together into separate
         // results, then their terms applied: the matrix core's latency overlaps
@@ -283,7 +285,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
         __syncthreads();  // the previous chunk's readers are done
         const bool odd = store_chunk();
         const bool any_odd = __syncthreads_or(odd);
-        if (c + 1 < nch) load_chunk((c + 1) * kGemmKC);  // in flight while this chunk is multiplied
+        load_chunk((c + 1 < nch ? c + 1 : c) * kGemmKC);  // in flight while this chunk is multiplied (the last re-reads itself)
         if (any_odd)
             chunk_math(std::true_type{});
         else
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
     uint2 wbuf[D][RT][4];
     uint32_t sbuf[D][RT];
     uint32_t hbuf[D][RT];
-    auto issue = [&](int tile, int g, int slot) {
+    auto issue = [&](int tile, int g, int slot) __attribute__((always_inline)) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const int r0 = tile * RT * 16 + rt * 16 + l16;
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
                     d[jj][rt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bv[1], d[jj][rt], 0, 0, 0);
                 }
             }
-            auto terms = [&](auto skip_tag) {
+            auto terms = [&](auto skip_tag) __attribute__((always_inline)) {
                 constexpr bool SKIP = decltype(skip_tag)::value;
     #pragma unroll
                 for (int jj = 0; jj < 4; jj++) {
