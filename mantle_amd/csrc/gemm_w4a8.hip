@@ -56,6 +56,12 @@ struct GemmArgs {
     float* y;          // y[v * ldy + row]
     int n, ldy;
     int epi;           // kEpiStore or kEpiResAdd (y += sum)
+    // wide form, several matrices on the same activations in one launch: row
+    // tiles [tile_end[m-1], tile_end[m]) of the grid are matrix ws[m] into ys[m]
+    int nmat;
+    K4Mat ws[3];
+    float* ys[3];
+    int tile_end[3];
 };
 
 __device__ __forceinline__ float dpp_from_upper8(float v) {  // lane i <- lane i+8 within its row of 16
@@ -84,9 +90,18 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
     __shared__ __align__(16) float swT[kGemmKC * TR];    // [block][row]
     __shared__ __align__(16) float xsT[kGemmKC * TT];    // [block][vector]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row0 = (int)blockIdx.x * TR, v0 = (int)blockIdx.y * TT;
+    int tile = (int)blockIdx.x;
+    K4Mat W = a.w;  // this workgroup's matrix and output (locals: the arguments stay in registers)
+    float* Y = a.y;
+    if (!PAIR && a.nmat > 1) {
+        const int m = tile < a.tile_end[0] ? 0 : (tile < a.tile_end[1] ? 1 : 2);
+        tile -= m == 0 ? 0 : (m == 1 ? a.tile_end[0] : a.tile_end[1]);
+        W = m == 0 ? a.ws[0] : (m == 1 ? a.ws[1] : a.ws[2]);
+        Y = m == 0 ? a.ys[0] : (m == 1 ? a.ys[1] : a.ys[2]);
+    }
+    const int row0 = tile * TR, v0 = (int)blockIdx.y * TT;
     const int wr0 = (wave / NWT) * WR * 16, wt0 = (wave % NWT) * WT * 16;
-    const int rows = a.w.rows, bpr = a.bpr, spr = (bpr + 7) / 8;
+    const int rows = W.rows, bpr = a.bpr, spr = (bpr + 7) / 8;
     const int kq = lane >> 4, l16 = lane & 15;
     if constexpr (PAIR) {
         if (tid < 72) xq[TT * XP + tid] = 0u;
@@ -102,7 +117,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
         for (int i = 0; i < WN_ITEMS; i++) {
             const int it = tid + 256 * i, r = it >> 3, part = it & 7;
             const int gr = row0 + r < rows ? row0 + r : rows - 1;
-            const uint4 u = reinterpret_cast<const uint4*>(a.w.nib)[(size_t)gr * bpr + b0 + part];
+            const uint4 u = reinterpret_cast<const uint4*>(W.nib)[(size_t)gr * bpr + b0 + part];
             rw[i][0] = u.x; rw[i][1] = u.y; rw[i][2] = u.z; rw[i][3] = u.w;
         }
 #pragma unroll
@@ -117,8 +132,8 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
             const int it = tid + 256 * i;
             const int r = it / kGemmKC < TR ? it / kGemmKC : 0, blk = it % kGemmKC;
             const int gr = row0 + r < rows ? row0 + r : rows - 1;
-            rsub[i] = a.w.sub[(size_t)gr * bpr + b0 + blk];
-            rsup[i] = a.w.sup[(size_t)gr * spr + ((b0 + blk) >> 3)];
+            rsub[i] = W.sub[(size_t)gr * bpr + b0 + blk];
+            rsup[i] = W.sup[(size_t)gr * spr + ((b0 + blk) >> 3)];
         }
 #pragma unroll
         for (int i = 0; i < XS_ITEMS; i++) {
@@ -302,7 +317,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
             for (int i = 0; i < 4; i++) {
                 const int r = row0 + wr0 + rt * 16 + 4 * kq + i;
                 if (r >= rows) continue;
-                float* dst = a.y + (size_t)v * a.ldy + r;
+                float* dst = Y + (size_t)v * a.ldy + r;
                 *dst = a.epi == kEpiResAdd ? *dst + acc[rt][tt][i] : acc[rt][tt][i];
             }
         }
@@ -514,6 +529,9 @@ static void launch_gemv8(const GemmArgs& a, hipStream_t stream) {
     launch_gemv8_rt<NG, 1>(a, stream);
 }
 
+hipError_t launch_k4_gemm_w4a8_multi(const K4Mat* mats, float* const* ys, int nmat, int cols, const int8_t* qx,
+                                     const float* xs, int n, int ldy, GemvEpi epi, hipStream_t stream);
+
 // y[v][row] (+)= W x_v for n activation vectors already quantised (qx / xs as
 // quantize_vec writes them), on int8 MFMA.  Blocks per row a multiple of 8.
 hipError_t launch_k4_gemm_w4a8(const K4Mat& w, int cols, const int8_t* qx, const float* xs, int n, float* y, int ldy,
@@ -522,7 +540,7 @@ hipError_t launch_k4_gemm_w4a8(const K4Mat& w, int cols, const int8_t* qx, const
     if (!w.nib || !w.sub || !w.sup || w.rows <= 0 || cols != bpr * 32 || bpr % kGemmKC || !qx || !xs || !y ||
         n <= 0 || ldy < w.rows || (epi != kEpiStore && epi != kEpiResAdd))
         return hipErrorInvalidValue;
-    GemmArgs a;
+    GemmArgs a{};
     a.w = w;
     a.bpr = bpr;
     a.qx = qx;
@@ -555,9 +573,53 @@ hipError_t launch_k4_gemm_w4a8(const K4Mat& w, int cols, const int8_t* qx, const
         dim3 grid((w.rows + 127) / 128, 1);
         hipLaunchKernelGGL((k4_gemm_w4a8_mfma<2, 1, 4, 1, true>), grid, dim3(256), 0, stream, a);
     } else {
-        dim3 grid((w.rows + 63) / 64, (n + 63) / 64);
-        hipLaunchKernelGGL((k4_gemm_w4a8_mfma<2, 2, 2, 2, false>), grid, dim3(256), 0, stream, a);
+        return launch_k4_gemm_w4a8_multi(&w, &y, 1, cols, qx, xs, n, ldy, epi, stream);
     }
+    return hipGetLastError();
+}
+
+// The wide form for up to three matrices of the same width on one set of
+// activations (Q / K / V, gate / up), one launch: 64-row tiles, or 32-row ones
+// where 64-row tiles would leave the chip less than twice covered.
+hipError_t launch_k4_gemm_w4a8_multi(const K4Mat* mats, float* const* ys, int nmat, int cols, const int8_t* qx,
+                                     const float* xs, int n, int ldy, GemvEpi epi, hipStream_t stream) {
+    const int bpr = (cols + 31) / 32;
+    if (!mats || !ys || nmat < 1 || nmat > 3 || cols != bpr * 32 || bpr % kGemmKC || !qx || !xs || n <= 0 ||
+        (epi != kEpiStore && epi != kEpiResAdd))
+        return hipErrorInvalidValue;
+    int total64 = 0;
+    for (int m = 0; m < nmat; m++) {
+        if (!mats[m].nib || !mats[m].sub || !mats[m].sup || mats[m].rows <= 0 || !ys[m] || ldy < mats[m].rows)
+            return hipErrorInvalidValue;
+        total64 += (mats[m].rows + 63) / 64;
+    }
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int ncol = (n + 63) / 64;
+    const int TR = total64 * ncol < 2 * cus ? 32 : 64;
+    GemmArgs a{};
+    a.w = mats[0];
+    a.y = ys[0];
+    a.bpr = bpr;
+    a.qx = qx;
+    a.xs = xs;
+    a.n = n;
+    a.ldy = ldy;
+    a.epi = epi;
+    a.nmat = nmat;
+    int tiles = 0;
+    for (int m = 0; m < nmat; m++) {
+        a.ws[m] = mats[m];
+        a.ys[m] = ys[m];
+        tiles += (mats[m].rows + TR - 1) / TR;
+        a.tile_end[m] = tiles;
+    }
+    for (int m = nmat; m < 3; m++) a.tile_end[m] = tiles;
+    const dim3 grid(tiles, ncol);
+    if (TR == 32)
+        hipLaunchKernelGGL((k4_gemm_w4a8_mfma<1, 2, 2, 2, false>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((k4_gemm_w4a8_mfma<2, 2, 2, 2, false>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -60,6 +60,10 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
 // or += it (kEpiResAdd).  Bit-identical to launch_k4_gemv_w4a8 per vector.
 hipError_t launch_k4_gemm_w4a8(const K4Mat& w, int cols, const int8_t* qx, const float* xs, int n, float* y, int ldy,
                                GemvEpi epi, hipStream_t stream);
+// launch_k4_gemm_w4a8 for up to three matrices of one width on the same
+// activations in one launch (matrix m into ys[m], all with leading dimension ldy).
+hipError_t launch_k4_gemm_w4a8_multi(const K4Mat* mats, float* const* ys, int nmat, int cols, const int8_t* qx,
+                                     const float* xs, int n, int ldy, GemvEpi epi, hipStream_t stream);
 // Same arithmetic, but each workgroup quantises the fp32 activation x itself
 // (after Mantle's RMSNorm with norm_w when non-null): no separate quantiser
 // launch, and the weight loads are issued before the prologue runs.  With

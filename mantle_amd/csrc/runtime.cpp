@@ -889,9 +889,11 @@ static hipError_t prefill_rows(mantleHipModel* m, int R, hipStream_t s) {
         const auto& L = m->layers[l];
         // attention: RMSNorm + one int8 activation per row, Q / K / V
         TRY(launch_quantize_vec(p.x, L.attn_norm, c.eps, d, R, m->isa, p.qx, p.xs, nullptr, s));
-        TRY(launch_k4_gemm_w4a8(L.wq, d, p.qx, p.xs, R, p.qkv, qkvw, kEpiStore, s));
-        TRY(launch_k4_gemm_w4a8(L.wk, d, p.qx, p.xs, R, p.qkv + m->q_dim, qkvw, kEpiStore, s));
-        TRY(launch_k4_gemm_w4a8(L.wv, d, p.qx, p.xs, R, p.qkv + m->q_dim + m->kv_dim, qkvw, kEpiStore, s));
+        {
+            const K4Mat w3[3] = {L.wq, L.wk, L.wv};
+            float* y3[3] = {p.qkv, p.qkv + m->q_dim, p.qkv + m->q_dim + m->kv_dim};
+            TRY(launch_k4_gemm_w4a8_multi(w3, y3, 3, d, p.qx, p.xs, R, qkvw, kEpiStore, s));
+        }
         AttnArgs a{};
         a.q = p.qkv;
         a.k = p.qkv + m->q_dim;
@@ -956,8 +958,11 @@ static hipError_t prefill_rows(mantleHipModel* m, int R, hipStream_t s) {
         TRY(launch_k4_gemm_w4a8(L.wo, m->q_dim, p.attq, p.atts, R, p.x, d, kEpiResAdd, s));
         // FFN: RMSNorm + int8 activation, gate / up, SiLU(gate) * up re-quantised, down
         TRY(launch_quantize_vec(p.x, L.ffn_norm, c.eps, d, R, m->isa, p.qx, p.xs, nullptr, s));
-        TRY(launch_k4_gemm_w4a8(L.gate, d, p.qx, p.xs, R, p.gate, c.ffn, kEpiStore, s));
-        TRY(launch_k4_gemm_w4a8(L.up, d, p.qx, p.xs, R, p.up, c.ffn, kEpiStore, s));
+        {
+            const K4Mat w2[2] = {L.gate, L.up};
+            float* y2[2] = {p.gate, p.up};
+            TRY(launch_k4_gemm_w4a8_multi(w2, y2, 2, d, p.qx, p.xs, R, c.ffn, kEpiStore, s));
+        }
         TRY(launch_silu_mul(p.gate, p.up, p.gate, R * c.ffn, s));
         TRY(launch_quantize_vec(p.gate, nullptr, 0.0f, c.ffn, R, m->isa, p.qx, p.xs, nullptr, s));
         TRY(launch_k4_gemm_w4a8(L.down, c.ffn, p.qx, p.xs, R, p.x, d, kEpiResAdd, s));
