@@ -1668,13 +1668,57 @@ __global__ __launch_bounds__(kThreads) void attention_scores_rows(AttnArgs a, in
     }
 }
 
-// Softmax of (row blockIdx.y, head blockIdx.x) in place in the scores buffer
-// (head_softmax: max, exponentials, the ordered sum, x *= 1/sum).
-__global__ __launch_bounds__(kThreads) void attention_softmax_rows(AttnArgs a) {
-    __shared__ float red[8];
-    const int h = blockIdx.x, r = blockIdx.y;
+// Softmax of one (row, head) per wave, in place in the scores buffer:
+// head_softmax's values (max, fast_exp_scalar(x - max), the sum in key order,
+// x *= 1/sum).  The exponentials of each 1024-key chunk are also staged in the
+// wave's LDS, where lane 0 adds them in order (a dependent chain of adds from
+// LDS instead of from memory); four softmaxes per workgroup.
+static constexpr int kSoftmaxChunk = 1024;
+
+__global__ __launch_bounds__(kThreads) void attention_softmax_rows(AttnArgs a, int rows) {
+    __shared__ __align__(16) float buf[4][kSoftmaxChunk];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int i = (int)blockIdx.x * 4 + wave;
+    if (i >= rows * a.n_head) return;
+    const int r = i / a.n_head, h = i - r * a.n_head;
+    const int n = a.pos_host + r + 1;
     float* sg = a.scores + (size_t)r * a.scores_row + (size_t)h * a.max_ctx;
-    head_softmax<true>(sg, sg, red, a.pos_host + r);
+    float m = -INFINITY;
+    for (int t = lane; t < n; t += 64) m = fmaxf(m, sg[t]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float* b = buf[wave];
+    float sum = 0.0f;  // lane 0's running sum
+    for (int c0 = 0; c0 < n; c0 += kSoftmaxChunk) {
+        const int len = min(kSoftmaxChunk, n - c0);
+        for (int t = lane; t < len; t += 64) {
+            const float e = fast_exp_scalar(sg[c0 + t] - m);
+            sg[c0 + t] = e;
+            b[t] = e;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane == 0) {
+            int t = 0;
+            for (; t + 16 <= len; t += 16) {
+                float v[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) v[k] = b[t + k];
+#pragma unroll
+                for (int k = 0; k < 16; k++) sum += v[k];
+            }
+            for (; t < len; t++) sum += b[t];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    sum = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sum)));
+    if (sum != 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int t = lane; t < n; t += 64) sg[t] = sg[t] * inv;
+    }
 }
 
 // The V sum, transposed cache: workgroup (kv head g, block b of kPvRowsQ
@@ -1827,7 +1871,7 @@ static hipError_t launch_rows_batched(const AttnArgs& a, int rows, hipStream_t s
         {attention_pv_rows<128, kKvF32>, attention_pv_rows<128, kKvF16>, attention_pv_rows<128, kKvQ8>}};
     const size_t smem = sizeof(float) * ((size_t)kAttnKeys * (a.head_dim + 4) + (size_t)kRowsQ * a.head_dim);
     hipLaunchKernelGGL(sc[hd128][a.k_type], dim3(a.kv_heads, nchunks, nblk), dim3(kThreads), smem, stream, a, rows);
-    hipLaunchKernelGGL(attention_softmax_rows, dim3(a.n_head, rows), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(attention_softmax_rows, dim3((rows * a.n_head + 3) / 4), dim3(kThreads), 0, stream, a, rows);
     hipLaunchKernelGGL(pv[hd128][a.v_type], dim3(a.kv_heads, nblk_v), dim3(kThreads), 0, stream, a, rows);
     return hipGetLastError();
 }
