@@ -452,6 +452,11 @@ hipError_t launch_k4_gemv_w4a8(const K4Mat* mats, float* const* outs, int nmat, 
     p.qx = qx;
     p.xs = xs;
     p.key = argmax_key;
+    // batches of a tall matrix (the lm_head): the block dots on int8 matrix
+    // cores (bit-identical); the lane GEMV's DPP dot chains bound it there
+    if (batch >= 2 && nmat == 1 && (epi == kEpiStore || epi == kEpiResAdd) && p.bpr % 8 == 0 &&
+        mats[0].rows >= 16384 && ((uintptr_t)qx & 15) == 0)
+        return launch_k4_gemm_w4a8(mats[0], cols, qx, xs, batch, outs[0], mats[0].rows, epi, stream);
     bool used = false;
     hipError_t e = dispatch_lane_gemv(p, epi, stream, &used);
     if (used) return e;
