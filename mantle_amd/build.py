@@ -41,7 +41,10 @@ EXTRA = {
                       "-DMANTLE_F16_INPUT_FTZ=1"],
     # matrix-core results straight into VGPRs: the int32 dots are read by VALU
     # arithmetic at once, and AGPR results would cost a copy each
-    "gemm_w4a8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # f16 inputs flushed as in attention.hip: the weight super-scales decode
+    # through v_cvt_f32_f16 with Mantle's subnormal-to-zero
+    "gemm_w4a8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fdenormal-fp-math=preserve-sign", "-Xclang",
+                      "-fdenormal-fp-math-f32=ieee"],
 }
 
 

@@ -36,6 +36,7 @@
 // scales are all finite drops the skip test: a zero scale then gives a term of
 // +-0, which leaves the running sum unchanged, as the skip does.
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 #include <stdint.h>
 
 #include <type_traits>
@@ -66,6 +67,16 @@ struct GemmArgs {
 
 __device__ __forceinline__ float dpp_from_upper8(float v) {  // lane i <- lane i+8 within its row of 16
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true));
+}
+
+// k4_scale with the super-scale decoded by the hardware conversion: this file
+// is built with f16 denormals flushed, so a subnormal super becomes +-0 as
+// Mantle's decode makes it (NaN payloads may differ; NaN stays NaN).
+__device__ __forceinline__ float k4_scale_hw(uint16_t sup_bits, uint8_t sub) {
+    const float sup = __half2float(__ushort_as_half(sup_bits));
+    const uint32_t u6 = sub & 0x3Fu;
+    if (sup == 0.0f || u6 == 0) return 0.0f;
+    return sup * ((float)u6 * 0.03125f);
 }
 
 __device__ __forceinline__ bool finite_f(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
         for (int i = 0; i < SW_ITEMS; i++) {
             const int it = tid + 256 * i;
             if (TR * kGemmKC % 256 == 0 || it < TR * kGemmKC) {
-                const float s = k4_scale(rsup[i], (uint8_t)rsub[i]);
+                const float s = k4_scale_hw(rsup[i], (uint8_t)rsub[i]);
                 swT[(it % kGemmKC) * TR + it / kGemmKC] = s;
                 odd |= !finite_f(s);
             }
@@ -440,8 +451,8 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
             bool bad = false;
     #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
-                const float s0 = k4_scale((uint16_t)hbuf[slot][rt], (uint8_t)sbuf[slot][rt]);
-                const float s1 = k4_scale((uint16_t)hbuf[slot][rt], (uint8_t)(sbuf[slot][rt] >> 8));
+                const float s0 = k4_scale_hw((uint16_t)hbuf[slot][rt], (uint8_t)sbuf[slot][rt]);
+                const float s1 = k4_scale_hw((uint16_t)hbuf[slot][rt], (uint8_t)(sbuf[slot][rt] >> 8));
                 sww[rt * 128 + (2 * kq) * 16 + l16] = s0;
                 sww[rt * 128 + (2 * kq + 1) * 16 + l16] = s1;
                 bad |= !finite_f(s0) || !finite_f(s1);
