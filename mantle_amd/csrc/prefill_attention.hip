@@ -364,17 +364,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             const float m_new = fmaxf(m_run, mt * sl2t);
             float ls = 0.0f;
             f16x8 pb[2];
+            // V stored at a smaller scale than the output's: the probabilities
+            // enter the V sum times 2^vd (vf = 1 for vd = 0), the row sum without it
+            const float vf = ldexpf(1.0f, vd);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_new));
                 ls += pv;
-                pb[i >> 3][i & 7] = (_Float16)pv;
-            }
-            if (vd != 0) {  // wave-uniform: V stored at a smaller scale than the output's
-                const float vf = ldexpf(1.0f, vd);
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    pb[i >> 3][i & 7] = (_Float16)(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_new)) * vf);
+                pb[i >> 3][i & 7] = (_Float16)(pv * vf);
             }
             ls += __shfl_xor(ls, 32, 64);
             // rescale only when some query's running maximum moved (alpha = 1
