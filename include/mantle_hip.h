@@ -139,7 +139,10 @@ int mantleHipStoreKVF32Row(float* cache, const float* src, int cachePos, int kvS
  * keys start..pos, key t read from row t % cacheLen when 0 < cacheLen < pos + 1 (the
  * ring; else row t).  headDim 64 / 128 on the split attention paths.
  * f32 cache: the f32 twin of mantleCudaAttentionInnerF16CacheF32 (no reference counterpart:
- * Mantle's CUDA backend keeps f16 caches); scoresScratch: nHead*(pos-start+1) floats. */
+ * Mantle's CUDA backend keeps f16 caches); scoresScratch: nHead*(pos-start+1) floats.
+ * Under the one-launch attention path (mantleHipSetAttentionPath(FUSED), or past 32768 keys)
+ * the launch uses the library's per-device arrival counters: calls on one device must then
+ * be serialised on one stream (overlapping launches would corrupt each other's counts). */
 int mantleHipAttentionInnerF32Cache(const float* q, const float* cacheK, const float* cacheV, float* out,
                                     float* scoresScratch, int pos, int start, int kvStride, int headDim, int nHead,
                                     int kvHeads, int cacheLen, float scale, mantleHipStream_t stream);
@@ -173,7 +176,8 @@ int mantleHipStoreKVF16Row(uint16_t* cache, const float* src, int cachePos, int 
  * (ops.go:240-246, the scalar order), out_d = sum_t (p_t * v_t,d) * vScales[t] in key order.
  * Layout [pos][kvStride] int8 (kvStride a multiple of 16, 16-byte aligned rows), one scale
  * per position; scoresScratch, start and cacheLen as in mantleHipAttentionInnerF32Cache;
- * positions up to 32768.  Split attention paths only (both take the two-launch form). */
+ * positions up to 32768.  Split attention paths only (both take the two-launch form, which
+ * uses no shared counters; overlapping calls need scoresScratch of their own). */
 int mantleHipAttentionInnerQ8CacheF32(const float* q, const int8_t* cacheK, const int8_t* cacheV,
                                       const float* kScales, const float* vScales, float* out, float* scoresScratch,
                                       int pos, int start, int kvStride, int headDim, int nHead, int kvHeads,
