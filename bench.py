@@ -396,6 +396,9 @@ def main():
     ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV microbench")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill attention microbench")
     ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill microbench (for rocprofv3)")
+    ap.add_argument("--prompt-prefill-only", action="store_true",
+                    help="only the batched prompt prefill of the config-1 model (for rocprofv3)")
+    ap.add_argument("--gemv-batch", type=int, default=1, help="--gemv-only: the batch of the logits-shape GEMV")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the lm_head GEMV microbench and a copy calibration (for rocprofv3 --pmc runs)")
     ap.add_argument("--model", default="qwen3-0.6b", choices=["qwen3-0.6b", *LARGE_MODELS],
@@ -427,7 +430,7 @@ def main():
         return
 
     if args.gemv_only:
-        g = gemv_microbench([(151936, 1024)], [1], iters=50)[0]
+        g = gemv_microbench([(151936, 1024)], [args.gemv_batch], iters=50, modes=("w4a8",))[0]
         copy_calibration()
         print(json.dumps({"gemv": g}), flush=True)
         return
@@ -437,6 +440,9 @@ def main():
     t0 = time.perf_counter()
     mcf.pack_cached(path, 0, QWEN3_0_6B)
     log(f"model ready in {time.perf_counter() - t0:.1f} s: {path}")
+    if args.prompt_prefill_only:
+        print(json.dumps({"prompt_prefill": prompt_prefill_bench(path)}), flush=True)
+        return
     prompt = mcf.uniform_tokens(PROMPT_LEN, QWEN3_0_6B["vocab"], 1)
     max_ctx = PROMPT_LEN + args.warmup + args.steps + 8
     rt = mantle_amd.new_backend("hip").load_model(path, max_context=max_ctx)
