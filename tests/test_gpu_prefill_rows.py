@@ -52,8 +52,9 @@ def _run(path, ctx, prompt, steps, env, **kw):
 
 @pytest.mark.parametrize("kt,vt", [("f32", "f32"), ("f16", "f16"), ("q8_0", "q8_0"), ("f32", "q8_0"),
                                    ("q8_0", "f16")])
-@pytest.mark.parametrize("n,ctx", [(37, 96), (300, 650)])
+@pytest.mark.parametrize("n,ctx", [(37, 96), (300, 650), (300, 32768)])
 def test_prefill_rows_match_steps(hip, lane_path, kt, vt, n, ctx):
+    """(300, 32768): the scores of 32768-key rows cap a pass at 256 rows, so the prompt takes two passes."""
     print(f"prefill rows kv {kt}/{vt} n={n} ctx={ctx}", flush=True)
     prompt = models.prompt(n, models.LANE["vocab"], 21 + n)
     rows = _run(lane_path, ctx, prompt, 6, None, kv_cache_k=kt, kv_cache_v=vt)
