@@ -275,6 +275,39 @@ def cpu_baseline(path, cfg, prompt, steps=128, steps_1t=8):
                        f"reduction order (host dispatch would pick {hc['isa']}), {hc['model']}")
 
 
+def cpu_gemv_baseline(shapes=((151936, 1024), (3072, 1024), (1024, 3072), (2048, 1024)), threads=None,
+                      rotate_bytes=1 << 30, min_s=1.0):
+    """Config 2 on the host: the oracle's W4A8 GEMV (MatVecWithQuant: the activation's
+    int8 quantisation and the ordered block sums) at batch 1 on every usable core,
+    the same weights (seed 2) and x ~ N(0,1); weight copies rotated over >= 1 GiB so
+    the last-level cache cannot serve them; GB/s of algorithmic bytes."""
+    import numpy as np
+
+    from mantle_amd import mcf
+    from oracle import oracle as o
+
+    threads = threads or host_cpu()["usable"]
+    o.set_threads(threads)
+    out = []
+    for rows, cols in shapes:
+        payload = mcf.quantize_k4(mcf.fill_normal(rows * cols, 2 + rows).reshape(rows, cols))
+        copies = max(2, -(-rotate_bytes // payload.nbytes))
+        bufs = [payload] + [payload.copy() for _ in range(copies - 1)]
+        x = np.random.default_rng(2).standard_normal(cols).astype(np.float32)
+        o.matvec_w4a8(bufs[0], rows, cols, x)
+        n, t0 = 0, time.perf_counter()
+        while n < copies or time.perf_counter() - t0 < min_s:
+            o.matvec_w4a8(bufs[n % copies], rows, cols, x)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        algo = mcf.payload_size(rows, cols) + 4 * cols + 4 * rows
+        out.append(dict(rows=rows, cols=cols, batch=1, avg_us=round(dt * 1e6, 1), gbs=round(algo / dt / 1e9, 2),
+                        threads=threads, launches=n))
+        log(f"cpu gemv w4a8 {rows}x{cols}: {dt * 1e3:.2f} ms, {algo / dt / 1e9:.2f} GB/s on {threads} threads")
+        del bufs
+    return out
+
+
 def weight_bytes_per_token(cfg):
     """Weight bytes one decode token streams: every block matrix plus the lm_head
     (the tied embedding when tie_embeddings), norms as fp32; k4 payloads, or 2
@@ -473,6 +506,7 @@ def main():
     if not args.no_cpu:
         try:
             cpu = cpu_baseline(path, QWEN3_0_6B, prompt)
+            cpu["gemv"] = cpu_gemv_baseline()
             log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} threads, "
                 f"{cpu['value_1thread']:.3f} tok/s on 1 ({cpu['cpu_model']})")
         except Exception as e:  # the baseline is reported, never required
