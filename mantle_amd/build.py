@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmantle_hip.so")
 TRACE_LIB = os.path.join(HERE, "libmantle_hip_trace.so")
 OBJ_DIR = os.path.join(HERE, "_build")
-SOURCES = ["gemv_lane_store.hip", "gemv_lane_fused.hip", "gemv_lane_b8.hip", "gemv_w4a32.hip", "gemm_w4a8.hip", "gemv_bf16.hip", "attention.hip", "prefill_attention.hip", "kernels.hip", "runtime.cpp", "capi.cpp",
+SOURCES = ["gemv_lane_store.hip", "gemv_lane_fused.hip", "gemv_lane_b8.hip", "gemv_w4a32.hip", "gemm_w4a8.hip", "gemm_w4a32.hip", "gemv_bf16.hip", "attention.hip", "prefill_attention.hip", "kernels.hip", "runtime.cpp", "capi.cpp",
            "mcf.cpp"]
 ARCH = os.environ.get("MANTLE_HIP_ARCH", "gfx950")
 
@@ -41,6 +41,7 @@ EXTRA = {
                       "-DMANTLE_F16_INPUT_FTZ=1"],
     # matrix-core results straight into VGPRs: the int32 dots are read by VALU
     # arithmetic at once, and AGPR results would cost a copy each
+    "gemm_w4a32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     # f16 inputs flushed as in attention.hip: the weight super-scales decode
     # through v_cvt_f32_f16 with Mantle's subnormal-to-zero
     "gemm_w4a8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fdenormal-fp-math=preserve-sign", "-Xclang",

@@ -122,6 +122,8 @@ hipError_t lane_gemv_store(GemvParams& p, int pro, hipStream_t stream, bool* use
 hipError_t lane_gemv_fused(GemvParams& p, GemvEpi epi, int pro, hipStream_t stream, bool* used); // gemv_lane_fused.hip
 hipError_t lane_gemv_batch8(GemvParams& p, int pro, hipStream_t stream, bool* used);             // gemv_lane_b8.hip
 // W4A32 with one lane per row (gemv_w4a32.hip); *used false when x does not fit LDS.
+hipError_t k4_gemv_w4a32_mfma_launch(const K4Mat& m, int cols, const float* x, float* y, int batch,
+                                     hipStream_t stream, bool* used);  // gemm_w4a32.hip
 hipError_t k4_gemv_w4a32_lane(const K4Mat& m, int cols, const float* x, float* y, int batch, hipStream_t stream,
                               bool* used);
 

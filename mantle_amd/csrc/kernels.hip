@@ -578,7 +578,11 @@ hipError_t launch_k4_gemv_w4a32(const K4Mat& m, int cols, const float* x, float*
     p.x = x;
     if (!lane_gemv_disabled()) {
         bool used = false;
-        hipError_t e = k4_gemv_w4a32_lane(m, cols, x, y, batch, stream, &used);
+        hipError_t e = hipSuccess;
+        // batches: the block dots on f16 matrix cores (x as two f16 parts)
+        if (batch >= 2 && !getenv("MANTLE_HIP_W4A32_LANE")) e = k4_gemv_w4a32_mfma_launch(m, cols, x, y, batch, stream, &used);
+        if (used) return e;
+        e = k4_gemv_w4a32_lane(m, cols, x, y, batch, stream, &used);
         if (used) return e;
     }
     return launch_gemv<kModeW4A32>(p, kEpiStore, stream);
