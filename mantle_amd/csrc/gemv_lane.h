@@ -520,7 +520,13 @@ static hipError_t launch_lane_gemv_sized(GemvParams& p, hipStream_t stream) {
     // (16-lane rows make 16-row units at four waves: the quantising SiLU
     // epilogue takes the eight-wave instance below)
     if (large && (L8 || !q32)) {
-        if constexpr (L8) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 1>(p, stream);
+        if constexpr (L8) {
+            // with the RMSNorm prologue (the decode step's logits): resident
+            // workgroups streaming several units each, so each runs the
+            // prologue once (0.6B decode 1205 -> 1207 tok/s)
+            if (PRO == kProNorm) return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 2>(p, stream);
+            return launch_lane_gemv<EPI, 8, BPR / 8, NB, 4, PRO, 1>(p, stream);
+        }
         else if constexpr (C16 == T16) return launch_lane_gemv<EPI, 16, T16, NB, 4, PRO, 1>(p, stream);
         else return launch_lane_gemv<EPI, 16, C16, NB, 4, PRO, 2, T16>(p, stream);
     }
