@@ -108,3 +108,18 @@ def test_prefill_rows_gqa4_wide_rows(hip, tmp_models):
     steps = _run(path, 128, prompt, 3, "steps")
     for i, (a, b) in enumerate(zip(rows, steps)):
         np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"output {i}")
+
+
+HD64 = dict(n_layers=2, d_model=512, n_heads=8, n_kv_heads=4, head_dim=64, ffn=1024, vocab=1000,
+            rope_base=1e6, eps=1e-6, tie_embeddings=1)
+
+
+@pytest.mark.parametrize("kt,vt", [("f32", "f32"), ("f16", "q8_0")])
+def test_prefill_rows_head_dim_64(hip, tmp_models, kt, vt):
+    """head_dim 64 (one column wave per head in the V sum): rows equal the per-token steps."""
+    path = models.pack(str(tmp_models / "hd64_rows.mcf"), 2, HD64)
+    prompt = models.prompt(90, HD64["vocab"], 6)
+    rows = _run(path, 160, prompt, 4, None, kv_cache_k=kt, kv_cache_v=vt)
+    steps = _run(path, 160, prompt, 4, "steps", kv_cache_k=kt, kv_cache_v=vt)
+    for i, (a, b) in enumerate(zip(rows, steps)):
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=f"output {i}")
