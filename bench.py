@@ -163,7 +163,7 @@ def prefill_microbench(seqs=(512, 2048, 8192), nh=16, kvh=8, hd=128, reps=20):
         o = torch.empty(S * nh * hd, device="cuda:0")
         scale = ctypes.c_float(1.0 / np.sqrt(hd))
         nws = ctypes.c_size_t()
-        _lib.call("mantleHipAttentionPrefillWorkspaceSize", S, kvh, hd, ctypes.byref(nws))
+        _lib.call("mantleHipAttentionPrefillWorkspaceSize", S, nh, kvh, hd, ctypes.byref(nws))
         ws = torch.empty(nws.value, dtype=torch.uint8, device="cuda:0")
 
         def attn():

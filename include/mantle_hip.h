@@ -211,7 +211,7 @@ int mantleHipGetKVCacheType(void);
 int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ropeCos,
                                   const float* ropeSin, float* out, int seqLen, int nHead, int kvHeads, int headDim,
                                   float scale, void* workspace, size_t workspaceBytes, mantleHipStream_t stream);
-int mantleHipAttentionPrefillWorkspaceSize(int seqLen, int kvHeads, int headDim, size_t* bytes);
+int mantleHipAttentionPrefillWorkspaceSize(int seqLen, int nHead, int kvHeads, int headDim, size_t* bytes);
 /* Replaces mantleCudaSoftmaxRowsF32 (softmax.h:13), with Mantle's CPU fastExp / ordered sum. */
 int mantleHipSoftmaxRowsF32(float* data, int rows, int cols, mantleHipStream_t stream);
 /* Replaces mantleCudaSiluMulF32 (softmax.h:59-64), CPU fastSiluVec arithmetic. */

@@ -73,7 +73,7 @@ _SIGS = {
     "mantleHipStoreKVF32Row": (I, [P, P, I, I, P]),
     "mantleHipAttentionInnerF32Cache": (I, [P, P, P, P, P, I, I, I, I, I, I, I, F, P]),
     "mantleHipAttentionPrefillBF16": (I, [P, P, P, P, P, P, I, I, I, I, F, P, C.c_size_t, P]),
-    "mantleHipAttentionPrefillWorkspaceSize": (I, [I, I, I, C.POINTER(C.c_size_t)]),
+    "mantleHipAttentionPrefillWorkspaceSize": (I, [I, I, I, I, C.POINTER(C.c_size_t)]),
     "mantleHipSoftmaxRowsF32": (I, [P, I, I, P]),
     "mantleHipSiluMulF32": (I, [P, P, P, I, P]),
     "mantleHipAddVectorsF32": (I, [P, P, I, P]),

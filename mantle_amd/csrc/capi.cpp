@@ -302,9 +302,10 @@ int mantleHipAttentionPrefillBF16(const uint16_t* q, const uint16_t* k, const ui
                                          workspace, workspaceBytes, S(stream));
 }
 
-int mantleHipAttentionPrefillWorkspaceSize(int seqLen, int kvHeads, int headDim, size_t* bytes) {
-    if (!bytes || seqLen <= 0 || kvHeads <= 0 || headDim != 128) return hipErrorInvalidValue;
-    *bytes = attention_prefill_workspace(seqLen, kvHeads);
+int mantleHipAttentionPrefillWorkspaceSize(int seqLen, int nHead, int kvHeads, int headDim, size_t* bytes) {
+    if (!bytes || seqLen <= 0 || nHead <= 0 || kvHeads <= 0 || nHead % kvHeads || headDim != 128)
+        return hipErrorInvalidValue;
+    *bytes = attention_prefill_workspace(seqLen, nHead, kvHeads);
     return hipSuccess;
 }
 

@@ -174,12 +174,12 @@ bool set_attention_path(int path);
 // Causal GQA attention over a whole prompt on bf16 MFMA (head_dim 128): q bf16
 // [seq][n_head][128], k / v bf16 [seq][kv_heads][128], optional RoPE tables
 // [seq][64] applied to q and k, out fp32 [seq][n_head][128].
-// workspace: attention_prefill_workspace(seq, kv_heads) bytes, 16-byte aligned.
+// workspace: attention_prefill_workspace(seq, n_head, kv_heads) bytes, 16-byte aligned.
 hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                          const float* rope_cos, const float* rope_sin, float* out, int seq,
                                          int n_head, int kv_heads, int head_dim, float scale, void* workspace,
                                          size_t workspace_bytes, hipStream_t stream);
-size_t attention_prefill_workspace(int seq, int kv_heads);
+size_t attention_prefill_workspace(int seq, int n_head, int kv_heads);
 
 hipError_t launch_embed(const K4Mat& emb, int cols, const int* prompt, DecodeState* st, float* x,
                         hipStream_t stream);

@@ -41,6 +41,8 @@
 //    V in fp16 transposed [kv][128][seq] into the caller's workspace once, so
 //    the attention workgroups (seq/64 of them per KV group) stage plain copies.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <math.h>
 #include <stdint.h>
 
@@ -100,7 +102,25 @@ struct PrefillArgs {
     int q_block;       // queries per workgroup and head
     int n_qblocks;
     float scale;
+    // Load balance: a query block of more than t_max key tiles is split into
+    // ceil(tiles / t_max) parts (at most kPfMaxParts) of even size, so no
+    // workgroup's chain of tiles is much longer than the average one.  A split
+    // block leaves each part's unnormalised O^T, running max (log2 units) and
+    // sum in opart [seq][n_head][kPfMaxParts][128] / mlpart [seq][n_head][kPfMaxParts][2];
+    // prefill_combine_parts joins them.
+    int t_max;
+    float *opart, *mlpart;
 };
+
+static constexpr int kPfMaxParts = 4;
+
+__device__ __forceinline__ int pf_tiles(const PrefillArgs& a, int qb) {
+    return (min((qb + 1) * a.q_block, a.seq) + kPfKeys - 1) / kPfKeys;
+}
+__device__ __forceinline__ int pf_parts(const PrefillArgs& a, int qb) {
+    const int p = (pf_tiles(a, qb) + a.t_max - 1) / a.t_max;
+    return p < kPfMaxParts ? p : kPfMaxParts;
+}
 
 // The staging registers of one K/V tile (this thread's share: 32 bytes of each).
 struct TileRegs {
@@ -219,9 +239,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
     const int h2 = lane >> 5, l32 = lane & 31;
     const int wph = 4 / a.heads_per_wg;  // waves per head
     const int groups = a.n_head / a.heads_per_wg;
-    // the longest query blocks (most keys) are dispatched first
-    const int qb = a.n_qblocks - 1 - (int)blockIdx.x / groups;
-    const int hg = (int)blockIdx.x % groups;
+    // the longest query blocks (most keys) are dispatched first; block qb has
+    // pf_parts(qb) parts per head group
+    int qb = a.n_qblocks - 1, rest = (int)blockIdx.x, nparts = pf_parts(a, qb);
+    while (rest >= nparts * groups) {
+        rest -= nparts * groups;
+        qb--;
+        nparts = pf_parts(a, qb);
+    }
+    const int hg = rest / nparts, part = rest - hg * nparts;
     const int head = hg * a.heads_per_wg + wave / wph;
     const int kvh = head * a.kv_heads / a.n_head;
     const int q0 = qb * a.q_block;
@@ -324,14 +350,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
         __syncthreads();
         vmax = max(max(vred[0], vred[1]), max(vred[2], vred[3]));
     }
+    const int per_part = (ntiles + nparts - 1) / nparts;
+    const int it0 = part * per_part, it1 = min(ntiles, it0 + per_part);
     TileRegs tr;
-    load_tile(tr, 0);
+    load_tile(tr, it0 * kPfKeys);
     store_tile(tr, 0);
     __syncthreads();
-    for (int it = 0; it < ntiles; it++) {
-        const int buf = it & 1;
+    for (int it = it0; it < it1; it++) {
+        const int buf = (it - it0) & 1;
         const int t0 = it * kPfKeys;
-        if (it + 1 < ntiles) load_tile(tr, t0 + kPfKeys);
+        if (it + 1 < it1) load_tile(tr, t0 + kPfKeys);
         if (t0 <= qw + 31) {  // some key of the tile is visible to some query of this wave
             const float sl2t = sl2 * kfac[it];  // the tile's K factor
             const int vd = vexp[it] - vmax;     // its V factor relative to the output's
@@ -362,6 +390,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
             const float m_new = fmaxf(m_run, mt * sl2t);
+            // a query with no visible key yet (a later part of a split block):
+            // exponentials against 0 keep its all -inf scores at 0 instead of NaN
+            const float m_exp = m_new == -INFINITY ? 0.0f : m_new;
             float ls = 0.0f;
             f16x8 pb[2];
             // V stored at a smaller scale than the output's: the probabilities
@@ -369,7 +400,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             const float vf = ldexpf(1.0f, vd);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_new));
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_exp));
                 ls += pv;
                 pb[i >> 3][i & 7] = (_Float16)(pv * vf);
             }
@@ -377,7 +408,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             // rescale only when some query's running maximum moved (alpha = 1
             // exactly otherwise: the 64 multiplies would change nothing)
             if (__any(m_new != m_run)) {
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_exp);  // 0 while m_run is -inf
                 l_run = l_run * alpha;
 #pragma unroll
                 for (int t = 0; t < 4; t++)
@@ -402,10 +433,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             }
         }
         // the other buffer's last readers finished before the previous barrier
-        if (it + 1 < ntiles) store_tile(tr, buf ^ 1);
+        if (it + 1 < it1) store_tile(tr, buf ^ 1);
         __syncthreads();
     }
 
+    if (nparts > 1) {  // a part of a split block: its partial result
+        if (myq < a.seq) {
+            const size_t slot = ((size_t)myq * a.n_head + head) * kPfMaxParts + part;
+            float* orow = a.opart + slot * kPfHd;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    f32x4v r;
+                    r.x = o[t][4 * g];
+                    r.y = o[t][4 * g + 1];
+                    r.z = o[t][4 * g + 2];
+                    r.w = o[t][4 * g + 3];
+                    *reinterpret_cast<f32x4v*>(orow + 32 * t + 8 * g + 4 * h2) = r;
+                }
+            if (h2 == 0) {
+                a.mlpart[2 * slot] = m_run;
+                a.mlpart[2 * slot + 1] = l_run;
+            }
+        }
+        return;
+    }
     // ---- out[myq][head][hd] = O^T[hd][myq] / l
     if (myq < a.seq) {
         const float inv = ldexpf(1.0f / l_run, vmax);
@@ -424,9 +477,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
     }
 }
 
-size_t attention_prefill_workspace(int seq, int kv_heads) {
+// The parts of a split query block joined: M = max_p m_p, l = sum_p l_p 2^(m_p - M),
+// O = sum_p O_p 2^(m_p - M) (a part that saw no key: m = -inf, l = 0, O = 0),
+// out = O / l * 2^vmax (vmax: the block's largest V tile exponent, as every part
+// used).  One wave per (query, head) of a split block, lane = two columns.
+__global__ __launch_bounds__(256) void prefill_combine_parts(PrefillArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int idx = (int)blockIdx.x * 4 + wave;
+    if (idx >= a.seq * a.n_head) return;
+    const int q = idx / a.n_head, head = idx - q * a.n_head;
+    const int qb = q / a.q_block;
+    const int nparts = pf_parts(a, qb);
+    if (nparts <= 1) return;  // written whole by its workgroup
+    const int kvh = head * a.kv_heads / a.n_head;
+    const int ntiles = pf_tiles(a, qb);
+    const int* vexp = a.vexp + (size_t)kvh * (a.seq_pad / kPfKeys);
+    int vmax = -1000;
+    for (int i = lane; i < ntiles; i += 64) vmax = max(vmax, vexp[i]);
+    for (int off = 32; off > 0; off >>= 1) vmax = max(vmax, __shfl_xor(vmax, off, 64));
+    const size_t slot0 = ((size_t)q * a.n_head + head) * kPfMaxParts;
+    float M = -INFINITY;
+    for (int p = 0; p < nparts; p++) M = fmaxf(M, a.mlpart[2 * (slot0 + p)]);
+    float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int p = 0; p < nparts; p++) {
+        const float mp = a.mlpart[2 * (slot0 + p)];
+        if (mp == -INFINITY) continue;
+        const float al = __builtin_amdgcn_exp2f(mp - M);
+        l += a.mlpart[2 * (slot0 + p) + 1] * al;
+        const float* orow = a.opart + (slot0 + p) * kPfHd;
+        o0 += orow[lane] * al;
+        o1 += orow[lane + 64] * al;
+    }
+    const float inv = ldexpf(1.0f / l, vmax);
+    float* out = a.out + ((size_t)q * a.n_head + head) * kPfHd;
+    out[lane] = o0 * inv;
+    out[lane + 64] = o1 * inv;
+}
+
+static size_t prefill_base_bytes(int seq, int kv_heads) {
     const size_t seq_pad = (size_t)(seq + kPfKeys - 1) / kPfKeys * kPfKeys;
-    return (size_t)kv_heads * seq_pad * kPfHd * 2 * sizeof(uint16_t) + (size_t)kv_heads * (seq_pad / kPfKeys) * 8;
+    const size_t b = (size_t)kv_heads * seq_pad * kPfHd * 2 * sizeof(uint16_t) + (size_t)kv_heads * (seq_pad / kPfKeys) * 8;
+    return (b + 255) / 256 * 256;
+}
+
+size_t attention_prefill_workspace(int seq, int n_head, int kv_heads) {
+    return prefill_base_bytes(seq, kv_heads) + (size_t)seq * n_head * kPfMaxParts * (kPfHd + 2) * sizeof(float);
 }
 
 hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -439,7 +534,7 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)workspace) & 15) ||
         (rope_cos && (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15)))
         return hipErrorInvalidValue;
-    if (workspace_bytes < attention_prefill_workspace(seq, kv_heads)) return hipErrorInvalidValue;
+    if (workspace_bytes < attention_prefill_workspace(seq, n_head, kv_heads)) return hipErrorInvalidValue;
     PrefillArgs a;
     a.q = q;
     a.k = k;
@@ -459,11 +554,36 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     a.q_block = 32 * (4 / a.heads_per_wg);
     a.n_qblocks = (seq + a.q_block - 1) / a.q_block;
     a.scale = scale;
-    const long long grid = (long long)a.n_qblocks * (n_head / a.heads_per_wg);
+    // t_max: about the tiles one of the 3 x CUs resident workgroups gets on
+    // average (never fewer than 16), so the longest chain is near the mean
+    const int groups = n_head / a.heads_per_wg;
+    long long work = 0;
+    for (int qb = 0; qb < a.n_qblocks; qb++)
+        work += (long long)((std::min((qb + 1) * a.q_block, seq) + kPfKeys - 1) / kPfKeys) * groups;
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const long long avg = (work + 3LL * cus - 1) / (3LL * cus);
+    // only where the whole blocks leave CUs idle (S = 8192 measured 442 -> 450 us
+    // with the split, S = 2048 93 -> 51 us + 18 us of combine)
+    const bool fills = (long long)a.n_qblocks * groups >= 3LL * cus;
+    a.t_max = fills ? 0x3FFFFFFF : (int)std::max<long long>(4, avg);
+    a.opart = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_base_bytes(seq, kv_heads));
+    a.mlpart = a.opart + (size_t)seq * n_head * kPfMaxParts * kPfHd;
+    long long grid = 0;
+    bool split = false;
+    for (int qb = 0; qb < a.n_qblocks; qb++) {
+        const int tiles = (std::min((qb + 1) * a.q_block, seq) + kPfKeys - 1) / kPfKeys;
+        const int parts = std::min(kPfMaxParts, (tiles + a.t_max - 1) / a.t_max);
+        grid += (long long)parts * groups;
+        split |= parts > 1;
+    }
     const long long prep = (long long)kv_heads * (a.seq_pad / kPfKeys);
     if (grid > 0x7FFFFFFF || prep > 0x7FFFFFFF) return hipErrorInvalidValue;
     hipLaunchKernelGGL(prefill_prep_kv, dim3((unsigned)prep), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(attention_prefill_bf16, dim3((unsigned)grid), dim3(256), 0, stream, a);
+    if (split)
+        hipLaunchKernelGGL(prefill_combine_parts, dim3((unsigned)(((long long)seq * n_head + 3) / 4)), dim3(256), 0,
+                           stream, a);
     return hipGetLastError();
 }
 

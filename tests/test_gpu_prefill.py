@@ -42,9 +42,9 @@ def rope_tables(oracle, seq):
     return (np.stack([c for c, _ in cs]).astype(np.float32), np.stack([s for _, s in cs]).astype(np.float32))
 
 
-def workspace(seq, kvh):
+def workspace(seq, nh, kvh):
     n = ctypes.c_size_t()
-    g.call("mantleHipAttentionPrefillWorkspaceSize", seq, kvh, HD, ctypes.byref(n))
+    g.call("mantleHipAttentionPrefillWorkspaceSize", seq, nh, kvh, HD, ctypes.byref(n))
     return g.empty(n.value, dtype=torch.uint8), n.value
 
 
@@ -53,7 +53,7 @@ def run_gpu(bits, cos, sin, seq, nh, kvh, scale):
     out = g.empty(seq * nh * HD)
     cp = g.ptr(g.keep(cos)) if cos is not None else None
     sp = g.ptr(g.keep(sin)) if sin is not None else None
-    ws, nws = workspace(seq, kvh)
+    ws, nws = workspace(seq, nh, kvh)
     g.call("mantleHipAttentionPrefillBF16", g.ptr(qb), g.ptr(kb), g.ptr(vb), cp, sp, g.ptr(out), seq, nh, kvh, HD,
            ctypes.c_float(scale), g.ptr(ws), nws, g.stream())
     return g.host(out).reshape(seq, nh * HD)
