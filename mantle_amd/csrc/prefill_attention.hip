@@ -59,8 +59,6 @@ typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 
 static constexpr int kPfHd = 128;             // head_dim
 static constexpr int kPfKeys = 32;            // keys per tile
-static constexpr int kPfKPitch = kPfHd + 8;   // fp16 per staged K row (16-byte rows, 4-bank skew)
-static constexpr int kPfVPitch = kPfKeys + 4; // fp16 per staged V^T row (conflict-free 8-byte reads)
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -93,10 +91,11 @@ struct PrefillArgs {
     const float* rope_cos;  // [seq][64] or null (no RoPE)
     const float* rope_sin;
     float* out;  // fp32 [seq][n_head][128]
-    uint16_t* kr;  // workspace: fp16 RoPE'd K [kv_heads][seq_pad][128]
-    uint16_t* vtr;  // workspace: fp16 V^T [kv_heads][128][seq_pad]
-    float* kfac;    // workspace: [kv_heads][seq_pad/32] the K tile's power-of-two factor (stored K = K * 2^-e)
-    int* vexp;      // workspace: [kv_heads][seq_pad/32] the V tile's exponent e (stored V = V * 2^-e)
+    // workspace, per kv head and 32-key tile (8 KB blocks laid out as the
+    // attention's LDS tiles, so a tile is staged by plain 1 KB copies):
+    uint16_t* kt;   // fp16 RoPE'd K: [kv][tile][16-byte chunk c of hd][key][8]
+    uint16_t* vt;   // fp16 V: [kv][tile][key quad][hd][4]
+    uint32_t* kfv;  // [kv][tile][2]: the K tile's power-of-two factor (float bits; stored K = K * 2^-e), the V tile's exponent e
     int seq, seq_pad, n_head, kv_heads;
     int heads_per_wg;  // 2 (GQA groups of an even size) or 1
     int q_block;       // queries per workgroup and head
@@ -122,11 +121,17 @@ __device__ __forceinline__ int pf_parts(const PrefillArgs& a, int qb) {
     return p < kPfMaxParts ? p : kPfMaxParts;
 }
 
-// The staging registers of one K/V tile (this thread's share: 32 bytes of each).
-struct TileRegs {
-    u32x4v k0, k1;  // K row tid/8, hd 16*(tid%8) .. +16
-    u32x4v v0, v1;  // V^T row tid/2, keys 16*(tid%2) .. +16
-};
+
+// op(x of lane l, x of lane l ^ 32) in every lane, the two operands in the
+// same order in both lanes (v_permlane32_swap: no LDS round trip).
+__device__ __forceinline__ float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // The power of two 2^e that brings a block whose max |x| is m into
 // [2^14, 2^15] (fp16-safe after rounding, clear of fp16's subnormals): e = E -
@@ -149,9 +154,10 @@ __device__ __forceinline__ float wg_max256(float v, float* red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// Pre-pass: workgroup (kv head g, keys t0..t0+31) writes K RoPE'd in fp16 and
-// V transposed in fp16 (through LDS), zeros for keys past seq, each scaled by
-// the tile's power of two into fp16 range (factors in kfac / vexp).
+// Pre-pass: workgroup (kv head g, keys t0..t0+31) writes the tile's K RoPE'd
+// and its V (through LDS) in fp16 in the attention's tile layouts, zeros for
+// keys past seq, each scaled by the tile's power of two into fp16 range
+// (factors in kfv).
 __global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
     __shared__ __align__(16) uint16_t vs[kPfHd * 40];
     __shared__ float red[8];
@@ -192,8 +198,8 @@ __global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
     const int ek = range_exp(wg_max256(km, red));
     const int ev = range_exp(wg_max256(vm, red + 4));
     if (tid == 0) {
-        a.kfac[g * nkb + tile] = ldexpf(1.0f, ek);
-        a.vexp[g * nkb + tile] = ev;
+        a.kfv[2 * ((size_t)g * nkb + tile)] = __float_as_uint(ldexpf(1.0f, ek));
+        a.kfv[2 * ((size_t)g * nkb + tile) + 1] = (uint32_t)ev;
     }
     {
         const float f = ldexpf(1.0f, -ek);
@@ -211,21 +217,23 @@ __global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
         w0.z = pack_f16(x0[4], x0[5]); w0.w = pack_f16(x0[6], x0[7]);
         w1.x = pack_f16(x1[0], x1[1]); w1.y = pack_f16(x1[2], x1[3]);
         w1.z = pack_f16(x1[4], x1[5]); w1.w = pack_f16(x1[6], x1[7]);
-        uint16_t* dst = a.kr + ((size_t)g * a.seq_pad + t) * kPfHd;
-        *reinterpret_cast<u32x4v*>(dst + 8 * kc) = w0;
-        *reinterpret_cast<u32x4v*>(dst + 64 + 8 * kc) = w1;
+        // chunk c of key kk at c * 512 + kk * 16 bytes
+        uint16_t* dst = a.kt + ((size_t)g * nkb + tile) * (kPfKeys * kPfHd) + kk * 8;
+        *reinterpret_cast<u32x4v*>(dst + 256 * kc) = w0;
+        *reinterpret_cast<u32x4v*>(dst + 256 * (8 + kc)) = w1;
     }
 #pragma unroll
     for (int j = 0; j < 8; j++)
         *reinterpret_cast<uint32_t*>(&vs[(8 * vc + j) * 40 + 2 * vp]) = pack_f16(e0[j], e1[j]);
     __syncthreads();
-    {  // V^T row hd = tid/2, keys 16*(tid%2) .. +16
-        const int hd = tid >> 1, hf = tid & 1;
-        const u32x4v r0 = *reinterpret_cast<const u32x4v*>(&vs[hd * 40 + 16 * hf]);
-        const u32x4v r1 = *reinterpret_cast<const u32x4v*>(&vs[hd * 40 + 16 * hf + 8]);
-        uint16_t* dst = a.vtr + ((size_t)g * kPfHd + hd) * a.seq_pad + t0 + 16 * hf;
-        *reinterpret_cast<u32x4v*>(dst) = r0;
-        *reinterpret_cast<u32x4v*>(dst + 8) = r1;
+    // keys 4q .. 4q+3 of hd at q * 1024 + hd * 8 bytes: 16 bytes = hd pair (2p, 2p+1) of quad q
+    uint16_t* vdst = a.vt + ((size_t)g * nkb + tile) * (kPfKeys * kPfHd);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int u = tid + 256 * i, q = u >> 6, hp = u & 63;
+        const u32x2v r0 = *reinterpret_cast<const u32x2v*>(&vs[(2 * hp) * 40 + 4 * q]);
+        const u32x2v r1 = *reinterpret_cast<const u32x2v*>(&vs[(2 * hp + 1) * 40 + 4 * q]);
+        *reinterpret_cast<u32x4v*>(vdst + q * 512 + hp * 8) = u32x4v{r0.x, r0.y, r1.x, r1.y};
     }
 }
 
@@ -233,8 +241,6 @@ __global__ __launch_bounds__(256) void prefill_prep_kv(PrefillArgs a) {
 // register file then holds 165 VGPRs per lane, enough without spills, and one
 // wave's softmax overlaps another's MFMAs.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_prefill_bf16(PrefillArgs a) {
-    __shared__ __align__(16) uint16_t kt[2][kPfKeys * kPfKPitch];
-    __shared__ __align__(16) uint16_t vt[2][kPfHd * kPfVPitch];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int h2 = lane >> 5, l32 = lane & 31;
     const int wph = 4 / a.heads_per_wg;  // waves per head
@@ -301,28 +307,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             }
     }
 
-    // ---- tile staging (plain copies of the pre-pass output)
-    const int krw = tid >> 3, kcol = 16 * (tid & 7);  // K tile: row, first fp16
-    const int vrw = tid >> 1, vcol = 16 * (tid & 1);  // V^T tile: hd row, first key
-    const uint16_t* kbase = a.kr + (size_t)kvh * a.seq_pad * kPfHd;
-    const uint16_t* vbase = a.vtr + ((size_t)kvh * kPfHd + vrw) * a.seq_pad + vcol;
-    auto load_tile = [&](TileRegs& r, int t0) {
-        const uint16_t* kp = kbase + (size_t)(t0 + krw) * kPfHd + kcol;
-        r.k0 = *reinterpret_cast<const u32x4v*>(kp);
-        r.k1 = *reinterpret_cast<const u32x4v*>(kp + 8);
-        r.v0 = *reinterpret_cast<const u32x4v*>(vbase + t0);
-        r.v1 = *reinterpret_cast<const u32x4v*>(vbase + t0 + 8);
+    // ---- tile staging: direct global -> LDS loads (global_load_lds_dwordx4)
+    // of the pre-pass tiles, three stages deep (two tiles in flight while one
+    // is used), no registers held.  The pre-pass lays each tile out as the
+    // LDS wants it -- K chunk c of key r at c * 512 + r * 16 bytes, V keys
+    // 4q .. 4q+3 of hd at q * 1024 + hd * 8 -- so a tile is eight plain 1 KB
+    // copies of each, the MFMA operand reads take consecutive 16 / 8 bytes
+    // per lane (no bank conflicts) and differ only by immediate offsets.  The
+    // stages are separate arrays and the loop is unrolled by three, so every
+    // LDS read names its stage and the compiler's memory model needs no wait
+    // on the loads still in flight into the others; the waits are explicit:
+    // before stage i is read, this thread's loads of tile i (all but the last
+    // five issued) have landed, and the barrier then covers the other threads'.
+    __shared__ __align__(16) uint16_t ks0[kPfKeys * kPfHd], ks1[kPfKeys * kPfHd], ks2[kPfKeys * kPfHd];
+    __shared__ __align__(16) uint16_t vs0[kPfHd * kPfKeys], vs1[kPfHd * kPfKeys], vs2[kPfHd * kPfKeys];
+    // the tile's K factor and V exponent, copied the same way (a 256-byte slot
+    // per wave and stage; lane l brings word l % 2)
+    __shared__ __align__(16) uint32_t fs0[4 * 64], fs1[4 * 64], fs2[4 * 64];
+    const int nkb = a.seq_pad / kPfKeys;
+    const int kvh_u = __builtin_amdgcn_readfirstlane(kvh);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t* kfv = a.kfv + (size_t)kvh_u * nkb * 2;
+    const char* kblk = reinterpret_cast<const char*>(a.kt + (size_t)kvh_u * nkb * (kPfKeys * kPfHd));
+    const char* vblk = reinterpret_cast<const char*>(a.vt + (size_t)kvh_u * nkb * (kPfKeys * kPfHd));
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    // five loads per thread and tile: 1 KB pieces 2 wave, 2 wave + 1 of K and V, the factor pair
+    auto issue_tile = [&](int it, uint16_t* ks, uint16_t* vs, uint32_t* fs) __attribute__((always_inline)) {
+        const size_t tb = (size_t)it * (kPfKeys * kPfHd * 2);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int m = 2 * wv + j;
+            __builtin_amdgcn_global_load_lds(kblk + tb + m * 1024 + lane * 16, (lds_ptr)(ks + m * 512), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vblk + tb + m * 1024 + lane * 16, (lds_ptr)(vs + m * 512), 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds(kfv + 2 * (size_t)it + (lane & 1), (lds_ptr)(fs + wv * 64), 4, 0, 0);
     };
-    auto store_tile = [&](const TileRegs& r, int buf) {
-        *reinterpret_cast<u32x4v*>(&kt[buf][krw * kPfKPitch + kcol]) = r.k0;
-        *reinterpret_cast<u32x4v*>(&kt[buf][krw * kPfKPitch + kcol + 8]) = r.k1;
-        // V^T rows are 72 bytes (8-byte aligned): four 8-byte stores
-        u32x2v* vd = reinterpret_cast<u32x2v*>(&vt[buf][vrw * kPfVPitch + vcol]);
-        vd[0] = u32x2v{r.v0.x, r.v0.y};
-        vd[1] = u32x2v{r.v0.z, r.v0.w};
-        vd[2] = u32x2v{r.v1.x, r.v1.y};
-        vd[3] = u32x2v{r.v1.z, r.v1.w};
-    };
+    // operand reads (bytes within a stage): K chunk 2s + h2 of key l32 at
+    // kx + 1024 s; V keys 16 s2 + 4 h2 (+ 8) of hd 32 t + l32 at vx + 4096 s2 + 256 t (+ 2048)
+    const int kx = h2 * 512 + l32 * 16;
+    const int vx = h2 * 1024 + l32 * 8;
+    const int fx = wv * 256;  // this wave's factor slot (bytes)
 
     // ---- online softmax state of this lane's query, O^T accumulators
     f32x16 o[4];
@@ -337,14 +361,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
     const int ntiles = (kend + kPfKeys - 1) / kPfKeys;
     // the largest V tile exponent among those tiles: the output's factor 2^vmax;
     // tile j's probabilities carry 2^(e_j - vmax) <= 1
-    const int nkb = a.seq_pad / kPfKeys;
-    const float* kfac = a.kfac + (size_t)kvh * nkb;
-    const int* vexp = a.vexp + (size_t)kvh * nkb;
     __shared__ int vred[4];
     int vmax;
     {
         int e = -1000;
-        for (int i = tid; i < ntiles; i += 256) e = max(e, vexp[i]);
+        for (int i = tid; i < ntiles; i += 256) e = max(e, (int)kfv[2 * i + 1]);
         for (int off = 32; off > 0; off >>= 1) e = max(e, __shfl_xor(e, off, 64));
         if (lane == 0) vred[wave] = e;
         __syncthreads();
@@ -352,24 +373,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
     }
     const int per_part = (ntiles + nparts - 1) / nparts;
     const int it0 = part * per_part, it1 = min(ntiles, it0 + per_part);
-    TileRegs tr;
-    load_tile(tr, it0 * kPfKeys);
-    store_tile(tr, 0);
-    __syncthreads();
-    for (int it = it0; it < it1; it++) {
-        const int buf = (it - it0) & 1;
+    if (it0 < it1) issue_tile(it0, ks0, vs0, fs0);
+    if (it0 + 1 < it1) issue_tile(it0 + 1, ks1, vs1, fs1);
+    auto tile_step = [&](int it, const uint16_t* ks, const uint16_t* vs, const uint32_t* fs, uint16_t* ks_n,
+                         uint16_t* vs_n, uint32_t* fs_n) __attribute__((always_inline)) {
+        // this thread's loads of tile it have landed (those of it + 1 may not have)
+        if (it + 1 < it1) __builtin_amdgcn_s_waitcnt(0x0070 | 5);  // vmcnt(5) lgkmcnt(0)
+        else __builtin_amdgcn_s_waitcnt(0x0070);                   // vmcnt(0) lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();  // ... and every thread's; stage (it + 2) % 3 is free
+        if (it + 2 < it1) issue_tile(it + 2, ks_n, vs_n, fs_n);
+        const uint2 fw = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(fs) + fx);
+        const float kf_cur = __uint_as_float(fw.x);
+        const int ve_cur = (int)fw.y;
         const int t0 = it * kPfKeys;
-        if (it + 1 < it1) load_tile(tr, t0 + kPfKeys);
         if (t0 <= qw + 31) {  // some key of the tile is visible to some query of this wave
-            const float sl2t = sl2 * kfac[it];  // the tile's K factor
-            const int vd = vexp[it] - vmax;     // its V factor relative to the output's
+            const float sl2t = sl2 * kf_cur;  // the tile's K factor
+            const int vd = ve_cur - vmax;     // its V factor relative to the output's
             // S^T = K . Q^T
             f32x16 sacc;
 #pragma unroll
             for (int i = 0; i < 16; i++) sacc[i] = 0.0f;
 #pragma unroll
             for (int s = 0; s < 8; s++) {
-                const f16x8 ka = *reinterpret_cast<const f16x8*>(&kt[buf][l32 * kPfKPitch + 16 * s + 8 * h2]);
+                const f16x8 ka = *reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(ks) + kx + 1024 * s);
                 sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qop[s], sacc, 0, 0, 0);
             }
             // element i: key t0 + (i/4)*8 + 4*h2 + i%4 of query myq; the causal
@@ -388,7 +414,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
                     mt = fmaxf(mt, sacc[i]);
                 }
             }
-            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            mt = halves_max(mt);
             const float m_new = fmaxf(m_run, mt * sl2t);
             // a query with no visible key yet (a later part of a split block):
             // exponentials against 0 keep its all -inf scores at 0 instead of NaN
@@ -396,15 +422,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             float ls = 0.0f;
             f16x8 pb[2];
             // V stored at a smaller scale than the output's: the probabilities
-            // enter the V sum times 2^vd (vf = 1 for vd = 0), the row sum without it
-            const float vf = ldexpf(1.0f, vd);
+            // enter the V sum times 2^vd, the row sum without it.  For vd >= -64
+            // the factor joins the exponent (2^(x + vd)) and the tile's sum is
+            // scaled back by 2^-vd (exact: probabilities small enough to lose
+            // bits there are below 2^-60 of the running sum, which holds a 1);
+            // beyond that the probabilities are multiplied by 2^vd one by one.
+            if (vd >= -64) {
+                const float c = (float)vd - m_exp;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_exp));
-                ls += pv;
-                pb[i >> 3][i & 7] = (_Float16)(pv * vf);
+                for (int i = 0; i < 16; i++) {
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, c));
+                    ls += pv;
+                    pb[i >> 3][i & 7] = (_Float16)pv;
+                }
+                ls = ldexpf(ls, -vd);
+            } else {
+                const float vf = ldexpf(1.0f, vd);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i], sl2t, -m_exp));
+                    ls += pv;
+                    pb[i >> 3][i & 7] = (_Float16)(pv * vf);
+                }
             }
-            ls += __shfl_xor(ls, 32, 64);
+            ls = halves_sum(ls);
             // rescale only when some query's running maximum moved (alpha = 1
             // exactly otherwise: the 64 multiplies would change nothing)
             if (__any(m_new != m_run)) {
@@ -422,9 +463,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
             for (int t = 0; t < 4; t++) {
 #pragma unroll
                 for (int s2 = 0; s2 < 2; s2++) {
-                    const uint16_t* vr = &vt[buf][(32 * t + l32) * kPfVPitch + 16 * s2 + 4 * h2];
-                    const u32x2v lo = *reinterpret_cast<const u32x2v*>(vr);
-                    const u32x2v hi = *reinterpret_cast<const u32x2v*>(vr + 8);
+                    const char* vb = reinterpret_cast<const char*>(vs) + vx + 4096 * s2 + 256 * t;
+                    const u32x2v lo = *reinterpret_cast<const u32x2v*>(vb);
+                    const u32x2v hi = *reinterpret_cast<const u32x2v*>(vb + 2048);
                     u32x4v w;
                     w.x = lo.x; w.y = lo.y; w.z = hi.x; w.w = hi.y;
                     const f16x8 va = __builtin_bit_cast(f16x8, w);
@@ -432,10 +473,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
                 }
             }
         }
-        // the other buffer's last readers finished before the previous barrier
-        if (it + 1 < it1) store_tile(tr, buf ^ 1);
-        __syncthreads();
+    };
+    for (int it = it0; it < it1; it += 3) {
+        tile_step(it, ks0, vs0, fs0, ks2, vs2, fs2);
+        if (it + 1 < it1) tile_step(it + 1, ks1, vs1, fs1, ks0, vs0, fs0);
+        if (it + 2 < it1) tile_step(it + 2, ks2, vs2, fs2, ks1, vs1, fs1);
     }
+
 
     if (nparts > 1) {  // a part of a split block: its partial result
         if (myq < a.seq) {
@@ -491,9 +535,9 @@ __global__ __launch_bounds__(256) void prefill_combine_parts(PrefillArgs a) {
     if (nparts <= 1) return;  // written whole by its workgroup
     const int kvh = head * a.kv_heads / a.n_head;
     const int ntiles = pf_tiles(a, qb);
-    const int* vexp = a.vexp + (size_t)kvh * (a.seq_pad / kPfKeys);
+    const uint32_t* kfv = a.kfv + (size_t)kvh * (a.seq_pad / kPfKeys) * 2;
     int vmax = -1000;
-    for (int i = lane; i < ntiles; i += 64) vmax = max(vmax, vexp[i]);
+    for (int i = lane; i < ntiles; i += 64) vmax = max(vmax, (int)kfv[2 * i + 1]);
     for (int off = 32; off > 0; off >>= 1) vmax = max(vmax, __shfl_xor(vmax, off, 64));
     const size_t slot0 = ((size_t)q * a.n_head + head) * kPfMaxParts;
     float M = -INFINITY;
@@ -544,10 +588,9 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     a.out = out;
     a.seq = seq;
     a.seq_pad = (seq + kPfKeys - 1) / kPfKeys * kPfKeys;
-    a.kr = static_cast<uint16_t*>(workspace);
-    a.vtr = a.kr + (size_t)kv_heads * a.seq_pad * kPfHd;
-    a.kfac = reinterpret_cast<float*>(a.vtr + (size_t)kv_heads * a.seq_pad * kPfHd);
-    a.vexp = reinterpret_cast<int*>(a.kfac + (size_t)kv_heads * (a.seq_pad / kPfKeys));
+    a.kt = static_cast<uint16_t*>(workspace);
+    a.vt = a.kt + (size_t)kv_heads * a.seq_pad * kPfHd;
+    a.kfv = reinterpret_cast<uint32_t*>(a.vt + (size_t)kv_heads * a.seq_pad * kPfHd);
     a.n_head = n_head;
     a.kv_heads = kv_heads;
     a.heads_per_wg = (n_head / kv_heads) % 2 == 0 ? 2 : 1;
