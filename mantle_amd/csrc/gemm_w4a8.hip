@@ -336,11 +336,12 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
 
 // Batched GEMV (n <= 8) in the pair form with the weights read straight into
 // registers: every wave owns its own rows, so staging them in LDS would buy no
-// reuse.  Lane (row l%16, k group kq = 2p + s) loads, for block pair j, the 8
-// bytes at 32j + 8kq of its row: words 2s and 2s+1 of block 2j+p, which are
-// its A operand for halves h = 0 and 1 (word 2s+h).  B for column c (vector
-// c%8, parity c/8) and half h is that word's activations (permuted dwords 2s+h
-// and 4+2s+h of block 2j+p) where p == c/8, else zero.  The 8 activation
+// reuse.  Lane (row l%16, k group kq) loads, for block quad Q, the whole block
+// 4Q + kq of its row (16 bytes); its word w is the lane's A operand of the
+// quad's MFMAs w (one per half).  B for column c (vector c%8, parity c/8) and
+// half h is that word's activations (permuted dwords w and 4+w of block
+// 4Q + kq) where kq == 2h + c/8, else zero: half h yields the block dots of
+// blocks 4Q + 2h (columns 0-7) and 4Q + 2h + 1 (columns 8-15), the pair 2Q + h.  The 8 activation
 // vectors and their block scales sit in LDS for the whole row; the weight block
 // scales of each group of 8 blocks are computed by the lanes that loaded the
 // row (blocks 2kq, 2kq+1) and pass through a wave-private LDS tile into the
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
     // last.  D divides NG, so group g of any tile uses slot g % D.
     const int ntiles = (rows + RT * 16 - 1) / (RT * 16);
     const int tstride = (int)gridDim.x * 4;
-    uint2 wbuf[D][RT][4];
+    uint4 wbuf[D][RT][2];
     uint32_t sbuf[D][RT];
     uint32_t hbuf[D][RT];
     auto issue = [&](int tile, int g, int slot) __attribute__((always_inline)) {
@@ -372,10 +373,10 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
         for (int rt = 0; rt < RT; rt++) {
             const int r0 = tile * RT * 16 + rt * 16 + l16;
             const int r = r0 < rows ? r0 : rows - 1;
-            const uint2* wp = reinterpret_cast<const uint2*>(a.w.nib + (size_t)r * BPR * 16) + kq;
+            const uint4* wp = reinterpret_cast<const uint4*>(a.w.nib + (size_t)r * BPR * 16) + kq;
             const uint8_t* sp = a.w.sub + (size_t)r * BPR + 2 * kq;
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) wbuf[slot][rt][jj] = wp[4 * (4 * g + jj)];
+            for (int qq = 0; qq < 2; qq++) wbuf[slot][rt][qq] = wp[4 * (2 * g + qq)];
             sbuf[slot][rt] = (uint32_t)sp[kGemmKC * g] | ((uint32_t)sp[kGemmKC * g + 1] << 8);
             hbuf[slot][rt] = a.w.sup[(size_t)r * NG + g];
         }
@@ -429,8 +430,8 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
     const bool odd_x = __syncthreads_or(odd);
 
     const int par = l16 >> 3, vec = l16 & 7;
-    const uint32_t bmask = (kq >> 1) == par ? ~0u : 0u;
-    const uint32_t* xrow = xq + vec * XPW + par * 8 + 2 * (kq & 1);
+    const uint64_t bmask0 = kq == par ? ~0ull : 0ull, bmask1 = kq == 2 + par ? ~0ull : 0ull;
+    const uint32_t* xrow = xq + vec * XPW + kq * 8;
     float* sww = swW + wave * RT * 128;
 
     for (; tile < ntiles; tile += tstride) {
@@ -460,22 +461,28 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            v4i32 d[4][RT];
+            v4i32 d[4][RT];  // pair jj = 2 qq + h
     #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const int j = 4 * g + jj;
-                long bv[2];
-    #pragma unroll
-                for (int h = 0; h < 2; h++)
-                    bv[h] = (long)((uint64_t)(xrow[16 * j + h] & bmask) | ((uint64_t)(xrow[16 * j + h + 4] & bmask) << 32));
+            for (int qq = 0; qq < 2; qq++) {
+                const int Q = 2 * g + qq;
     #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
-                    const uint2 w = wbuf[slot][rt][jj];
-                    const long a0 = (long)((uint64_t)((w.x << 4) & 0xF0F0F0F0u) | ((uint64_t)(w.x & 0xF0F0F0F0u) << 32));
-                    const long a1 = (long)((uint64_t)((w.y << 4) & 0xF0F0F0F0u) | ((uint64_t)(w.y & 0xF0F0F0F0u) << 32));
                     const v4i32 zero = {0, 0, 0, 0};
-                    d[jj][rt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bv[0], zero, 0, 0, 0);
-                    d[jj][rt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bv[1], d[jj][rt], 0, 0, 0);
+                    d[2 * qq][rt] = zero;
+                    d[2 * qq + 1][rt] = zero;
+                }
+    #pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const uint64_t xv = (uint64_t)xrow[32 * Q + w] | ((uint64_t)xrow[32 * Q + w + 4] << 32);
+                    const long b0 = (long)(xv & bmask0), b1 = (long)(xv & bmask1);
+    #pragma unroll
+                    for (int rt = 0; rt < RT; rt++) {
+                        const uint4 wq = wbuf[slot][rt][qq];
+                        const uint32_t ww = w == 0 ? wq.x : (w == 1 ? wq.y : (w == 2 ? wq.z : wq.w));
+                        const long aw = (long)((uint64_t)((ww << 4) & 0xF0F0F0F0u) | ((uint64_t)(ww & 0xF0F0F0F0u) << 32));
+                        d[2 * qq][rt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, b0, d[2 * qq][rt], 0, 0, 0);
+                        d[2 * qq + 1][rt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aw, b1, d[2 * qq + 1][rt], 0, 0, 0);
+                    }
                 }
             }
             auto terms = [&](auto skip_tag) __attribute__((always_inline)) {
@@ -527,7 +534,7 @@ static void launch_gemv8_rt(const GemmArgs& a, hipStream_t stream) {
     constexpr int BPR = NG * kGemmKC;
     const size_t smem = sizeof(uint32_t) * (8 * (BPR * 8 + 39) + BPR * 8 + 4 * RT * 128);
     const int ntiles = (a.w.rows + RT * 16 - 1) / (RT * 16);
-    constexpr int per_cu = 2;  // workgroups per CU; each stages the activations once
+    constexpr int per_cu = 3;  // workgroups per CU; each stages the activations once
     int cus = 256, dev = 0;
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const int want = (ntiles + 3) / 4;
