@@ -21,10 +21,13 @@
 // scaled by s_w and accumulated per lane; lanes 2v and 2v+1 add their hi and lo
 // sums at the end.
 //
-// Tiling: four waves of 2 x 16 rows = 128 rows per workgroup; chunks of 8
-// blocks of weights (coalesced 16-byte loads) and of the activations (fp32,
-// split while staging) go through LDS, the next chunk's loads in flight while
-// the current one is multiplied.
+// Tiling (TR rows per workgroup): chunks of 8 blocks of weights (coalesced
+// 16-byte loads) and of the activations (fp32, split while staging) go through
+// LDS, the next chunk's loads in flight while the current one is multiplied.
+// TR = 128: four waves of 2 x 16 rows, each over all 8 blocks of a chunk.
+// TR = 32 (matrices of few rows, where 128-row workgroups would leave most of
+// the chip idle): the four waves take the same 2 x 16 rows and blocks 2w, 2w+1
+// of every chunk, and their sums are added through LDS at the end.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -38,7 +41,6 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 static constexpr int kW32KC = 8;      // blocks per chunk
-static constexpr int kW32TR = 128;    // rows per workgroup
 static constexpr int kW32WP = 36;     // weight row pitch in LDS (words): 8 blocks x 16 bytes + pad
 static constexpr int kW32XP = 132;    // activation column pitch (words): 8 blocks x 32 f16 + pad
 
@@ -73,7 +75,11 @@ __device__ __forceinline__ half8_t w32_nibbles_f16(uint32_t w) {
     return r;
 }
 
+template <int TR>
 __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
+    constexpr int kW32TR = TR;
+    constexpr bool KS = TR == 32;  // waves split the blocks of a chunk
+    constexpr int NI = TR / 32;    // 16-byte weight loads per thread and chunk
     __shared__ __align__(16) uint32_t wn[kW32TR * kW32WP];
     __shared__ __align__(16) uint32_t xh[16 * kW32XP];
     __shared__ __align__(16) float swT[kW32KC * kW32TR];
@@ -81,7 +87,7 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kq = lane >> 4, l16 = lane & 15;
     const int rows = a.w.rows, bpr = a.bpr, spr = (bpr + 7) / 8, cols = bpr * 32;
-    const int row0 = (int)blockIdx.x * kW32TR, wr0 = wave * 32;
+    const int row0 = (int)blockIdx.x * kW32TR, wr0 = KS ? 0 : wave * 32;
 
     // the vectors' range factors: wave w takes vectors 2w, 2w+1
 #pragma unroll
@@ -100,13 +106,13 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
     const int sv = tid >> 5, sblk = (tid & 31) >> 2, sg = tid & 3;
     const float sfac = ldexpf(1.0f, -vexp[sv]);
 
-    uint32_t rw[4][4];
+    uint32_t rw[NI][4];
     float rx[8];
-    uint32_t rsub[4];
-    uint16_t rsup[4];
+    uint32_t rsub[NI];
+    uint16_t rsup[NI];
     auto load_chunk = [&](int b0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {  // 128 rows x 8 blocks of 16 bytes
+        for (int i = 0; i < NI; i++) {  // TR rows x 8 blocks of 16 bytes
             const int it = tid + 256 * i, r = it >> 3, part = it & 7;
             const int gr = row0 + r < rows ? row0 + r : rows - 1;
             const uint4 u = reinterpret_cast<const uint4*>(a.w.nib)[(size_t)gr * bpr + b0 + part];
@@ -118,7 +124,7 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
         rx[0] = x0.x; rx[1] = x0.y; rx[2] = x0.z; rx[3] = x0.w;
         rx[4] = x1.x; rx[5] = x1.y; rx[6] = x1.z; rx[7] = x1.w;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {  // 128 rows x 8 block scales
+        for (int i = 0; i < NI; i++) {  // TR rows x 8 block scales
             const int it = tid + 256 * i, r = it >> 3, blk = it & 7;
             const int gr = row0 + r < rows ? row0 + r : rows - 1;
             rsub[i] = a.w.sub[(size_t)gr * bpr + b0 + blk];
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
     };
     auto store_chunk = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NI; i++) {
             const int it = tid + 256 * i;
             *reinterpret_cast<uint4*>(wn + (it >> 3) * kW32WP + (it & 7) * 4) =
                 make_uint4(rw[i][0], rw[i][1], rw[i][2], rw[i][3]);
@@ -145,7 +151,7 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
         *reinterpret_cast<half8_t*>(xh + (2 * sv) * kW32XP + sblk * 16 + sg * 4) = hi;
         *reinterpret_cast<half8_t*>(xh + (2 * sv + 1) * kW32XP + sblk * 16 + sg * 4) = lo;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NI; i++) {
             const int it = tid + 256 * i;
             swT[(it & 7) * kW32TR + (it >> 3)] = k4_scale(rsup[i], (uint8_t)rsub[i]);
         }
@@ -164,7 +170,8 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
         __syncthreads();
         load_chunk((c + 1 < nch ? c + 1 : c) * kW32KC);  // in flight while this chunk is multiplied
 #pragma unroll
-        for (int b = 0; b < kW32KC; b++) {
+        for (int bb = 0; bb < (KS ? 2 : kW32KC); bb++) {
+            const int b = KS ? 2 * wave + bb : bb;
             const half8_t bx = *reinterpret_cast<const half8_t*>(xh + l16 * kW32XP + b * 16 + kq * 4);
 #pragma unroll
             for (int rt = 0; rt < 2; rt++) {
@@ -178,6 +185,23 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
                 acc[rt][3] = __builtin_fmaf(d[3], sw.w, acc[rt][3]);
             }
         }
+    }
+    if constexpr (KS) {  // waves 1-3 hand their sums to wave 0 (added in wave order)
+        float* red = reinterpret_cast<float*>(xh);  // the activation tile is no longer read (1536 of its 2112 words)
+        __syncthreads();
+        if (wave > 0)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) red[((wave - 1) * 8 + rt * 4 + i) * 64 + lane] = acc[rt][i];
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 1; w < 4; w++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[rt][i] += red[((w - 1) * 8 + rt * 4 + i) * 64 + lane];
     }
     // column l16 = 2v + part: the lo lane's sums join the hi lane's
     const int v = l16 >> 1;
@@ -205,7 +229,13 @@ hipError_t k4_gemv_w4a32_mfma_launch(const K4Mat& m, int cols, const float* x, f
     a.batch = batch;
     a.x = x;
     a.y = y;
-    hipLaunchKernelGGL(k4_gemv_w4a32_mfma, dim3((m.rows + kW32TR - 1) / kW32TR), dim3(256), 0, stream, a);
+    // 128-row workgroups where they give at least one per CU, else 32-row ones
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if ((m.rows + 127) / 128 >= cus)
+        hipLaunchKernelGGL(k4_gemv_w4a32_mfma<128>, dim3((m.rows + 127) / 128), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(k4_gemv_w4a32_mfma<32>, dim3((m.rows + 31) / 32), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
