@@ -106,9 +106,11 @@ struct PrefillArgs {
     // workgroup's chain of tiles is much longer than the average one.  A split
     // block leaves each part's unnormalised O^T, running max (log2 units) and
     // sum in opart [seq][n_head][kPfMaxParts][128] / mlpart [seq][n_head][kPfMaxParts][2];
-    // prefill_combine_parts joins them.
+    // prefill_combine_parts joins them, with the block's output factor
+    // exponent vmax (below) from vmx [query block][head group].
     int t_max;
     float *opart, *mlpart;
+    int* vmx;
 };
 
 static constexpr int kPfMaxParts = 4;
@@ -482,6 +484,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
 
 
     if (nparts > 1) {  // a part of a split block: its partial result
+        if (part == 0 && tid == 0) a.vmx[qb * groups + hg] = vmax;
         if (myq < a.seq) {
             const size_t slot = ((size_t)myq * a.n_head + head) * kPfMaxParts + part;
             float* orow = a.opart + slot * kPfHd;
@@ -533,12 +536,7 @@ __global__ __launch_bounds__(256) void prefill_combine_parts(PrefillArgs a) {
     const int qb = q / a.q_block;
     const int nparts = pf_parts(a, qb);
     if (nparts <= 1) return;  // written whole by its workgroup
-    const int kvh = head * a.kv_heads / a.n_head;
-    const int ntiles = pf_tiles(a, qb);
-    const uint32_t* kfv = a.kfv + (size_t)kvh * (a.seq_pad / kPfKeys) * 2;
-    int vmax = -1000;
-    for (int i = lane; i < ntiles; i += 64) vmax = max(vmax, (int)kfv[2 * i + 1]);
-    for (int off = 32; off > 0; off >>= 1) vmax = max(vmax, __shfl_xor(vmax, off, 64));
+    const int vmax = a.vmx[qb * (a.n_head / a.heads_per_wg) + head / a.heads_per_wg];
     const size_t slot0 = ((size_t)q * a.n_head + head) * kPfMaxParts;
     float M = -INFINITY;
     for (int p = 0; p < nparts; p++) M = fmaxf(M, a.mlpart[2 * (slot0 + p)]);
@@ -565,7 +563,9 @@ static size_t prefill_base_bytes(int seq, int kv_heads) {
 }
 
 size_t attention_prefill_workspace(int seq, int n_head, int kv_heads) {
-    return prefill_base_bytes(seq, kv_heads) + (size_t)seq * n_head * kPfMaxParts * (kPfHd + 2) * sizeof(float);
+    // + vmx: one int per (query block of >= 32 queries, head group <= heads)
+    return prefill_base_bytes(seq, kv_heads) + (size_t)seq * n_head * kPfMaxParts * (kPfHd + 2) * sizeof(float) +
+           ((size_t)seq + 31) / 32 * n_head * sizeof(int);
 }
 
 hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -612,6 +612,7 @@ hipError_t launch_attention_prefill_bf16(const uint16_t* q, const uint16_t* k, c
     a.t_max = fills ? 0x3FFFFFFF : (int)std::max<long long>(4, avg);
     a.opart = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_base_bytes(seq, kv_heads));
     a.mlpart = a.opart + (size_t)seq * n_head * kPfMaxParts * kPfHd;
+    a.vmx = reinterpret_cast<int*>(a.mlpart + (size_t)seq * n_head * kPfMaxParts * 2);
     long long grid = 0;
     bool split = false;
     for (int qb = 0; qb < a.n_qblocks; qb++) {
