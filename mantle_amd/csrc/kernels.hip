@@ -392,6 +392,9 @@ static hipError_t launch_gemv_epi(GemvParams& p, hipStream_t stream) {
 static hipError_t dispatch_lane_gemv(GemvParams& p, GemvEpi epi, hipStream_t stream, bool* used) {
     *used = false;
     if (lane_gemv_disabled() || p.cols != p.bpr * 32) return hipSuccess;
+    // 8-lane rows read their u6 bytes and f16 supers as u32 words
+    for (int i = 0; i < p.nmat; i++)
+        if (((uintptr_t)p.mats[i].sub | (uintptr_t)p.mats[i].sup) & 3) return hipSuccess;
     int pro = kProQx;
     if (!p.qx) {
         if (((uintptr_t)p.x | (uintptr_t)p.norm_w) & 15) return hipSuccess;

@@ -1,9 +1,9 @@
 """Per-kernel phase breakdown of one decode step (latency study).
 
     python -m mantle_amd.build --phase-trace     # once: libmantle_hip_trace.so
-    python -m mantle_amd.phase_trace [--steps N]
+    python -m mantle_amd.phase_trace [--steps N] [--model qwen3-0.6b|qwen3-4b] [--prompt P]
 
-Runs the Qwen3-0.6B-shape k4 decode on the phase-trace
+Runs the Qwen3-0.6B-shape k4 decode (or the 4B shape) on the phase-trace
 build of the library, whose kernels stamp workgroup 0's wall clock (100 MHz)
 at fixed points, and prints, per kernel of the decoder layer, the mean offset
 of each stamp from that workgroup's start and the start-to-start time to the
@@ -30,6 +30,9 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--model-dir", default=os.environ.get("MANTLE_BENCH_DIR", "/tmp/mantle_bench"))
+    ap.add_argument("--model", default="qwen3-0.6b", choices=("qwen3-0.6b", "qwen3-4b"))
+    ap.add_argument("--prompt", type=int, default=31, help="prompt tokens before the traced decode steps")
+    ap.add_argument("--raw", type=int, default=0, help="also print the first N stamped launches of the last step")
     args = ap.parse_args()
     trace = os.path.join(HERE, "libmantle_hip_trace.so")
     if not os.path.exists(trace):
@@ -40,14 +43,16 @@ def main() -> None:
     from . import mcf
     from .backend import new_backend
     os.makedirs(args.model_dir, exist_ok=True)
-    path = mcf.pack_cached(os.path.join(args.model_dir, "qwen3_0_6b_k4_seed0.mcf"), 0, mcf.QWEN3_0_6B)
-    rt = new_backend().load_model(path, max_context=512)
+    cfg, seed, name = ((mcf.QWEN3_0_6B, 0, "qwen3_0_6b_k4_seed0.mcf") if args.model == "qwen3-0.6b"
+                       else (mcf.QWEN3_4B, 4, "qwen3_4b_k4_seed4.mcf"))
+    path = mcf.pack_cached(os.path.join(args.model_dir, name), seed, cfg)
+    rt = new_backend().load_model(path, max_context=max(512, args.prompt + args.steps + 16))
     fn = _lib.lib().mantleHipDebugPhaseTrace
     fn.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_uint)]
     buf = np.zeros(8192 * 8, dtype=np.uint64)
     n = C.c_uint()
     try:
-        rt.prefill_tokens(mcf.uniform_tokens(31, mcf.QWEN3_0_6B["vocab"], 1))
+        rt.prefill_tokens(mcf.uniform_tokens(args.prompt, cfg["vocab"], 1))
         rt.synchronize()
         fn(buf.ctypes.data, 8192, C.byref(n))
         n0 = n.value
@@ -61,7 +66,12 @@ def main() -> None:
     t = buf[:n1 * 8].reshape(n1, 8).astype(np.int64)
     steps = min(5, args.steps)
     rows = t[n1 - steps * per:].reshape(steps, per, 8)
-    L = mcf.QWEN3_0_6B["n_layers"]
+    L = cfg["n_layers"]
+    if args.raw:
+        last = rows[-1]
+        for i in range(min(args.raw, per - 1)):
+            st = [f"{(last[i, c] - last[i, 0]) * 0.01:.2f}" if last[i, c] > 0 else "-" for c in (1, 2, 6, 3, 4, 5)]
+            print(f"launch {i}: start-to-next {(last[i + 1, 0] - last[i, 0]) * 0.01:.2f} us, stamps", " ".join(st))
     head = per - 6 * L - 1  # stamped launches before the first layer (embed)
     start = rows[:, :, 0]
     s2s = np.diff(start, axis=1) * 0.01  # us
