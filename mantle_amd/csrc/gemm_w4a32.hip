@@ -89,23 +89,8 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
     const int rows = a.w.rows, bpr = a.bpr, spr = (bpr + 7) / 8, cols = bpr * 32;
     const int row0 = (int)blockIdx.x * kW32TR, wr0 = KS ? 0 : wave * 32;
 
-    // the vectors' range factors: wave w takes vectors 2w, 2w+1
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int v = 2 * wave + j;
-        float m = 0.0f;
-        if (v < a.batch)
-            for (int i = lane * 4; i < cols; i += 256)
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(a.x[(size_t)v * cols + i]), fabsf(a.x[(size_t)v * cols + i + 1])),
-                                   fmaxf(fabsf(a.x[(size_t)v * cols + i + 2]), fabsf(a.x[(size_t)v * cols + i + 3]))));
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        if (lane == 0) vexp[v] = w32_range_exp(m);
-    }
-    __syncthreads();
     // this thread's activation group: vector tid/32, block (tid%32)/4 of the chunk, elements 8*(tid%4) .. +7
     const int sv = tid >> 5, sblk = (tid & 31) >> 2, sg = tid & 3;
-    const float sfac = ldexpf(1.0f, -vexp[sv]);
-
     uint32_t rw[NI][4];
     float rx[8];
     uint32_t rsub[NI];
@@ -131,6 +116,22 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
             rsup[i] = a.w.sup[(size_t)gr * spr + ((b0 + blk) >> 3)];
         }
     };
+    load_chunk(0);  // the first chunk's loads in flight while the range factors are found
+    // the vectors' range factors: wave w takes vectors 2w, 2w+1
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int v = 2 * wave + j;
+        float m = 0.0f;
+        if (v < a.batch)
+            for (int i = lane * 4; i < cols; i += 256) {  // cols: a multiple of 256
+                const float4 q = *reinterpret_cast<const float4*>(a.x + (size_t)v * cols + i);
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
+            }
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        if (lane == 0) vexp[v] = w32_range_exp(m);
+    }
+    __syncthreads();
+    const float sfac = ldexpf(1.0f, -vexp[sv]);
     auto store_chunk = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -163,7 +164,6 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_mfma(W32MfmaArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[rt][i] = 0.0f;
     const int nch = bpr / kW32KC;
-    load_chunk(0);
     for (int c = 0; c < nch; c++) {
         __syncthreads();  // the previous chunk's readers are done
         store_chunk();
