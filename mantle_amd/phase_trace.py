@@ -69,9 +69,10 @@ def main() -> None:
     L = cfg["n_layers"]
     if args.raw:
         last = rows[-1]
-        for i in list(range(min(args.raw, per - 1))) + list(range(max(args.raw, per - 4), per - 1)):
+        for i in list(range(min(args.raw, per - 1))) + list(range(max(args.raw, per - 4), per)):
             st = [f"{(last[i, c] - last[i, 0]) * 0.01:.2f}" if last[i, c] > 0 else "-" for c in (1, 2, 6, 3, 4, 5)]
-            print(f"launch {i}: start-to-next {(last[i + 1, 0] - last[i, 0]) * 0.01:.2f} us, stamps", " ".join(st))
+            nxt = f"{(last[i + 1, 0] - last[i, 0]) * 0.01:.2f} us" if i + 1 < per else "-"
+            print(f"launch {i}: start-to-next {nxt}, stamps", " ".join(st))
     head = per - 6 * L - 1  # stamped launches before the first layer (embed)
     start = rows[:, :, 0]
     s2s = np.diff(start, axis=1) * 0.01  # us
