@@ -69,17 +69,30 @@ __device__ __forceinline__ float dpp_from_upper8(float v) {  // lane i <- lane i
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true));
 }
 
-// k4_scale with the super-scale decoded by the hardware conversion: this file
-// is built with f16 denormals flushed, so a subnormal super becomes +-0 as
-// Mantle's decode makes it (NaN payloads may differ; NaN stays NaN).
-__device__ __forceinline__ float k4_scale_hw(uint16_t sup_bits, uint8_t sub) {
+__device__ __forceinline__ bool finite_f(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
+
+// The int8 MFMA sees each weight as 16q, so its block dot d is 16 * dot.  The
+// fast path takes d as is against s_w / 16: k4_scale16_hw is the block scale
+// f16(super) * u6/32 divided by 16 (u6 / 512: the product of the f16 super and
+// u6 stays exact in fp32 and is at least 2^-23, so no rounding either way).
+// The super decodes through the hardware conversion: this file is built with
+// f16 denormals flushed, so a subnormal super becomes +-0 as Mantle's decode
+// makes it (NaN payloads may differ; NaN stays NaN).  For an activation scale
+// s_x that is 0 or within [2^-100, 2^100], (s_w/16)*s_x is (s_w*s_x)/16 exactly
+// (no underflow or overflow), and float(d) * that equals float(dot) *
+// (s_w*s_x) (d = 16*dot is exact in fp32): the same bits as the CPU's term with
+// one instruction (the shift) fewer.  Other scales take the exact form
+// float(d >> 4) * ((16*(s_w/16)) * s_x) on the kernels' zero-test path.
+__device__ __forceinline__ float k4_scale16_hw(uint16_t sup_bits, uint8_t sub) {
     const float sup = __half2float(__ushort_as_half(sup_bits));
     const uint32_t u6 = sub & 0x3Fu;
     if (sup == 0.0f || u6 == 0) return 0.0f;
-    return sup * ((float)u6 * 0.03125f);
+    return sup * ((float)u6 * 0.001953125f);
 }
-
-__device__ __forceinline__ bool finite_f(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
+__device__ __forceinline__ bool fast_xscale(float sx) {
+    const float m = fabsf(sx);
+    return sx == 0.0f || (m >= 0x1p-100f && m <= 0x1p100f);
+}
 
 template <int WR, int WT, int NWR, int NWT, bool PAIR>
 __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
@@ -171,7 +184,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
         for (int i = 0; i < SW_ITEMS; i++) {
             const int it = tid + 256 * i;
             if (TR * kGemmKC % 256 == 0 || it < TR * kGemmKC) {
-                const float s = k4_scale_hw(rsup[i], (uint8_t)rsub[i]);
+                const float s = k4_scale16_hw(rsup[i], (uint8_t)rsub[i]);
                 swT[(it % kGemmKC) * TR + it / kGemmKC] = s;
                 odd |= !finite_f(s);
             }
@@ -181,7 +194,7 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
             const int it = tid + 256 * i;
             if (TT * kGemmKC % 256 == 0 || it < TT * kGemmKC) {
                 xsT[(it % kGemmKC) * TT + it / kGemmKC] = rxs[i];
-                odd |= !finite_f(rxs[i]);
+                odd |= !finite_f(rxs[i]) || !fast_xscale(rxs[i]);
             }
         }
         return odd;
@@ -250,8 +263,13 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
                             const float sx = xsT[b * TT + wt0 + tt * 16 + l16];
 #pragma unroll
                             for (int i = 0; i < 4; i++) {
-                                float term = (float)(d[g][rt][tt][i] >> 4) * (sw[i] * sx);
-                                if constexpr (SKIP) term = sw[i] != 0.0f && sx != 0.0f ? term : 0.0f;
+                                float term;
+                                if constexpr (SKIP) {
+                                    term = (float)(d[g][rt][tt][i] >> 4) * ((16.0f * sw[i]) * sx);
+                                    term = sw[i] != 0.0f && sx != 0.0f ? term : 0.0f;
+                                } else {
+                                    term = (float)d[g][rt][tt][i] * (sw[i] * sx);
+                                }
                                 acc[rt][tt][i] = acc[rt][tt][i] + term;
                             }
                         }
@@ -293,8 +311,13 @@ __global__ __launch_bounds__(256) void k4_gemm_w4a8_mfma(GemmArgs a) {
                     const float sw[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        float term = (float)(d[pr][rt][i] >> 4) * (sw[i] * sx);
-                        if constexpr (SKIP) term = sw[i] != 0.0f && sx != 0.0f ? term : 0.0f;
+                        float term;
+                        if constexpr (SKIP) {
+                            term = (float)(d[pr][rt][i] >> 4) * ((16.0f * sw[i]) * sx);
+                            term = sw[i] != 0.0f && sx != 0.0f ? term : 0.0f;
+                        } else {
+                            term = (float)d[pr][rt][i] * (sw[i] * sx);
+                        }
                         // block b's term, then block b+1's from the lane 8 columns up
                         const float up = dpp_from_upper8(term);
                         acc[rt][0][i] = acc[rt][0][i] + term;
@@ -424,7 +447,7 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
         const int i = tid + 256 * k;
         if (BPR * 8 % 256 == 0 || i < BPR * 8) {
             xsT[i] = sr[k];
-            odd |= !finite_f(sr[k]);
+            odd |= !finite_f(sr[k]) || !fast_xscale(sr[k]);
         }
     }
     const bool odd_x = __syncthreads_or(odd);
@@ -452,8 +475,8 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
             bool bad = false;
     #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
-                const float s0 = k4_scale_hw((uint16_t)hbuf[slot][rt], (uint8_t)sbuf[slot][rt]);
-                const float s1 = k4_scale_hw((uint16_t)hbuf[slot][rt], (uint8_t)(sbuf[slot][rt] >> 8));
+                const float s0 = k4_scale16_hw((uint16_t)hbuf[slot][rt], (uint8_t)sbuf[slot][rt]);
+                const float s1 = k4_scale16_hw((uint16_t)hbuf[slot][rt], (uint8_t)(sbuf[slot][rt] >> 8));
                 sww[rt * 128 + (2 * kq) * 16 + l16] = s0;
                 sww[rt * 128 + (2 * kq + 1) * 16 + l16] = s1;
                 bad |= !finite_f(s0) || !finite_f(s1);
@@ -496,8 +519,13 @@ __global__ __launch_bounds__(256) void k4_gemv8_w4a8_mfma(GemmArgs a) {
                         const float sw[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
     #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            float term = (float)(d[jj][rt][i] >> 4) * (sw[i] * sx);
-                            if constexpr (SKIP) term = sw[i] != 0.0f && sx != 0.0f ? term : 0.0f;
+                            float term;
+                            if constexpr (SKIP) {
+                                term = (float)(d[jj][rt][i] >> 4) * ((16.0f * sw[i]) * sx);
+                                term = sw[i] != 0.0f && sx != 0.0f ? term : 0.0f;
+                            } else {
+                                term = (float)d[jj][rt][i] * (sw[i] * sx);
+                            }
                             const float up = dpp_from_upper8(term);
                             acc[rt][i] = acc[rt][i] + term;
                             acc[rt][i] = acc[rt][i] + up;

@@ -99,3 +99,54 @@ def test_w4a8_matmul_nonfinite_scales(hip, oracle, n):
         np.testing.assert_array_equal(np.isnan(got[v]), np.isnan(want))
         ok = ~np.isnan(want)
         g.assert_bitexact(got[v][ok], want[ok], f"nonfinite v={v}")
+
+
+def _extreme_x(n, cols, seed):
+    """Activation rows whose block scales (max|x| / 127) fall below 2^-100 and
+    above 2^100 in some blocks, beside ordinary ones."""
+    x = np.random.default_rng(seed).standard_normal((n, cols)).astype(np.float32)
+    x[:, 32:64] *= np.float32(1e-33)    # scale ~1e-35: the matrix-core kernels' exact fallback
+    x[:, 96:128] *= np.float32(3e32)    # scale ~1e31
+    x[0, 160:192] *= np.float32(1e-38)  # subnormal activations
+    x[-1, 192:224] = np.float32(3e38)   # scale near the fp32 maximum
+    return x
+
+
+@pytest.mark.parametrize("n", [3, 24])
+def test_w4a8_matmul_extreme_activation_scales(hip, oracle, n):
+    """Activation block scales outside [2^-100, 2^100] send a chunk to the exact
+    form of the term (the fast form takes the block dot against s_w / 16):
+    still bit-identical to the CPU arithmetic, infinities and NaN included."""
+    rows, cols = 80, 512
+    from mantle_amd import mcf
+    payload = mcf.quantize_k4(_weights(rows, cols, 9))
+    x = _extreme_x(n, cols, 40 + n)
+    got, _ = _matmul(payload, rows, cols, x)
+    for v in range(n):
+        want = oracle.matvec_w4a8(payload, rows, cols, x[v])
+        np.testing.assert_array_equal(np.isnan(got[v]), np.isnan(want))
+        ok = ~np.isnan(want)
+        g.assert_bitexact(got[v][ok], want[ok], f"extreme scales v={v}")
+
+
+def test_w4a8_gemv8_extreme_activation_scales(hip, oracle):
+    """The same at batch 8 on a tall matrix (the matrix-core pair-form GEMV)."""
+    rows, cols, batch = 16384, 1024, 8
+    from mantle_amd import mcf
+    payload = mcf.quantize_k4(_weights(rows, cols, 10))
+    x = _extreme_x(batch, cols, 77)
+    keep, qn, qs, qsub = g.k4_dev(payload, rows, cols)
+    bpr = cols // 32
+    xd = g.dev(x)
+    y = g.empty(batch * rows)
+    qx = g.empty(batch * cols, torch.int8)
+    xs = g.empty(batch * bpr)
+    g.call("mantleHipQuantMatVecK4W4A8F32", qn, qs, qsub, g.ptr(xd), g.ptr(y), rows, bpr, cols, batch, g.ptr(qx),
+           g.ptr(xs), g.stream())
+    got = g.host(y).reshape(batch, rows)
+    oracle.set_threads(8)
+    for b in range(batch):
+        want = oracle.matvec_w4a8(payload, rows, cols, x[b])
+        np.testing.assert_array_equal(np.isnan(got[b]), np.isnan(want))
+        ok = ~np.isnan(want)
+        g.assert_bitexact(got[b][ok], want[ok], f"gemv8 extreme scales b={b}")
