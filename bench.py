@@ -522,7 +522,7 @@ def main():
         "ms_per_step": round(dt / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        # the CPU leg measured on this host (BASELINE.md publishes no number for this metric)
+        # the CPU leg measured on this host (no published number exists for this metric on this hardware)
         "vs_baseline": round(tps / cpu["value"], 2) if cpu else None,
         "dtype": "k4 weights x int8 activations, int32 block dots, fp32 accumulation",
         "data": "synthetic: random-init N(0,0.02) weights seed 0 packed to MCF k4, 31 uniform token ids seed 1",
