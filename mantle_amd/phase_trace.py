@@ -76,6 +76,9 @@ def main() -> None:
     head = per - 6 * L - 1  # stamped launches before the first layer (embed)
     start = rows[:, :, 0]
     s2s = np.diff(start, axis=1) * 0.01  # us
+    if args.raw and steps > 1:
+        cross = (rows[1:, 0, 0] - rows[:-1, per - 1, 0]) * 0.01
+        print(f"last launch of a step to the first of the next: {cross.mean():.2f} us")
     print(f"stamped launches per step: {per}; step start-to-start "
           f"{(start[:, -1] - start[:, 0]).mean() * 0.01:.1f} us over the last {steps} steps")
     print("| kernel | start-to-start us | " + " | ".join(f"stamp {k}" for k in (1, 2, 6, 3, 4, 5)) + " |")
