@@ -1349,7 +1349,9 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             dst[i] = *reinterpret_cast<const Raw*>(colbase + ((size_t)(ee >> 6) * a.vt_stride + t) * esz);
         }
     };
-    auto store = [&](const Raw (&src)[kPvItems], int slot) {
+    // f32 / f16: the loaders store the terms p_t * v_t (the chain wave's own
+    // multiply, done here off its critical path); q8_0 stores q_t and its scale
+    auto store = [&](const Raw (&src)[kPvItems], int slot, int c) {
 #pragma unroll
         for (int i = 0; i < kPvItems; i++) {
             const int e = lt + 192 * i;
@@ -1367,6 +1369,10 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             } else {
                 v = src[i];
             }
+            if constexpr (!Q8) {
+                const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + c * kPvChunk + 4 * (e & 63));
+                v.x = p4.x * v.x; v.y = p4.y * v.y; v.z = p4.z * v.z; v.w = p4.w * v.w;
+            }
             if (e < 32 * kPvChunk / 4)
                 *reinterpret_cast<f32x4*>(vr + (slot * 32 + (e >> 6)) * kPvPitch + 4 * (e & 63)) = v;
         }
@@ -1381,7 +1387,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
     }
     head_softmax<false>(sg, p, red, pos);
     if (wave != 0) {
-        store(la, 0);
+        store(la, 0, 0);
         store_scales(sa, 0);
         if (nch > 2) {
             issue(la, 2);
@@ -1401,9 +1407,11 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             float pg[32], vg[32], sgk[Q8 ? 32 : 1];
 #pragma unroll
             for (int i4 = 0; i4 < 8; i4++) {
-                const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + k0 + 4 * i4);
                 const f32x4 v4 = *reinterpret_cast<const f32x4*>(col + k0 + 4 * i4);
-                pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                if constexpr (Q8) {
+                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + k0 + 4 * i4);
+                    pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
+                }
                 vg[4 * i4] = v4.x; vg[4 * i4 + 1] = v4.y; vg[4 * i4 + 2] = v4.z; vg[4 * i4 + 3] = v4.w;
                 if constexpr (Q8) {
                     const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + k0 + 4 * i4);
@@ -1412,7 +1420,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             }
             auto term = [&](int k) {
                 if constexpr (Q8) return (pg[k] * vg[k]) * sgk[k];
-                else return pg[k] * vg[k];
+                else return vg[k];  // p_t * v_t, formed by the loaders
             };
             if (k0 + 32 <= n) {
 #pragma unroll
@@ -1431,7 +1439,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             sum_chunk(0, c);
         } else {
             if (c + 1 < nch) {
-                store(lb, 1);
+                store(lb, 1, c + 1);
                 store_scales(sb, 1);
             }
             if (c + 3 < nch) {
@@ -1445,7 +1453,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             sum_chunk(1, c + 1);
         } else {
             if (c + 2 < nch) {
-                store(la, 0);
+                store(la, 0, c + 2);
                 store_scales(sa, 0);
             }
             if (c + 4 < nch) {
