@@ -1173,7 +1173,7 @@ __device__ __forceinline__ void head_softmax(const float* sg, float* p, float* r
     for (int t = tid; t <= pos; t += kThreads) p[t] = fast_exp_scalar(p[t] - mx);
     if (PG) __threadfence_block();
     __syncthreads();
-    if (tid == 0) red[4] = ordered_sum(p, 1, pos + 1);
+    if (tid == 0) red[4] = ((uintptr_t)p & 15) ? ordered_sum(p, 1, pos + 1) : ordered_sum_contig(p, pos + 1);
     __syncthreads();
     const float sum = red[4];
     if (sum != 0.0f) {

@@ -84,6 +84,40 @@ __device__ __forceinline__ float ordered_sum(const float* t, int stride, int n) 
     return sum;
 }
 
+// ordered_sum over contiguous (16-byte aligned) values in batches of 64 (then
+// 16): one LDS / memory latency per 64 dependent adds instead of per 16.
+__device__ __forceinline__ float ordered_sum_contig(const float* t, int n) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    float sum = 0.0f;
+    int b = 0;
+    for (; b + 64 <= n; b += 64) {
+        f4 v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = *reinterpret_cast<const f4*>(t + b + 4 * k);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            sum += v[k].x;
+            sum += v[k].y;
+            sum += v[k].z;
+            sum += v[k].w;
+        }
+    }
+    for (; b + 16 <= n; b += 16) {
+        f4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = *reinterpret_cast<const f4*>(t + b + 4 * k);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            sum += v[k].x;
+            sum += v[k].y;
+            sum += v[k].z;
+            sum += v[k].w;
+        }
+    }
+    for (; b < n; b++) sum += t[b];
+    return sum;
+}
+
 // Dot exactly as dotAVX512 / dotSIMD / dotScalar (internal/backend/simd/ops_avx512.go:27-90,
 // ops_avx2.go:25-51, ops.go:49-55).  One thread computes the whole dot.
 // Compile-time length: every accumulator stays in a register.
