@@ -1403,10 +1403,12 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
         const float* cs = vsc + slot * kPvChunk;
         const int t0 = c * kPvChunk;
         const int n = min(kPvChunk, pos + 1 - t0);
-        for (int k0 = 0; k0 < n; k0 += 32) {
-            float pg[32], vg[32], sgk[Q8 ? 32 : 1];
+        // batches of KB keys: their reads issued together, one LDS latency per batch
+        constexpr int KB = Q8 ? 32 : 64;
+        for (int k0 = 0; k0 < n; k0 += KB) {
+            float pg[Q8 ? KB : 1], vg[KB], sgk[Q8 ? KB : 1];
 #pragma unroll
-            for (int i4 = 0; i4 < 8; i4++) {
+            for (int i4 = 0; i4 < KB / 4; i4++) {
                 const f32x4 v4 = *reinterpret_cast<const f32x4*>(col + k0 + 4 * i4);
                 if constexpr (Q8) {
                     const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + k0 + 4 * i4);
@@ -1422,12 +1424,12 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
                 if constexpr (Q8) return (pg[k] * vg[k]) * sgk[k];
                 else return vg[k];  // p_t * v_t, formed by the loaders
             };
-            if (k0 + 32 <= n) {
+            if (k0 + KB <= n) {
 #pragma unroll
-                for (int k = 0; k < 32; k++) acc = acc + term(k);
+                for (int k = 0; k < KB; k++) acc = acc + term(k);
             } else {
 #pragma unroll
-                for (int k = 0; k < 32; k++) {
+                for (int k = 0; k < KB; k++) {
                     const float nacc = acc + term(k);
                     acc = k0 + k < n ? nacc : acc;
                 }
