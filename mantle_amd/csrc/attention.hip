@@ -1349,8 +1349,9 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             dst[i] = *reinterpret_cast<const Raw*>(colbase + ((size_t)(ee >> 6) * a.vt_stride + t) * esz);
         }
     };
-    // f32 / f16: the loaders store the terms p_t * v_t (the chain wave's own
-    // multiply, done here off its critical path); q8_0 stores q_t and its scale
+    // the loaders store p_t * v_t (f32 / f16: the whole term; q8_0: p_t * q_t,
+    // which the chain wave multiplies by the key's scale) -- the chain wave's
+    // own first multiply, done here off its critical path
     auto store = [&](const Raw (&src)[kPvItems], int slot, int c) {
 #pragma unroll
         for (int i = 0; i < kPvItems; i++) {
@@ -1369,7 +1370,7 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
             } else {
                 v = src[i];
             }
-            if constexpr (!Q8) {
+            {
                 const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + c * kPvChunk + 4 * (e & 63));
                 v.x = p4.x * v.x; v.y = p4.y * v.y; v.z = p4.z * v.z; v.w = p4.w * v.w;
             }
@@ -1404,16 +1405,12 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
         const int t0 = c * kPvChunk;
         const int n = min(kPvChunk, pos + 1 - t0);
         // batches of KB keys: their reads issued together, one LDS latency per batch
-        constexpr int KB = Q8 ? 32 : 64;
+        constexpr int KB = 64;
         for (int k0 = 0; k0 < n; k0 += KB) {
-            float pg[Q8 ? KB : 1], vg[KB], sgk[Q8 ? KB : 1];
+            float vg[KB], sgk[Q8 ? KB : 1];
 #pragma unroll
             for (int i4 = 0; i4 < KB / 4; i4++) {
                 const f32x4 v4 = *reinterpret_cast<const f32x4*>(col + k0 + 4 * i4);
-                if constexpr (Q8) {
-                    const f32x4 p4 = *reinterpret_cast<const f32x4*>(p + t0 + k0 + 4 * i4);
-                    pg[4 * i4] = p4.x; pg[4 * i4 + 1] = p4.y; pg[4 * i4 + 2] = p4.z; pg[4 * i4 + 3] = p4.w;
-                }
                 vg[4 * i4] = v4.x; vg[4 * i4 + 1] = v4.y; vg[4 * i4 + 2] = v4.z; vg[4 * i4 + 3] = v4.w;
                 if constexpr (Q8) {
                     const f32x4 s4 = *reinterpret_cast<const f32x4*>(cs + k0 + 4 * i4);
@@ -1421,8 +1418,8 @@ __global__ __launch_bounds__(kThreads) void attention_pv_lds(AttnArgs a) {
                 }
             }
             auto term = [&](int k) {
-                if constexpr (Q8) return (pg[k] * vg[k]) * sgk[k];
-                else return vg[k];  // p_t * v_t, formed by the loaders
+                if constexpr (Q8) return vg[k] * sgk[k];  // (p_t * q_t, formed by the loaders) * s_t
+                else return vg[k];                         // p_t * v_t, formed by the loaders
             };
             if (k0 + KB <= n) {
 #pragma unroll
