@@ -1706,17 +1706,7 @@ __global__ __launch_bounds__(kThreads) void attention_softmax_rows(AttnArgs a, i
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane == 0) {
-            int t = 0;
-            for (; t + 16 <= len; t += 16) {
-                float v[16];
-#pragma unroll
-                for (int k = 0; k < 16; k++) v[k] = b[t + k];
-#pragma unroll
-                for (int k = 0; k < 16; k++) sum += v[k];
-            }
-            for (; t < len; t++) sum += b[t];
-        }
+        if (lane == 0) sum = ordered_sum_contig(b, len, sum);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

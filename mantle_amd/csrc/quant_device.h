@@ -85,10 +85,10 @@ __device__ __forceinline__ float ordered_sum(const float* t, int stride, int n) 
 }
 
 // ordered_sum over contiguous (16-byte aligned) values in batches of 64 (then
-// 16): one LDS / memory latency per 64 dependent adds instead of per 16.
-__device__ __forceinline__ float ordered_sum_contig(const float* t, int n) {
+// 16), continuing the running sum `sum`: one LDS / memory latency per 64
+// dependent adds instead of per 16.
+__device__ __forceinline__ float ordered_sum_contig(const float* t, int n, float sum = 0.0f) {
     typedef float f4 __attribute__((ext_vector_type(4)));
-    float sum = 0.0f;
     int b = 0;
     for (; b + 64 <= n; b += 64) {
         f4 v[16];
