@@ -25,8 +25,8 @@
 // path within the tolerance above, not bit for bit.
 //
 // Layout (queries are MFMA columns throughout):
-//  * S^T = K . Q^T per 32-key tile: A = K rows from LDS (RoPE applied while
-//    staging), B = this wave's 32 queries, RoPE'd once into registers.  Lane l
+//  * S^T = K . Q^T per 32-key tile: A = K rows from LDS (RoPE'd by the
+//    pre-pass), B = this wave's 32 queries, RoPE'd once into registers.  Lane l
 //    then holds query l % 32 and 16 of the tile's keys, so each query's max and
 //    sum are one lane's 16 values plus one exchange with lane l ^ 32.
 //  * O^T += V^T . P^T: B = P straight from the S^T registers (fp16), A = V^T
@@ -35,11 +35,10 @@
 //    column too, so the online-softmax rescale is one factor per lane.
 //  * A workgroup is four waves: two query heads of one KV group x 64 queries
 //    (or, without GQA, one head x 128 queries); K/V tiles are staged once for
-//    all four and double-buffered, the next tile's global loads in flight
-//    while the current one is used.
-//  * A pre-pass (prefill_prep_kv) writes K RoPE'd in fp16 [kv][seq][128] and
-//    V in fp16 transposed [kv][128][seq] into the caller's workspace once, so
-//    the attention workgroups (seq/64 of them per KV group) stage plain copies.
+//    all four by direct global-to-LDS copies, three stages deep.
+//  * A pre-pass (prefill_prep_kv) writes each 32-key tile of K (RoPE'd) and V
+//    in fp16 into the caller's workspace once, already in the LDS layout the
+//    operand reads want, so the attention workgroups stage plain 1 KB copies.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
