@@ -155,9 +155,8 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_rows(K4Mat m, int bpr, cons
     }
 }
 
-template <int NB>
-static hipError_t launch_rows(const K4Mat& m, int bpr, const float* x, float* y, hipStream_t stream) {
-    constexpr int R = NB >= 3 ? 2 : 1;  // wider batches: two rows per lane group share each x read
+template <int NB, int R>
+static hipError_t launch_rows_r(const K4Mat& m, int bpr, const float* x, float* y, hipStream_t stream) {
     auto kern = k4_gemv_w4a32_rows<NB, R>;
     const size_t smem = sizeof(float) * (size_t)NB * bpr * 32;
     static bool lds_ok = false;
@@ -174,6 +173,23 @@ static hipError_t launch_rows(const K4Mat& m, int bpr, const float* x, float* y,
     const int grid = units < 8 * cus ? units : 8 * cus;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, m, bpr, x, y, units);
     return hipGetLastError();
+}
+
+// Wider batches hold two rows per lane group so that each x word read from LDS
+// serves both.  So does batch 1-2 on matrices of more than eight workgroups
+// per CU (the logits: 151936x1024 at batch 1 27.1 -> 25.5 us); smaller ones
+// keep one row, which spreads their few rows over more waves (3072x1024 at
+// batch 1: 4.8 us with one row, 8.7 with two).
+template <int NB>
+static hipError_t launch_rows(const K4Mat& m, int bpr, const float* x, float* y, hipStream_t stream) {
+    if constexpr (NB >= 3) {
+        return launch_rows_r<NB, 2>(m, bpr, x, y, stream);
+    } else {
+        int cus = 256, dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if ((m.rows + kW32Rows - 1) / kW32Rows >= 8 * cus) return launch_rows_r<NB, 2>(m, bpr, x, y, stream);
+        return launch_rows_r<NB, 1>(m, bpr, x, y, stream);
+    }
 }
 
 // Whole rows of 32-weight blocks with x staged in at most 160 KiB of LDS;
