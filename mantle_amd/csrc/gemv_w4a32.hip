@@ -23,7 +23,7 @@
 namespace mantle {
 
 static constexpr int kW32Lanes = 8;               // lanes per row
-static constexpr int kW32Rows = 32;               // rows per unit: 4 waves x 8 rows
+static constexpr int kW32Rows = 32;               // rows per unit of four-wave workgroups: 4 waves x 8 rows
 static constexpr int kW32Group = 4;               // blocks per lane per load group
 
 // Byte C of w, sign-extended, as fp32 (SDWA byte select): one instruction.
@@ -41,30 +41,32 @@ __device__ __forceinline__ float sbyte_f32(uint32_t w) {
     return r;
 }
 
-// xs: LDS [NB][cols] fp32.  Unit u covers rows 32u .. 32u+31: eight lanes per
+// xs: LDS [NB][cols] fp32.  Workgroups of NW waves; unit u covers rows
+// 8NW*R*u onwards, 8NW*R of them: eight lanes per
 // row, lane j taking blocks j, j+8, ... so that a row's lanes read 128
 // contiguous bytes per load and the lanes of one block index share x words.
-template <int NB, int R>
+template <int NB, int R, int NW>
 __global__ __launch_bounds__(256) void k4_gemv_w4a32_rows(K4Mat m, int bpr, const float* __restrict__ x,
                                                           float* __restrict__ y, int units) {
     extern __shared__ __align__(16) float xs[];
     const int tid = threadIdx.x;
     const int cols = bpr * 32;
     // stage x once: NB * cols floats (cols is a multiple of 32)
-    for (int i = tid * 4; i < NB * cols; i += 256 * 4)
+    constexpr int RPU = 8 * NW;  // rows per lane-group slab: NW waves x 8 rows
+    for (int i = tid * 4; i < NB * cols; i += NW * 64 * 4)
         *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
     __syncthreads();
     const int spr = (bpr + 7) / 8;
     const int j = tid & (kW32Lanes - 1);
     for (int u = blockIdx.x; u < units; u += gridDim.x) {
         // R rows per lane group (rows r0, r0 + 32, ...): each x word read from LDS serves R rows
-        const int r0 = u * kW32Rows * R + tid / kW32Lanes;
+        const int r0 = u * RPU * R + tid / kW32Lanes;
         const uint4* nib[R];
         const uint8_t* sub[R];
         const uint16_t* sup[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int row = r0 + r * kW32Rows;
+            const int row = r0 + r * RPU;
             const int rc = row < m.rows ? row : m.rows - 1;  // rows past the end re-read the last (not stored)
             nib[r] = reinterpret_cast<const uint4*>(m.nib) + (size_t)rc * bpr;
             sub[r] = m.sub + (size_t)rc * bpr;
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_rows(K4Mat m, int bpr, cons
                 v += __shfl_xor(v, 4, 64);
                 acc[r][b] = v;
             }
-            const int row = r0 + r * kW32Rows;
+            const int row = r0 + r * RPU;
             if (j == 0 && row < m.rows) {
 #pragma unroll
                 for (int b = 0; b < NB; b++) y[(size_t)b * m.rows + row] = acc[r][b];
@@ -155,9 +157,9 @@ __global__ __launch_bounds__(256) void k4_gemv_w4a32_rows(K4Mat m, int bpr, cons
     }
 }
 
-template <int NB, int R>
+template <int NB, int R, int NW = 4>
 static hipError_t launch_rows_r(const K4Mat& m, int bpr, const float* x, float* y, hipStream_t stream) {
-    auto kern = k4_gemv_w4a32_rows<NB, R>;
+    auto kern = k4_gemv_w4a32_rows<NB, R, NW>;
     const size_t smem = sizeof(float) * (size_t)NB * bpr * 32;
     static bool lds_ok = false;
     if (smem > 64 * 1024 && !lds_ok) {
@@ -166,12 +168,13 @@ static hipError_t launch_rows_r(const K4Mat& m, int bpr, const float* x, float* 
             return hipErrorInvalidValue;
         lds_ok = true;
     }
-    const int units = (m.rows + kW32Rows * R - 1) / (kW32Rows * R);
+    const int units = (m.rows + 8 * NW * R - 1) / (8 * NW * R);
     int cus = 256, dev = 0;
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     // a few resident workgroups per CU, each staging x once for several units
-    const int grid = units < 8 * cus ? units : 8 * cus;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), smem, stream, m, bpr, x, y, units);
+    const int cap = 32 / NW * cus;
+    const int grid = units < cap ? units : cap;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), smem, stream, m, bpr, x, y, units);
     return hipGetLastError();
 }
 
@@ -188,6 +191,10 @@ static hipError_t launch_rows(const K4Mat& m, int bpr, const float* x, float* y,
         int cus = 256, dev = 0;
         if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if ((m.rows + kW32Rows - 1) / kW32Rows >= 8 * cus) return launch_rows_r<NB, 2>(m, bpr, x, y, stream);
+        // wide rows with fewer 32-row units than CUs (1024x3072): one-wave
+        // workgroups of 8 rows spread them over four times as many CUs
+        // (10.3 -> 9.3 us; the 1024-column shapes measured no faster)
+        if (bpr >= 64 && (m.rows + kW32Rows - 1) / kW32Rows < cus) return launch_rows_r<NB, 1, 1>(m, bpr, x, y, stream);
         return launch_rows_r<NB, 1>(m, bpr, x, y, stream);
     }
 }

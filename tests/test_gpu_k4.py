@@ -154,7 +154,7 @@ def test_w4a32_gemv_kat(hip):
     np.testing.assert_allclose(o.matvec_w4a32(payload, rows, cols, x), want, atol=1e-4, rtol=0)
 
 
-@pytest.mark.parametrize("rows,cols", [(3072, 1024), (1024, 3072), (2048, 1024), (151936, 1024), (70001, 1024)])
+@pytest.mark.parametrize("rows,cols", [(3072, 1024), (1024, 3072), (2048, 1024), (151936, 1024), (70001, 1024), (1001, 3072)])
 def test_w4a32_gemv_tolerance(hip, oracle, rows, cols):
     """W4A32 (fp32 activations): within max-abs 1e-3 / rel 1e-2 of the oracle."""
     from mantle_amd import mcf
