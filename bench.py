@@ -432,6 +432,8 @@ def main():
     ap.add_argument("--prompt-prefill-only", action="store_true",
                     help="only the batched prompt prefill of the config-1 model (for rocprofv3)")
     ap.add_argument("--gemv-batch", type=int, default=1, help="--gemv-only: the batch of the logits-shape GEMV")
+    ap.add_argument("--gemv-mode", default="w4a8", choices=["w4a8", "w4a32"],
+                    help="--gemv-only: int8 (CPU-parity) or fp32 activations")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the lm_head GEMV microbench and a copy calibration (for rocprofv3 --pmc runs)")
     ap.add_argument("--model", default="qwen3-0.6b", choices=["qwen3-0.6b", *LARGE_MODELS],
@@ -463,7 +465,7 @@ def main():
         return
 
     if args.gemv_only:
-        g = gemv_microbench([(151936, 1024)], [args.gemv_batch], iters=50, modes=("w4a8",))[0]
+        g = gemv_microbench([(151936, 1024)], [args.gemv_batch], iters=50, modes=(args.gemv_mode,))[0]
         copy_calibration()
         print(json.dumps({"gemv": g}), flush=True)
         return
